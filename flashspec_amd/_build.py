@@ -1,0 +1,86 @@
+"""Build libflashspec_hip.so in-tree with hipcc for gfx950.
+
+``python -m flashspec_amd._build [--resource-usage]`` compiles every ``csrc/*.hip``
+to an object under ``_build/`` (in parallel) and links the shared library next to
+this file, where ``flashspec_amd._lib`` loads it.  No torch headers are used.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG.parent / "_build"
+LIB_NAME = "libflashspec_hip.so"
+ARCH = os.environ.get("FLASHSPEC_OFFLOAD_ARCH", "gfx950")
+
+# Packed-FP32 instructions stay disabled (see csrc/fs_common.h users); the host pass
+# warns that it does not know the feature, which is harmless.
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-result",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; set HIPCC")
+
+
+def _compile(src: Path, extra: list[str]) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr[-8000:]}")
+    if proc.stderr.strip():
+        lines = [ln for ln in proc.stderr.splitlines() if "packed-fp32-ops" not in ln]
+        if any(ln.strip() for ln in lines):
+            sys.stderr.write("\n".join(lines) + "\n")
+    return obj
+
+
+def build(resource_usage: bool = False, jobs: int = 4) -> Path:
+    """Compile and link; returns the path of the shared library."""
+
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if resource_usage else []
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+        objs = list(pool.map(lambda s: _compile(s, extra), sources))
+    lib = PKG / LIB_NAME
+    tmp = PKG / (LIB_NAME + ".tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr[-8000:]}")
+    os.replace(tmp, lib)
+    return lib
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--resource-usage", action="store_true", help="print per-kernel VGPR/SGPR/LDS/occupancy")
+    ap.add_argument("-j", "--jobs", type=int, default=4)
+    args = ap.parse_args()
+    print(build(resource_usage=args.resource_usage, jobs=args.jobs))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,124 @@
+"""ctypes binding of libflashspec_hip.so (the C ABI declared in include/flashspec_hip.h).
+
+The library is loaded once at import.  ``available()`` says whether it loaded;
+``require()`` returns it or raises RuntimeError naming the load failure, so a
+GPU call never silently falls back to another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libflashspec_hip.so")
+
+FS_OK, FS_ERR_INVALID, FS_ERR_RUNTIME = 0, 1, 2
+DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+# (name, restype, argtypes) for every exported entry point.
+_SIGNATURES = {
+    "fs_last_error": (ctypes.c_char_p, []),
+    "fs_abi_version": (c_int, []),
+    "fs_decode_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "fs_fused_decode_i8": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_int64, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int,
+         c_void_p],
+    ),
+    "fs_paged_decode_i8": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
+         c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_int, c_int64, c_int, c_int, c_int,
+         c_float, c_int, c_int, c_int, c_void_p],
+    ),
+    "fs_combine_splits": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p]
+    ),
+    "fs_quantize_i8": (
+        c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]
+    ),
+    "fs_dequantize_i8": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p]
+    ),
+    "fs_quantize_pages_i8": (
+        c_int,
+        [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p],
+    ),
+    "fs_update_pages_i8": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+         c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p],
+    ),
+}
+
+_lib = None
+LOAD_ERROR: str | None = None
+
+
+def _load() -> None:
+    global _lib, LOAD_ERROR
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        LOAD_ERROR = None
+    except (OSError, AttributeError) as exc:  # missing/stale .so
+        _lib = None
+        LOAD_ERROR = f"{type(exc).__name__}: {exc}"
+
+
+_load()
+
+
+def available() -> bool:
+    return _lib is not None
+
+
+def require():
+    if _lib is None:
+        raise RuntimeError(
+            f"libflashspec_hip.so is not loaded ({LOAD_ERROR}); build it with "
+            "`python -m flashspec_amd._build` — GPU tensors have no other implementation"
+        )
+    return _lib
+
+
+def reload() -> bool:
+    """Re-open the library after an in-process build."""
+
+    _load()
+    return available()
+
+
+def check(rc: int) -> None:
+    """Map a C status to the reference's exception classes."""
+
+    if rc == FS_OK:
+        return
+    msg = _lib.fs_last_error().decode(errors="replace") if _lib is not None else "unknown error"
+    if rc == FS_ERR_INVALID:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float16, bfloat16 or float32") from None
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

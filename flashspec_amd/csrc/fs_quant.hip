@@ -1,0 +1,230 @@
+// Affine per-block INT8 quantization kernels for gfx950, bit-exact with the float32 op
+// sequence of reference src/flashspec/quant.py:141-158:
+//     scale = max((mx - mn) / 255, 1e-8)        (IEEE float32 division)
+//     zero  = clamp(rint(-mn / scale), 0, 255)
+//     q     = clamp(rint(x / scale + zero), 0, 255),  stored as q - 128
+// Contraction is disabled so `x / scale + zero` keeps its two roundings; division is the
+// correctly rounded HIP default.  One wavefront quantizes one [rows, head_dim] group.
+
+#include "fs_common.h"
+
+#pragma clang fp contract(off)
+
+namespace fs {
+
+template <typename Get>
+__device__ __forceinline__ void quantize_group(const Get& get, int rows, int D, int8_t* dst, float* scale_out,
+                                               int16_t* zero_out, int lane) {
+  const int n = rows * D;
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+  for (int r = 0; r < rows; ++r) {
+    for (int d = lane; d < D; d += kWave) {
+      const float x = get(r, d);
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
+    }
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
+  const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
+  for (int r = 0; r < rows; ++r) {
+    for (int d = lane; d < D; d += kWave) {
+      const float x = get(r, d);
+      const float qv = fminf(fmaxf(__builtin_rintf(x / scale + zero), 0.0f), 255.0f);
+      dst[(size_t)r * D + d] = (int8_t)((int)qv - 128);
+    }
+  }
+  (void)n;
+  if (lane == 0) {
+    *scale_out = scale;
+    *zero_out = (int16_t)zero;
+  }
+}
+
+// x [outer, S, D] -> values [outer, nb, bs, D]; group = (o, block); rows past S read as 0.
+template <typename XT>
+__global__ void __launch_bounds__(256)
+quantize_blocks_kernel(const XT* x, int64_t outer, int S, int D, int bs, int nb, int8_t* values, float* scale,
+                       int16_t* zero) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (grp >= outer * nb) return;
+  const int64_t o = grp / nb;
+  const int blk = (int)(grp - o * nb);
+  const XT* src = x + ((size_t)o * S) * D;
+  auto get = [&](int r, int d) -> float {
+    const int s = blk * bs + r;
+    return s < S ? to_f32(src[(size_t)s * D + d]) : 0.0f;
+  };
+  quantize_group(get, bs, D, values + (size_t)grp * bs * D, scale + grp, zero + grp, lane);
+}
+
+// dense [B, H, S, D] -> page store [P, H, page, D]; physical page j holds batch-major
+// logical page src[j] (identity when src is null); rows past S read as 0.
+template <typename XT>
+__global__ void __launch_bounds__(256)
+quantize_pages_kernel(const XT* x, int H, int S, int D, int page, int nbps, const int64_t* page_src, int64_t P,
+                      int8_t* values, float* scale, int16_t* zero) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (grp >= P * H) return;
+  const int64_t j = grp / H;
+  const int h = (int)(grp - j * H);
+  const int64_t o = page_src ? page_src[j] : j;
+  const int64_t b = o / nbps;
+  const int lb = (int)(o - b * nbps);
+  const XT* src = x + ((size_t)(b * H + h) * S) * D;
+  auto get = [&](int r, int d) -> float {
+    const int s = lb * page + r;
+    return s < S ? to_f32(src[(size_t)s * D + d]) : 0.0f;
+  };
+  quantize_group(get, page, D, values + (size_t)grp * page * D, scale + grp, zero + grp, lane);
+}
+
+// Rewrite listed pages (see fs_update_pages_i8).
+template <typename XT>
+__global__ void __launch_bounds__(256)
+update_pages_kernel(const int8_t* in_values, const float* in_scale, const int16_t* in_zero, int64_t in_pages,
+                    int in_qb, int8_t* out_values, float* out_scale, int16_t* out_zero, const int64_t* pages,
+                    const uint8_t* fresh, int64_t n_pages, const int32_t* row_src, const XT* src, int src_tokens,
+                    int H, int page, int D) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (grp >= n_pages * H) return;
+  const int64_t i = grp / H;
+  const int h = (int)(grp - i * H);
+  const int64_t pg = pages ? pages[i] : i;
+  const bool from_zero = pg >= in_pages || (fresh != nullptr && fresh[i] != 0);
+  const int nqb_in = page / in_qb;
+  const int32_t* rs = row_src + (size_t)i * page;
+  auto get = [&](int r, int d) -> float {
+    const int32_t si = rs[r];
+    if (si >= 0) {
+      const int n = si / src_tokens;
+      const int t = si - n * src_tokens;
+      return to_f32(src[(((size_t)n * H + h) * src_tokens + t) * D + d]);
+    }
+    if (from_zero) return 0.0f;
+    const int qb = r / in_qb;
+    const int qo = r - qb * in_qb;
+    const int64_t sidx = (pg * H + h) * nqb_in + qb;
+    const int u = (int)in_values[((size_t)sidx * in_qb + qo) * D + d] + 128;
+    return ((float)u - (float)in_zero[sidx]) * in_scale[sidx];
+  };
+  const int64_t og = pg * H + h;
+  quantize_group(get, page, D, out_values + (size_t)og * page * D, out_scale + og, out_zero + og, lane);
+}
+
+template <typename OT>
+__global__ void __launch_bounds__(256)
+dequantize_kernel(const int8_t* values, const float* scale, const int16_t* zero, int64_t outer, int nb, int bs,
+                  int D, int S, OT* out) {
+  const int64_t total = outer * (int64_t)S * D;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t od = e / D;
+    const int d = (int)(e - od * D);
+    const int64_t o = od / S;
+    const int s = (int)(od - o * S);
+    const int blk = s / bs;
+    const int64_t sidx = o * nb + blk;
+    const int u = (int)values[((size_t)o * nb * bs + s) * D + d] + 128;
+    out[e] = from_f32<OT>(((float)u - (float)zero[sidx]) * scale[sidx]);
+  }
+}
+
+static dim3 wave_grid(int64_t groups) { return dim3((unsigned)((groups + 3) / 4)); }
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" int fs_quantize_i8(const void* x, int x_dtype, int64_t outer, int seq_len, int head_dim, int block_size,
+                              int8_t* values, float* scale, int16_t* zero, void* stream) {
+  if (outer <= 0 || seq_len <= 0 || head_dim <= 0 || block_size <= 0)
+    return set_error(FS_ERR_INVALID, "quantize: sizes must be positive");
+  if (!x || !values || !scale || !zero) return set_error(FS_ERR_INVALID, "quantize: null pointer");
+  const int nb = (seq_len + block_size - 1) / block_size;
+  const int64_t groups = outer * nb;
+  if ((groups + 3) / 4 > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "quantize: too many groups");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+  switch (x_dtype) {
+    case FS_F32: hipLaunchKernelGGL(quantize_blocks_kernel<float>, grid, block, 0, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL(quantize_blocks_kernel<__half>, grid, block, 0, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL(quantize_blocks_kernel<__hip_bfloat16>, grid, block, 0, st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
+    default: return set_error(FS_ERR_INVALID, "quantize: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("quantize_int8_per_block");
+}
+
+extern "C" int fs_dequantize_i8(const int8_t* values, const float* scale, const int16_t* zero, int64_t outer,
+                                int n_blocks, int block_size, int head_dim, int seq_len, void* out, int out_dtype,
+                                void* stream) {
+  if (outer <= 0 || n_blocks <= 0 || block_size <= 0 || head_dim <= 0 || seq_len < 0 ||
+      (int64_t)n_blocks * block_size < seq_len)
+    return set_error(FS_ERR_INVALID, "dequantize: invalid sizes");
+  if (!values || !scale || !zero || !out) return set_error(FS_ERR_INVALID, "dequantize: null pointer");
+  const int64_t total = outer * (int64_t)seq_len * head_dim;
+  if (total == 0) return FS_OK;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks), block(256);
+  switch (out_dtype) {
+    case FS_F32: hipLaunchKernelGGL(dequantize_kernel<float>, grid, block, 0, st, values, scale, zero, outer, n_blocks, block_size, head_dim, seq_len, (float*)out); break;
+    case FS_F16: hipLaunchKernelGGL(dequantize_kernel<__half>, grid, block, 0, st, values, scale, zero, outer, n_blocks, block_size, head_dim, seq_len, (__half*)out); break;
+    case FS_BF16: hipLaunchKernelGGL(dequantize_kernel<__hip_bfloat16>, grid, block, 0, st, values, scale, zero, outer, n_blocks, block_size, head_dim, seq_len, (__hip_bfloat16*)out); break;
+    default: return set_error(FS_ERR_INVALID, "dequantize: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("dequantize_int8_per_block");
+}
+
+extern "C" int fs_quantize_pages_i8(const void* x, int x_dtype, int batch, int heads, int seq_len, int head_dim,
+                                    int page_size, const int64_t* page_src, int64_t num_pages, int8_t* values,
+                                    float* scale, int16_t* zero, void* stream) {
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0 || page_size <= 0)
+    return set_error(FS_ERR_INVALID, "quantize_pages: sizes must be positive");
+  if (!x || !values || !scale || !zero) return set_error(FS_ERR_INVALID, "quantize_pages: null pointer");
+  const int nbps = (seq_len + page_size - 1) / page_size;
+  if (num_pages != (int64_t)batch * nbps)
+    return set_error(FS_ERR_INVALID, "quantize_pages: num_pages must equal batch * ceil(seq_len / page)");
+  const int64_t groups = num_pages * heads;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+  switch (x_dtype) {
+    case FS_F32: hipLaunchKernelGGL(quantize_pages_kernel<float>, grid, block, 0, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL(quantize_pages_kernel<__half>, grid, block, 0, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL(quantize_pages_kernel<__hip_bfloat16>, grid, block, 0, st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;
+    default: return set_error(FS_ERR_INVALID, "quantize_pages: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("quantize_pages");
+}
+
+extern "C" int fs_update_pages_i8(const int8_t* in_values, const float* in_scale, const int16_t* in_zero,
+                                  int64_t in_pages, int in_quant_block, int8_t* out_values, float* out_scale,
+                                  int16_t* out_zero, const int64_t* pages, const uint8_t* fresh, int64_t n_pages,
+                                  const int32_t* row_src, const void* src, int src_dtype, int src_tokens, int heads,
+                                  int page_size, int head_dim, void* stream) {
+  if (n_pages <= 0) return FS_OK;
+  if (heads <= 0 || page_size <= 0 || head_dim <= 0 || src_tokens <= 0 || in_pages < 0)
+    return set_error(FS_ERR_INVALID, "update_pages: sizes must be positive");
+  if (in_quant_block <= 0 || page_size % in_quant_block != 0)
+    return set_error(FS_ERR_INVALID, "update_pages: page_size must be a multiple of the input quant block");
+  if (in_values == out_values && in_quant_block != page_size)
+    return set_error(FS_ERR_INVALID, "update_pages: in-place update needs quant block == page_size");
+  if (!out_values || !out_scale || !out_zero || !row_src || !src)
+    return set_error(FS_ERR_INVALID, "update_pages: null pointer");
+  if (in_pages > 0 && (!in_values || !in_scale || !in_zero)) return set_error(FS_ERR_INVALID, "update_pages: null input store");
+  const int64_t groups = n_pages * heads;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+  switch (src_dtype) {
+    case FS_F32: hipLaunchKernelGGL(update_pages_kernel<float>, grid, block, 0, st, in_values, in_scale, in_zero, in_pages, in_quant_block, out_values, out_scale, out_zero, pages, fresh, n_pages, row_src, (const float*)src, src_tokens, heads, page_size, head_dim); break;
+    case FS_F16: hipLaunchKernelGGL(update_pages_kernel<__half>, grid, block, 0, st, in_values, in_scale, in_zero, in_pages, in_quant_block, out_values, out_scale, out_zero, pages, fresh, n_pages, row_src, (const __half*)src, src_tokens, heads, page_size, head_dim); break;
+    case FS_BF16: hipLaunchKernelGGL(update_pages_kernel<__hip_bfloat16>, grid, block, 0, st, in_values, in_scale, in_zero, in_pages, in_quant_block, out_values, out_scale, out_zero, pages, fresh, n_pages, row_src, (const __hip_bfloat16*)src, src_tokens, heads, page_size, head_dim); break;
+    default: return set_error(FS_ERR_INVALID, "update_pages: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("update_pages");
+}

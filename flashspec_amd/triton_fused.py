@@ -1,0 +1,152 @@
+"""Kernel 1: contiguous INT8 KV decode attention on the HIP backend.
+
+Drop-in for reference src/flashspec/triton_fused.py: same public entry
+``fused_dequant_attention_triton(q, k_quant, v_quant, lengths=None,
+return_stats=False)``, same private knob names, same validation errors.  The
+launch goes to ``fs_fused_decode_i8`` (libflashspec_hip.so), which streams the
+int8 K/V once, dequantizes in registers and merges split-K partials with an
+fp32 log-sum-exp combine.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from . import _lib
+from .quant import QuantizedTensor, build_compression_stats, estimate_quantized_bytes
+from .triton_utils import (
+    arrival_counters,
+    device_cu_count,
+    dispatch_triton_or_fallback,
+    plan_splits,
+    resolve_block_n as _resolve_block_n,
+    resolve_num_warps as _resolve_num_warps,
+    split_merge_mode,
+    validate_decode_query,
+)
+
+__all__ = ["fused_dequant_attention_triton", "_compute_num_splits", "_resolve_block_n", "_resolve_num_warps"]
+
+_DEFAULT_NUM_SPLITS = 4
+_TOKENS_PER_SPLIT = 512
+_S_MAX = 32
+
+
+def _compute_num_splits(seq_len: int, block_n: int) -> int:
+    """The reference's split-count rule (triton_fused.py:560-601), kept for its callers.
+
+    ``FLASHSPEC_NUM_SPLITS`` wins (clamped to ``ceil(seq_len/block_n)``); otherwise
+    1 split up to 512 tokens, else ``min(4, ceil(seq_len/block_n))`` capped at 32.
+    The HIP launch sizes its splits for the GPU instead (``triton_utils.plan_splits``)
+    and honours the same environment override.
+    """
+
+    from .triton_utils import forced_num_splits
+
+    forced = forced_num_splits(seq_len, block_n)
+    if forced is not None:
+        return forced
+    max_splits = max(1, (seq_len + block_n - 1) // block_n)
+    if seq_len <= _TOKENS_PER_SPLIT:
+        return 1
+    return max(1, min(min(_DEFAULT_NUM_SPLITS, max_splits), _S_MAX))
+
+
+def _validate_triton_fused_inputs(q: torch.Tensor, k_quant: QuantizedTensor, v_quant: QuantizedTensor,
+                                  lengths: torch.Tensor | None) -> None:
+    """Reference checks (triton_fused.py:506-548) plus the layout facts the kernel relies on."""
+
+    validate_decode_query(q, kernel_name="fused")
+    if len(k_quant.original_shape) != 4 or len(v_quant.original_shape) != 4:
+        raise ValueError("k_quant and v_quant must come from [batch, heads, seq_len, head_dim] tensors")
+    if k_quant.original_shape != v_quant.original_shape:
+        raise ValueError("k_quant and v_quant original_shape must match")
+    if tuple(q.shape) != (k_quant.original_shape[0], k_quant.original_shape[1], k_quant.original_shape[3]):
+        raise ValueError("q batch, heads and head_dim must match the quantized K/V")
+    if k_quant.device != q.device or v_quant.device != q.device:
+        raise RuntimeError("q, k_quant and v_quant must be on the same GPU")
+    if lengths is not None:
+        if lengths.ndim != 1 or lengths.shape[0] != q.shape[0]:
+            raise ValueError("lengths must be [batch]")
+        if lengths.device != q.device:
+            raise RuntimeError("lengths must be on q's GPU")
+    if q.dtype not in _lib.DTYPE_CODE:
+        raise ValueError("q dtype must be float16, bfloat16 or float32")
+    batch, heads, seq_len, head_dim = k_quant.original_shape
+    for name, qt in (("k_quant", k_quant), ("v_quant", v_quant)):
+        if qt.values.dtype != torch.int8 or qt.scale.dtype != torch.float32 or qt.zero_point.dtype != torch.int16:
+            raise ValueError(f"{name} must hold int8 values, float32 scale and int16 zero_point")
+        n_blocks = (seq_len + qt.block_size - 1) // qt.block_size
+        if tuple(qt.values.shape) != (batch, heads, n_blocks, qt.block_size, head_dim):
+            raise ValueError(f"{name}.values must be [batch, heads, n_blocks, block_size, head_dim]")
+        if qt.scale.numel() != batch * heads * n_blocks or qt.zero_point.numel() != batch * heads * n_blocks:
+            raise ValueError(f"{name} scale/zero_point must have one entry per block")
+    if k_quant.block_size != v_quant.block_size:
+        raise ValueError("K/V quant block sizes must match")
+
+
+def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTensor, v_quant: QuantizedTensor,
+                                        lengths: torch.Tensor | None = None, return_stats: bool = False,
+                                        ) -> torch.Tensor | tuple[torch.Tensor, dict[str, float]]:
+    """Launch the HIP fused kernel (replaces triton_fused.py:604-761); no dense K/V is built."""
+
+    _validate_triton_fused_inputs(q, k_quant, v_quant, lengths)
+    lib = _lib.require()
+    dev = q.device
+    q_c = q.contiguous()
+    kv = [t.contiguous() for t in (k_quant.values, k_quant.scale, k_quant.zero_point,
+                                    v_quant.values, v_quant.scale, v_quant.zero_point)]
+    lengths_c = None if lengths is None else lengths.to(torch.int64).contiguous()
+    batch, heads, head_dim = (int(s) for s in q_c.shape)
+    seq_len = int(k_quant.original_shape[-2])
+    n_blocks = int(kv[0].shape[-3])
+    block_size = int(k_quant.block_size)
+    block_n = _resolve_block_n()
+    num_warps = _resolve_num_warps()
+    out = torch.empty_like(q_c)
+    sm_scale = 1.0 / math.sqrt(float(head_dim))
+    rows = batch * heads
+    split_tiles, max_splits = plan_splits(seq_len, rows, block_n, device_cu_count(dev))
+    stream = _lib.stream_ptr(dev)
+    workspace, ws_bytes, counters = None, 0, None
+    if max_splits > 1:
+        ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        if split_merge_mode() == "inline":
+            counters = arrival_counters(dev, stream, rows)
+    _lib.check(lib.fs_fused_decode_i8(
+        q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), _lib.ptr(lengths_c),
+        out.data_ptr(), _lib.ptr(workspace), ws_bytes, _lib.ptr(counters), batch, heads, head_dim, seq_len,
+        n_blocks, block_size, sm_scale, split_tiles, max_splits, num_warps, stream))
+    if max_splits > 1 and counters is None:
+        _lib.check(lib.fs_combine_splits(
+            workspace.data_ptr(), _lib.ptr(lengths_c), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,
+            head_dim, seq_len, split_tiles, max_splits, stream))
+    if not return_stats:
+        return out
+    dense_bytes = 2 * batch * heads * seq_len * head_dim * q_c.element_size()
+    quant_bytes = estimate_quantized_bytes(k_quant) + estimate_quantized_bytes(v_quant)
+    return out, build_compression_stats(
+        dense_bytes, quant_bytes, materializes_dense_kv=False,
+        num_splits=float(max_splits), block_n=float(block_n), num_warps=float(num_warps),
+        split_tiles=float(split_tiles),
+    )
+
+
+def fused_dequant_attention_triton(*_args: Any, **_kwargs: Any) -> Any:
+    """Kernel 1 entry: HIP kernel for GPU tensors, portable ``fused_dequant_attention`` otherwise.
+
+    Same signature as the reference (triton_fused.py:764-791):
+    ``(q, k_quant, v_quant, lengths=None, return_stats=False)``.
+    """
+
+    def _load_fallback():
+        from .attention import fused_dequant_attention
+
+        return fused_dequant_attention
+
+    return dispatch_triton_or_fallback(_args, _kwargs, run_triton=_run_fused_dequant_attention_triton,
+                                       load_fallback=_load_fallback)

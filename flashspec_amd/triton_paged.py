@@ -1,0 +1,136 @@
+"""Kernel 2: paged INT8 KV decode attention on the HIP backend.
+
+Drop-in for reference src/flashspec/triton_paged.py: same public entry
+``paged_quant_attention_triton(q, cache, return_stats=False)``, same knob names
+and validation errors.  The launch goes to ``fs_paged_decode_i8``: each wave
+resolves its block_table entries once per page into a base offset (instead of
+per-token-lane table loads), streams the int8 pages with coalesced 16-byte
+loads, and splits long rows across waves with an fp32 log-sum-exp merge.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from . import _lib
+from .paged import PagedKVCache
+from .quant import build_compression_stats
+from .triton_utils import (
+    arrival_counters,
+    device_cu_count,
+    dispatch_triton_or_fallback,
+    plan_splits,
+    resolve_block_n as _resolve_block_n,
+    resolve_num_warps as _resolve_num_warps,
+    split_merge_mode,
+    validate_decode_query,
+)
+
+__all__ = ["paged_quant_attention_triton", "_resolve_block_n", "_resolve_num_warps"]
+
+
+def _validate_triton_paged_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
+    """Reference checks (triton_paged.py:302-335) plus the layout facts the kernel relies on."""
+
+    validate_decode_query(q, kernel_name="paged")
+    if q.shape[0] != cache.batch_size or q.shape[1] != cache.num_heads or q.shape[2] != cache.head_dim:
+        raise ValueError("q batch, heads and head_dim must match the PagedKVCache")
+    if cache.k_quant.original_shape != cache.v_quant.original_shape:
+        raise ValueError("cache.k_quant and cache.v_quant original_shape must match")
+    if len(cache.k_quant.original_shape) != 4:
+        raise ValueError("PagedKVCache k_quant/v_quant must come from [physical, heads, block, head_dim] tensors")
+    if cache.k_quant.original_shape[2] != cache.block_size:
+        raise ValueError("the physical page's sequence dim must equal cache.block_size")
+    if cache.k_quant.block_size != cache.v_quant.block_size:
+        raise ValueError("K/V quant block_size must match")
+    if cache.block_size % cache.k_quant.block_size != 0:
+        raise ValueError("cache.block_size must be a multiple of the quant block_size")
+    if cache.k_quant.device != q.device or cache.v_quant.device != q.device:
+        raise RuntimeError("q and the cache's quantized K/V must be on the same GPU")
+    if cache.block_table.device != q.device or cache.lengths.device != q.device:
+        raise RuntimeError("block_table and lengths must be on q's GPU")
+    if q.dtype not in _lib.DTYPE_CODE:
+        raise ValueError("q dtype must be float16, bfloat16 or float32")
+    pages, heads, page, head_dim = cache.k_quant.original_shape
+    qb = cache.k_quant.block_size
+    for name, qt in (("k_quant", cache.k_quant), ("v_quant", cache.v_quant)):
+        if qt.values.dtype != torch.int8 or qt.scale.dtype != torch.float32 or qt.zero_point.dtype != torch.int16:
+            raise ValueError(f"cache.{name} must hold int8 values, float32 scale and int16 zero_point")
+        if tuple(qt.values.shape) != (pages, heads, page // qb, qb, head_dim):
+            raise ValueError(f"cache.{name}.values must be [pages, heads, page/quant_block, quant_block, head_dim]")
+        if qt.scale.numel() != pages * heads * (page // qb) or qt.zero_point.numel() != pages * heads * (page // qb):
+            raise ValueError(f"cache.{name} scale/zero_point must have one entry per quant block")
+    if cache.block_table.ndim != 2 or cache.block_table.dtype not in (torch.int32, torch.int64):
+        raise ValueError("block_table must be a 2-D int32/int64 tensor")
+    if cache.lengths.ndim != 1 or cache.lengths.shape[0] != cache.batch_size:
+        raise ValueError("lengths must be [batch]")
+
+
+def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, return_stats: bool = False,
+                                      ) -> torch.Tensor | tuple[torch.Tensor, dict[str, float]]:
+    """Launch the HIP paged kernel (replaces triton_paged.py:338-450); no dense K/V is built."""
+
+    _validate_triton_paged_inputs(q, cache)
+    lib = _lib.require()
+    dev = q.device
+    q_c = q.contiguous()
+    kq, vq = cache.k_quant, cache.v_quant
+    kv = [t.contiguous() for t in (kq.values, kq.scale, kq.zero_point, vq.values, vq.scale, vq.zero_point)]
+    table = cache.block_table.contiguous()
+    lengths = cache.lengths if cache.lengths.dtype == torch.int64 else cache.lengths.to(torch.int64)
+    lengths = lengths.contiguous()
+    batch, heads, head_dim = (int(s) for s in q_c.shape)
+    max_seq_len = int(cache.max_seq_len)
+    num_pages = int(kq.original_shape[0])
+    block_n = _resolve_block_n()
+    num_warps = _resolve_num_warps()
+    out = torch.empty_like(q_c)
+    sm_scale = 1.0 / math.sqrt(float(head_dim))
+    rows = batch * heads
+    split_tiles, max_splits = plan_splits(max_seq_len, rows, block_n, device_cu_count(dev))
+    stream = _lib.stream_ptr(dev)
+    workspace, ws_bytes, counters = None, 0, None
+    if max_splits > 1:
+        ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        if split_merge_mode() == "inline":
+            counters = arrival_counters(dev, stream, rows)
+    _lib.check(lib.fs_paged_decode_i8(
+        q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), table.data_ptr(),
+        table.element_size(), int(table.shape[1]), lengths.data_ptr(), out.data_ptr(), _lib.ptr(workspace),
+        ws_bytes, _lib.ptr(counters), batch, heads, head_dim, num_pages, int(cache.block_size),
+        int(kq.block_size), max_seq_len, sm_scale, split_tiles, max_splits, num_warps, stream))
+    if max_splits > 1 and counters is None:
+        _lib.check(lib.fs_combine_splits(
+            workspace.data_ptr(), lengths.data_ptr(), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,
+            head_dim, max_seq_len, split_tiles, max_splits, stream))
+    if not return_stats:
+        return out
+    dense_bytes = 2 * batch * heads * max_seq_len * head_dim * q_c.element_size()
+    return out, build_compression_stats(
+        dense_bytes, cache.estimated_bytes(), materializes_dense_kv=False,
+        physical_blocks=float(cache.block_table.ge(0).sum().item()),
+        block_n=float(block_n), num_warps=float(num_warps), num_splits=float(max_splits),
+        split_tiles=float(split_tiles),
+    )
+
+
+def paged_quant_attention_triton(*_args: Any, **_kwargs: Any) -> Any:
+    """Kernel 2 entry: HIP kernel for a GPU ``q`` with a ``PagedKVCache``, portable path otherwise.
+
+    Same signature as the reference (triton_paged.py:453-490): ``(q, cache, return_stats=False)``.
+    """
+
+    def _needs_paged_cache(args) -> bool:
+        return len(args) >= 2 and isinstance(args[1], PagedKVCache)
+
+    def _load_fallback():
+        from .attention import paged_quant_attention
+
+        return paged_quant_attention
+
+    return dispatch_triton_or_fallback(_args, _kwargs, run_triton=_run_paged_quant_attention_triton,
+                                       load_fallback=_load_fallback, extra_guard=_needs_paged_cache)

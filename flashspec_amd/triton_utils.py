@@ -1,0 +1,161 @@
+"""Backend gate, dispatch and launch knobs (reference src/flashspec/triton_utils.py).
+
+The reference gates its GPU path on ``HAS_TRITON``.  Here the accelerated
+backend is the HIP library, so ``HAS_TRITON`` (alias ``HAS_HIP``) means
+"libflashspec_hip.so is loaded".  Dispatch keeps the reference's contract —
+GPU path when the first positional argument is a GPU tensor, portable torch
+path otherwise — except that a GPU tensor with the library missing raises
+instead of silently running the portable path.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+from . import _lib
+
+HAS_HIP = _lib.available()
+HAS_TRITON = HAS_HIP  # name kept for callers of the reference (tests, microbench)
+
+TILE_TOKENS = 16  # tokens per decode tile / quant block on the fast path
+
+
+def next_power_of_2(x: int) -> int:
+    return 1 << (x - 1).bit_length()
+
+
+def validate_decode_query(q, *, kernel_name: str) -> None:
+    """Query checks shared by both kernels (triton_utils.py:33-45)."""
+
+    if q.ndim != 3:
+        raise ValueError("q must be [batch, heads, head_dim]")
+    if q.device.type != "cuda":
+        raise RuntimeError(f"HIP {kernel_name} attention needs a GPU q tensor")
+    if q.shape[-1] > 256:
+        raise ValueError(f"HIP {kernel_name} attention supports head_dim <= 256")
+
+
+def dispatch_triton_or_fallback(args, kwargs, *, run_triton, load_fallback, extra_guard=None):
+    """GPU path iff ``args[0]`` is a GPU tensor and ``extra_guard(args)`` holds (triton_utils.py:48-73).
+
+    A GPU call without the HIP library raises RuntimeError rather than falling back.
+    """
+
+    import torch
+
+    if args and isinstance(args[0], torch.Tensor) and args[0].device.type == "cuda" and (
+        extra_guard is None or extra_guard(args)
+    ):
+        _lib.require()
+        return run_triton(*args, **kwargs)
+    return load_fallback()(*args, **kwargs)
+
+
+_DEFAULT_BLOCK_N = 128
+
+
+def resolve_block_n() -> int:
+    """Tokens per tile knob, default 128, ``FLASHSPEC_BLOCK_N`` in {16,32,64,128} (triton_utils.py:81-98).
+
+    The HIP kernels always stream 16-token tiles; block_n is the granularity the
+    ``FLASHSPEC_NUM_SPLITS`` override is clamped with, as in the reference.
+    """
+
+    override = os.environ.get("FLASHSPEC_BLOCK_N")
+    if override is not None:
+        try:
+            v = int(override)
+        except ValueError:
+            v = 0
+        if v in (16, 32, 64, 128):
+            return v
+    return _DEFAULT_BLOCK_N
+
+
+def resolve_num_warps() -> int:
+    """Waves per workgroup, default 4, ``FLASHSPEC_NUM_WARPS`` in {1,2,4,8} (triton_utils.py:101-116)."""
+
+    override = os.environ.get("FLASHSPEC_NUM_WARPS")
+    if override is not None:
+        try:
+            v = int(override)
+        except ValueError:
+            v = 0
+        if v in (1, 2, 4, 8):
+            return v
+    return 4
+
+
+# ---- split-K planning for the HIP kernels ---------------------------------------------------
+# One wave streams one split.  The plan aims at WAVES_PER_CU resident waves per CU for
+# a uniform batch and bounds a split to [MIN, MAX] tiles so short rows are not
+# over-split and long rows of a ragged batch still spread over many waves.
+WAVES_PER_CU = 16
+MIN_SPLIT_TILES = 8
+MAX_SPLIT_TILES = 64
+
+_CU_CACHE: dict = {}
+
+
+def device_cu_count(device) -> int:
+    import torch
+
+    key = torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device()
+    if key not in _CU_CACHE:
+        _CU_CACHE[key] = int(torch.cuda.get_device_properties(key).multi_processor_count)
+    return _CU_CACHE[key]
+
+
+def forced_num_splits(seq_len: int, block_n: int) -> int | None:
+    """``FLASHSPEC_NUM_SPLITS`` clamped to [1, ceil(seq_len/block_n)] (triton_fused.py:586-595)."""
+
+    override = os.environ.get("FLASHSPEC_NUM_SPLITS")
+    if override is None:
+        return None
+    try:
+        forced = int(override)
+    except ValueError:
+        return None
+    if forced < 1:
+        return None
+    max_splits = max(1, (seq_len + block_n - 1) // block_n)
+    return max(1, min(forced, max_splits))
+
+
+def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int) -> tuple[int, int]:
+    """Return ``(split_tiles, max_splits)`` for a launch over ``rows`` rows of up to ``seq_len`` tokens."""
+
+    tiles = max(1, math.ceil(seq_len / TILE_TOKENS))
+    forced = forced_num_splits(seq_len, block_n)
+    if forced is not None:
+        split_tiles = math.ceil(tiles / forced)
+    else:
+        want = math.ceil(rows * tiles / max(1, cu_count * WAVES_PER_CU))
+        split_tiles = min(max(want, MIN_SPLIT_TILES), MAX_SPLIT_TILES)
+        split_tiles = min(split_tiles, tiles)
+    split_tiles = max(1, split_tiles)
+    return split_tiles, math.ceil(tiles / split_tiles)
+
+
+def split_merge_mode() -> str:
+    """``inline`` (last arriving wave merges; default) or ``launch`` (separate combine kernel)."""
+
+    mode = os.environ.get("FLASHSPEC_SPLIT_MERGE", "inline").strip().lower()
+    return mode if mode in ("inline", "launch") else "inline"
+
+
+_COUNTERS: dict = {}
+
+
+def arrival_counters(device, stream_ptr: int, rows: int):
+    """Zeroed per-row arrival counters, cached per (device, stream) and left zero by the kernels."""
+
+    import torch
+
+    key = (torch.device(device).index, stream_ptr)
+    buf = _COUNTERS.get(key)
+    if buf is None or buf.numel() < rows:
+        buf = torch.zeros(max(rows, 1024), dtype=torch.int32, device=device)
+        _COUNTERS[key] = buf
+    return buf

@@ -1,0 +1,167 @@
+/*
+ * flashspec_hip.h — C ABI of libflashspec_hip.so, the MI355X (gfx950) INT8
+ * decode-attention library.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed
+ * as `void*` (NULL = the null stream).  The library never allocates device
+ * memory: the caller owns every buffer, including the split-K workspace and
+ * the per-row arrival counters.  Work is enqueued asynchronously on `stream`.
+ *
+ * Return value: FS_OK (0) on success.  FS_ERR_INVALID means a shape/layout
+ * argument was rejected before launch (the reference raises ValueError);
+ * FS_ERR_RUNTIME means a HIP runtime failure (the reference raises
+ * RuntimeError).  fs_last_error() returns the calling thread's last message.
+ *
+ * dtype codes: FS_F32 = 0, FS_F16 = 1, FS_BF16 = 2.
+ */
+#ifndef FLASHSPEC_HIP_H_
+#define FLASHSPEC_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FS_OK 0
+#define FS_ERR_INVALID 1
+#define FS_ERR_RUNTIME 2
+
+#define FS_F32 0
+#define FS_F16 1
+#define FS_BF16 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fs_last_error(void);
+
+/* ABI revision of this header; bumped on any signature change. */
+int fs_abi_version(void);
+
+/*
+ * Bytes of split-K workspace fs_fused_decode_i8 / fs_paged_decode_i8 need for
+ * `rows` (= batch*heads) rows, `max_splits` splits per row and `head_dim`:
+ * rows*max_splits*(2 + head_dim) floats.
+ */
+int64_t fs_decode_workspace_bytes(int64_t rows, int64_t max_splits, int64_t head_dim);
+
+/*
+ * Contiguous INT8 decode attention (one query token per row), split-K with an
+ * fp32 log-sum-exp merge.
+ *
+ * Replaces the launches of _fused_dequant_attention_kernel,
+ * _fused_dequant_attention_split_kernel and _combine_splits_kernel in
+ * reference src/flashspec/triton_fused.py:697-744 (launcher
+ * _run_fused_dequant_attention_triton, triton_fused.py:604-761).
+ *
+ *   q        [batch, heads, head_dim]            q_dtype
+ *   k/v      values [batch, heads, n_blocks, block_size, head_dim] int8 (uint8 - 128)
+ *            scale  [batch, heads, n_blocks] fp32, zero [batch, heads, n_blocks] int16
+ *   lengths  [batch] int64 or NULL (NULL = every row uses seq_len)
+ *   out      [batch, heads, head_dim]            q_dtype
+ *   workspace  >= fs_decode_workspace_bytes(batch*heads, max_splits, head_dim)
+ *   counters   [batch*heads] uint32, all zero on entry; left zero on exit.
+ *              NULL selects the two-launch path (split kernel + combine kernel).
+ *   split_tiles  16-token tiles per split; max_splits = ceil(ceil(seq_len/16)/split_tiles)
+ *   waves_per_block  1, 2, 4 or 8 (the reference's num_warps knob)
+ */
+int fs_fused_decode_i8(const void* q, int q_dtype,
+                       const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                       const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                       const int64_t* lengths, void* out,
+                       void* workspace, int64_t workspace_bytes, uint32_t* counters,
+                       int batch, int heads, int head_dim, int seq_len,
+                       int n_blocks, int block_size, float sm_scale,
+                       int split_tiles, int max_splits, int waves_per_block, void* stream);
+
+/*
+ * Paged INT8 decode attention over a block_table, split-K, fp32 LSE merge.
+ *
+ * Replaces the launch of _paged_quant_attention_kernel in reference
+ * src/flashspec/triton_paged.py:428-434 (launcher
+ * _run_paged_quant_attention_triton, triton_paged.py:338-450).
+ *
+ *   k/v values [num_pages, heads, page_size/quant_block, quant_block, head_dim] int8
+ *       scale/zero [num_pages, heads, page_size/quant_block]
+ *   block_table [batch, table_cols], int32 (table_index_bytes = 4) or int64 (8);
+ *       entries < 0 or >= num_pages mark unallocated pages, whose tokens are masked.
+ *   lengths [batch] int64; a row attends to min(lengths[b], max_seq_len) tokens.
+ */
+int fs_paged_decode_i8(const void* q, int q_dtype,
+                       const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                       const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                       const void* block_table, int table_index_bytes, int64_t table_cols,
+                       const int64_t* lengths, void* out,
+                       void* workspace, int64_t workspace_bytes, uint32_t* counters,
+                       int batch, int heads, int head_dim, int64_t num_pages,
+                       int page_size, int quant_block, int max_seq_len, float sm_scale,
+                       int split_tiles, int max_splits, int waves_per_block, void* stream);
+
+/*
+ * Merge per-split partial states written by a decode call made with
+ * counters == NULL.  Replaces _combine_splits_kernel
+ * (reference src/flashspec/triton_fused.py:445-503).  `lengths` may be NULL;
+ * with it each row merges ceil(min(len,seq_len)/16/split_tiles) splits (>= 1).
+ */
+int fs_combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype,
+                      int batch, int heads, int head_dim, int seq_len,
+                      int split_tiles, int max_splits, void* stream);
+
+/*
+ * Affine per-block INT8 quantization, bit-exact with the float32 op sequence
+ * of reference src/flashspec/quant.py:94-165 (replaces its eager chain).
+ *   x [outer, seq_len, head_dim] x_dtype (contiguous)
+ *   values [outer, ceil(seq_len/block), block, head_dim] int8
+ *   scale/zero [outer, ceil(seq_len/block)] fp32 / int16
+ */
+int fs_quantize_i8(const void* x, int x_dtype, int64_t outer, int seq_len, int head_dim,
+                   int block_size, int8_t* values, float* scale, int16_t* zero, void* stream);
+
+/*
+ * Dequantize ((v + 128) - zero) * scale and crop the padding.  Replaces
+ * reference src/flashspec/quant.py:168-204.
+ *   out [outer, seq_len, head_dim] out_dtype
+ */
+int fs_dequantize_i8(const int8_t* values, const float* scale, const int16_t* zero,
+                     int64_t outer, int n_blocks, int block_size, int head_dim, int seq_len,
+                     void* out, int out_dtype, void* stream);
+
+/*
+ * Quantize dense K or V [batch, heads, seq_len, head_dim] straight into the
+ * physical page store [num_pages = batch*ceil(seq_len/page), heads, page, head_dim]
+ * (one quant block per page), gathering page j from batch-major logical page
+ * page_src[j] (NULL = identity).  Replaces the permute/pad/index/quantize chain
+ * of PagedKVCache.from_dense, reference src/flashspec/paged.py:343-412.
+ */
+int fs_quantize_pages_i8(const void* x, int x_dtype, int batch, int heads, int seq_len,
+                         int head_dim, int page_size, const int64_t* page_src, int64_t num_pages,
+                         int8_t* values, float* scale, int16_t* zero, void* stream);
+
+/*
+ * Rewrite whole pages: for each listed page, start from zeros (fresh[i] != 0)
+ * or from the dequantized old page (all rows, stale ones included), overwrite
+ * the rows that row_src names with new tokens, requantize the page per head
+ * (quant block = page_size) and store it.
+ *
+ * Replaces PagedKVCache.append's dequantize/write/requantize
+ * (reference src/flashspec/paged.py:498-550) and the allocator's per-page
+ * path (paged.py:92-136, 226-255).
+ *
+ *   in_*     old store [in_pages, heads, page/in_quant_block, in_quant_block, head_dim]
+ *   out_*    new store [*, heads, 1, page, head_dim]; may alias in_* (in place)
+ *   pages    [n_pages] int64 page ids to rewrite, or NULL = pages 0..n_pages-1
+ *   fresh    [n_pages] uint8 or NULL (= none fresh); pages >= in_pages are fresh
+ *   row_src  [n_pages, page] int32: -1 keeps the row, else n*src_tokens + t
+ *            selects token t of entry n of src [*, heads, src_tokens, head_dim]
+ */
+int fs_update_pages_i8(const int8_t* in_values, const float* in_scale, const int16_t* in_zero,
+                       int64_t in_pages, int in_quant_block,
+                       int8_t* out_values, float* out_scale, int16_t* out_zero,
+                       const int64_t* pages, const uint8_t* fresh, int64_t n_pages,
+                       const int32_t* row_src, const void* src, int src_dtype, int src_tokens,
+                       int heads, int page_size, int head_dim, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHSPEC_HIP_H_ */

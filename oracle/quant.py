@@ -1,0 +1,85 @@
+"""Oracle: affine per-block INT8 quantization (test infrastructure only).
+
+Restates reference src/flashspec/quant.py:94-204 in numpy float32.  Every torch
+op there is one IEEE-754 float32 operation, so the same op sequence in numpy
+float32 gives the same bits:
+
+* ``(mx - mn) / 255.0``       -> float32 subtraction, float32 true division
+* ``clamp_min(1e-8)``         -> max with float32(1e-8)
+* ``round(-mn / scale)``      -> float32 division, round-half-to-even
+* ``round(x / scale + zp)``   -> float32 division, float32 add, half-to-even
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Tuple
+
+import numpy as np
+
+F32 = np.float32
+SCALE_FLOOR = F32(1.0e-8)
+
+
+@dataclass(frozen=True)
+class OracleQuant:
+    """Mirror of ``QuantizedTensor`` (reference quant.py:9-41)."""
+
+    values: np.ndarray  # int8 [..., n_blocks, block_size, head_dim]
+    scale: np.ndarray  # float32 [..., n_blocks, 1, 1]
+    zero_point: np.ndarray  # int16 [..., n_blocks, 1, 1]
+    block_size: int
+    original_shape: Tuple[int, ...]
+
+
+def pad_sequence_dim(x: np.ndarray, block_size: int) -> np.ndarray:
+    """Zero-pad the sequence axis (-2) up to a multiple of block_size (quant.py:69-91)."""
+
+    pad = (-x.shape[-2]) % block_size
+    if pad == 0:
+        return x
+    widths = [(0, 0)] * x.ndim
+    widths[-2] = (0, pad)
+    return np.pad(x, widths)
+
+
+def quantize_int8_per_block(x: np.ndarray, block_size: int = 16) -> OracleQuant:
+    """Affine INT8 quantization per [block_size, head_dim] block (quant.py:94-165).
+
+    The zero padding of a ragged tail block takes part in min/max (quant.py:120).
+    """
+
+    if x.ndim < 2:
+        raise ValueError("x needs sequence and feature axes")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    if x.shape[-1] <= 0 or x.shape[-2] <= 0:
+        raise ValueError("sequence and feature axes must be non-empty")
+    original_shape = tuple(int(s) for s in x.shape)
+    xf = pad_sequence_dim(np.asarray(x).astype(F32), block_size)
+    lead = xf.shape[:-2]
+    n_blocks = xf.shape[-2] // block_size
+    blocked = xf.reshape(*lead, n_blocks, block_size, xf.shape[-1])
+    mn = blocked.min(axis=(-2, -1), keepdims=True)
+    mx = blocked.max(axis=(-2, -1), keepdims=True)
+    scale = np.maximum((mx - mn) / F32(255.0), SCALE_FLOOR).astype(F32)  # quant.py:146
+    zp = np.clip(np.rint(-mn / scale), F32(0), F32(255)).astype(F32)  # quant.py:150
+    qu = np.clip(np.rint(blocked / scale + zp), F32(0), F32(255))  # quant.py:154
+    values = (qu.astype(np.int16) - 128).astype(np.int8)  # quant.py:158
+    return OracleQuant(values, scale, zp.astype(np.int16), block_size, original_shape)
+
+
+def dequantize_int8_per_block(q: OracleQuant) -> np.ndarray:
+    """``(float(v + 128) - float(zp)) * scale``, then crop the padding (quant.py:168-204)."""
+
+    u = q.values.astype(np.int16) + 128
+    x = (u.astype(F32) - q.zero_point.astype(F32)) * q.scale.astype(F32)
+    lead = q.original_shape[:-2]
+    seq_len, head_dim = q.original_shape[-2], q.original_shape[-1]
+    return x.reshape(*lead, -1, head_dim)[..., :seq_len, :].astype(F32)
+
+
+def estimate_quantized_bytes(q: OracleQuant) -> int:
+    """values + 4 B per scale + 2 B per zero point (quant.py:232-247)."""
+
+    return int(q.values.size + q.scale.size * 4 + q.zero_point.size * 2)

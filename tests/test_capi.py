@@ -1,0 +1,63 @@
+"""The C-ABI library loads and exports every entry point include/flashspec_hip.h declares.
+
+CPU only: nothing here launches a kernel.  Argument validation happens before
+any HIP call, so rejected calls are safe without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from flashspec_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "flashspec_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fs_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads():
+    assert _lib.available(), _lib.LOAD_ERROR
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    names = declared_symbols()
+    assert "fs_paged_decode_i8" in names and "fs_fused_decode_i8" in names
+    for name in names:
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib._SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_abi_version_and_workspace_size():
+    lib = _lib.require()
+    assert lib.fs_abi_version() == 1
+    assert lib.fs_decode_workspace_bytes(256, 16, 128) == 256 * 16 * 130 * 4
+
+
+def test_invalid_arguments_are_rejected_before_launch():
+    lib = _lib.require()
+    # head_dim 0 -> FS_ERR_INVALID, message names the problem
+    rc = lib.fs_paged_decode_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, None, 0, None, 1, 1, 0, 4, 16, 16, 64,
+                                0.1, 4, 1, 4, None)
+    assert rc == _lib.FS_ERR_INVALID
+    assert "head_dim" in lib.fs_last_error().decode()
+    with pytest.raises(ValueError):
+        _lib.check(rc)
+    # splits that do not cover the sequence
+    rc = lib.fs_fused_decode_i8(1, 1, 1, 1, 1, 1, 1, 1, None, 1, None, 0, None, 1, 1, 128, 4096, 256, 16, 0.1,
+                                4, 4, 4, None)
+    assert rc == _lib.FS_ERR_INVALID and "cover" in lib.fs_last_error().decode()
+    # unsupported dtype code in quantize
+    rc = lib.fs_quantize_i8(1, 9, 1, 16, 128, 16, 1, 1, 1, None)
+    assert rc == _lib.FS_ERR_INVALID
+    # in-place page update with a different quant block
+    rc = lib.fs_update_pages_i8(1, 1, 1, 4, 8, 1, 1, 1, None, None, 4, 1, 1, 0, 1, 2, 16, 64, None)
+    assert rc == _lib.FS_ERR_INVALID and "in-place" in lib.fs_last_error().decode()

@@ -1,0 +1,412 @@
+"""GPU parity: the HIP kernels (through the public API and the C ABI) against the CPU oracle.
+
+Integer/byte outputs (quantized values, scales, zero points, tables) must be
+bit-exact; attention outputs must be within max-abs 2e-3 / max-rel 1e-2 (fp16).
+Inputs are drawn on the CPU from seeded generators so they are device-independent.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import flashspec_amd as fa
+from flashspec_amd import _lib, triton_utils
+from oracle import attention as oa
+from oracle import paged as op
+from oracle import quant as oq
+from tests._helpers import (
+    assert_attention_close,
+    assert_quant_equal,
+    from_cache,
+    from_qt,
+    golden_cache,
+    golden_quant,
+    load_npz,
+    np_of,
+    oracle_fused_attention,
+    oracle_paged_attention,
+    randn,
+    to_cache,
+    to_qt,
+)
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+
+
+def announce(msg: str) -> None:
+    print(f"[gpu case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(autouse=True)
+def _require_gpu(monkeypatch):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    assert _lib.available(), _lib.LOAD_ERROR
+    for key in ("FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_WARPS", "FLASHSPEC_SPLIT_MERGE"):
+        monkeypatch.delenv(key, raising=False)
+
+
+def sync():
+    torch.cuda.synchronize(DEV)
+
+
+# ---- quantize / dequantize -------------------------------------------------------------------
+
+def test_quantize_matches_reference_golden_vectors_bit_exact():
+    d = load_npz("quant_golden.npz")
+    for name in d["names"]:
+        x = torch.from_numpy(d[f"{name}_x"]).to(DEV)
+        bs = int(d[f"{name}_block"])
+        announce(f"quantize golden {name} shape={tuple(x.shape)} bs={bs}")
+        q = fa.quantize_int8_per_block(x, block_size=bs)
+        sync()
+        assert q.original_shape == tuple(x.shape)
+        assert_quant_equal(from_qt(q), golden_quant(d, name), name)
+        deq = fa.dequantize_int8_per_block(q)
+        assert np.array_equal(np_of(deq).view(np.uint32), d[f"{name}_deq"].view(np.uint32)), name
+
+
+@pytest.mark.parametrize("shape,bs,dtype", [
+    ((2, 3, 19, 16), 8, torch.float32),
+    ((8, 32, 300, 128), 16, torch.float16),
+    ((2, 4, 50, 64), 16, torch.bfloat16),
+    ((3, 1, 16, 256), 32, torch.float16),
+    ((5, 7, 24), 4, torch.float32),
+])
+def test_quantize_bit_exact_against_oracle(shape, bs, dtype):
+    announce(f"quantize shape={shape} bs={bs} dtype={dtype}")
+    x = randn(shape, seed=sum(shape), dtype=dtype) * 3.0
+    q = fa.quantize_int8_per_block(x.to(DEV), block_size=bs)
+    ref = oq.quantize_int8_per_block(np_of(x.to(torch.float32)), bs)
+    sync()
+    assert_quant_equal(from_qt(q), ref, str(shape))
+    out = fa.dequantize_int8_per_block(q)
+    assert np.array_equal(np_of(out).view(np.uint32), oq.dequantize_int8_per_block(ref).view(np.uint32))
+    half = fa.dequantize_int8_per_block(q, dtype=torch.float16)
+    assert half.dtype == torch.float16
+    assert torch.equal(half.cpu(), torch.from_numpy(oq.dequantize_int8_per_block(ref)).to(torch.float16))
+
+
+# ---- paged cache construction, append, allocator ----------------------------------------------
+
+@pytest.mark.parametrize("layout", ["contiguous", "shuffled", "interleaved"])
+def test_from_dense_pages_bit_exact(layout):
+    announce(f"from_dense layout={layout}")
+    k = randn((3, 4, 70, 64), 1)
+    v = randn((3, 4, 70, 64), 2)
+    lengths = torch.tensor([70, 33, 1])
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=16, lengths=lengths.to(DEV),
+                                       block_table_pattern=layout, layout_seed=3)
+    sync()
+    table = np_of(cache.block_table)
+    perm = None
+    if layout != "contiguous":
+        perm = np.empty(table.size, dtype=np.int64)
+        perm[table.ravel()] = np.arange(table.size)
+    ref = op.from_dense(np_of(k.float()), np_of(v.float()), 16, lengths=np_of(lengths), perm=perm)
+    assert np.array_equal(table, ref.block_table)
+    assert_quant_equal(from_qt(cache.k_quant), ref.k_quant, "k")
+    assert_quant_equal(from_qt(cache.v_quant), ref.v_quant, "v")
+    kd, vd = cache.to_dense()
+    rk, rv = op.to_dense(ref)
+    assert np.array_equal(np_of(kd), rk) and np.array_equal(np_of(vd), rv)
+
+
+def test_append_matches_reference_golden_vectors_bit_exact():
+    d = load_npz("append_golden.npz")
+    for name in d["names"]:
+        announce(f"append golden {name}")
+        cin = to_cache(golden_cache(d, f"{name}_in"), DEV)
+        ref = golden_cache(d, f"{name}_out")
+        out = cin.append(torch.from_numpy(d[f"{name}_kn"]).to(DEV), torch.from_numpy(d[f"{name}_vn"]).to(DEV))
+        sync()
+        assert np.array_equal(np_of(out.block_table), ref.block_table), name
+        assert np.array_equal(np_of(out.lengths), ref.lengths), name
+        assert out.max_seq_len == ref.max_seq_len
+        assert_quant_equal(from_qt(out.k_quant), ref.k_quant, f"{name}/k")
+        assert_quant_equal(from_qt(out.v_quant), ref.v_quant, f"{name}/v")
+
+
+def test_append_fp16_tokens_bit_exact_against_oracle():
+    announce("append fp16 B4 H8 D128 page16 T=21")
+    k, v = randn((4, 8, 40, 128), 5), randn((4, 8, 40, 128), 6)
+    kn, vn = randn((4, 8, 21, 128), 7), randn((4, 8, 21, 128), 8)
+    lengths = torch.tensor([40, 17, 16, 0])
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), 16, lengths=lengths.to(DEV),
+                                       block_table_pattern="shuffled", layout_seed=1)
+    out = cache.append(kn.to(DEV), vn.to(DEV))
+    sync()
+    ref = op.append(from_cache(cache), np_of(kn.float()), np_of(vn.float()))
+    assert np.array_equal(np_of(out.block_table), ref.block_table)
+    assert_quant_equal(from_qt(out.k_quant), ref.k_quant, "k")
+    assert_quant_equal(from_qt(out.v_quant), ref.v_quant, "v")
+    q = randn((4, 8, 128), 9)
+    announce("append fp16 -> paged attention")
+    got = fa.paged_quant_attention_triton(q.to(DEV), out)
+    assert_attention_close(got, oa.paged_quant_attention(np_of(q), ref), torch.float16, "after append")
+
+
+def test_allocator_lifecycle_matches_reference_golden_vectors_bit_exact():
+    d = load_npz("allocator_golden.npz")
+    H, D, bs, cap = (int(x) for x in d["config"])
+    alloc = fa.PagedKVAllocator(capacity_blocks=cap, heads=H, head_dim=D, block_size=bs, device=DEV)
+    for step, (code, rid, n) in enumerate(d["script"]):
+        announce(f"allocator golden step {step} op={code} rid={rid} n={n}")
+        if code == 0:
+            alloc.add_request(int(rid), torch.from_numpy(d[f"s{step}_k"]).to(DEV),
+                              torch.from_numpy(d[f"s{step}_v"]).to(DEV))
+        elif code == 1:
+            alloc.append_request(int(rid), torch.from_numpy(d[f"s{step}_k"]).to(DEV),
+                                 torch.from_numpy(d[f"s{step}_v"]).to(DEV))
+        else:
+            alloc.release_request(int(rid))
+        sync()
+        for t, key in ((alloc.k_quant, "k"), (alloc.v_quant, "v")):
+            assert np.array_equal(np_of(t.values), d[f"s{step}_{key}values"]), (step, key)
+            assert np.array_equal(np_of(t.scale).view(np.uint32), d[f"s{step}_{key}scale"].view(np.uint32))
+            assert np.array_equal(np_of(t.zero_point), d[f"s{step}_{key}zero"])
+        live = alloc.live_request_ids
+        if live:
+            c = alloc.to_cache(live)
+            assert np.array_equal(np_of(c.block_table), d[f"s{step}_table"])
+
+
+def test_allocator_batched_append_bit_exact_against_oracle():
+    announce("allocator batched append H4 D64 page16")
+    H, D, bs = 4, 64, 16
+    alloc = fa.PagedKVAllocator(capacity_blocks=64, heads=H, head_dim=D, block_size=bs, device=DEV)
+    ora = op.OracleAllocator(64, H, D, bs)
+    lens = [5, 16, 31, 1]
+    for rid, L in enumerate(lens):
+        k, v = randn((1, H, L, D), 100 + rid), randn((1, H, L, D), 200 + rid)
+        alloc.add_request(rid, k.to(DEV), v.to(DEV))
+        ora.add_request(rid, np_of(k.float()), np_of(v.float()))
+    alloc.release_request(1)
+    ora.release_request(1)
+    rids = [0, 2, 3]
+    for step in range(20):
+        kn, vn = randn((3, H, 1, D), 300 + step), randn((3, H, 1, D), 400 + step)
+        alloc.append_batch(rids, kn.to(DEV), vn.to(DEV))
+        ora.append_batch(rids, np_of(kn.float()), np_of(vn.float()))
+    sync()
+    assert np.array_equal(np_of(alloc.k_quant.values), ora.k_quant.values)
+    assert np.array_equal(np_of(alloc.v_quant.scale).view(np.uint32), ora.v_quant.scale.view(np.uint32))
+    q = randn((3, H, D), 77)
+    cache = alloc.to_cache(rids)
+    announce("allocator cache -> paged attention")
+    got = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    assert_attention_close(got, oa.paged_quant_attention(np_of(q), ora.to_cache(rids)), torch.float16, "alloc")
+
+
+# ---- attention parity ------------------------------------------------------------------------
+
+def _fused_case(B, H, S, D, bs, seed, q_dtype=torch.float16, lengths=None):
+    q = randn((B, H, D), seed, q_dtype)
+    k = randn((B, H, S, D), seed + 1, torch.float16)
+    v = randn((B, H, S, D), seed + 2, torch.float16)
+    kq = oq.quantize_int8_per_block(np_of(k.float()), bs)
+    vq = oq.quantize_int8_per_block(np_of(v.float()), bs)
+    lens = None if lengths is None else torch.tensor(lengths, dtype=torch.int64)
+    return q, kq, vq, lens
+
+
+@pytest.mark.parametrize("B,H,S,D,bs,q_dtype,lengths", [
+    (2, 3, 129, 64, 16, torch.float16, [129, 113]),       # reference GPU test shape
+    (2, 4, 1500, 128, 16, torch.float16, [1500, 977]),    # reference split-K test shape
+    (4, 32, 2048, 128, 16, torch.float16, None),          # config 1
+    (2, 8, 700, 128, 16, torch.bfloat16, [700, 1]),
+    (2, 8, 300, 128, 16, torch.float32, [0, 300]),
+    (1, 2, 517, 256, 16, torch.float16, None),
+    (2, 2, 77, 32, 16, torch.float16, [77, 40]),          # generic path: head_dim 32
+    (2, 3, 200, 64, 8, torch.float16, [200, 99]),         # generic path: quant block 8
+])
+def test_fused_attention_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
+    announce(f"fused B{B} H{H} S{S} D{D} bs{bs} {q_dtype} lengths={lengths}")
+    q, kq, vq, lens = _fused_case(B, H, S, D, bs, seed=B * 1000 + S, q_dtype=q_dtype, lengths=lengths)
+    got, stats = fa.fused_dequant_attention_triton(
+        q.to(DEV), to_qt(kq, DEV), to_qt(vq, DEV), lengths=None if lens is None else lens.to(DEV),
+        return_stats=True)
+    sync()
+    assert stats["materializes_dense_kv"] == 0.0
+    ref = oa.fused_dequant_attention(np_of(q), kq, vq, None if lens is None else lens.numpy())
+    if lengths is not None and 0 in lengths:
+        zero_rows = [i for i, L in enumerate(lengths) if L == 0]
+        assert (got[zero_rows] == 0).all()  # an empty row writes zeros (triton_utils.py:181-186)
+        keep = [i for i, L in enumerate(lengths) if L != 0]
+        got, ref = got[keep], ref[keep]
+    assert_attention_close(got, ref, q_dtype, "fused")
+
+
+def test_fused_split_k_is_used_and_matches_single_split(monkeypatch):
+    announce("fused split vs single split")
+    q, kq, vq, _ = _fused_case(2, 4, 1500, 128, 16, seed=5)
+    args = (q.to(DEV), to_qt(kq, DEV), to_qt(vq, DEV))
+    multi, stats = fa.fused_dequant_attention_triton(*args, return_stats=True)
+    assert stats["num_splits"] > 1.0
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", "1")
+    single, stats1 = fa.fused_dequant_attention_triton(*args, return_stats=True)
+    sync()
+    assert stats1["num_splits"] == 1.0
+    assert (multi.float() - single.float()).abs().max().item() <= 2e-3
+
+
+def _paged_case(B, H, S, D, page, seed, layout="contiguous", lengths=None, q_dtype=torch.float16):
+    q = randn((B, H, D), seed, q_dtype)
+    k = randn((B, H, S, D), seed + 1)
+    v = randn((B, H, S, D), seed + 2)
+    lens = None if lengths is None else torch.tensor(lengths, dtype=torch.int64)
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=page,
+                                       lengths=None if lens is None else lens.to(DEV),
+                                       block_table_pattern=layout, layout_seed=seed)
+    return q, cache
+
+
+@pytest.mark.parametrize("B,H,S,D,page,layout,lengths", [
+    (2, 3, 129, 64, 16, "contiguous", [129, 113]),        # reference GPU test shape
+    (8, 32, 2048, 128, 16, "contiguous", None),           # config 3
+    (16, 32, 4096, 128, 16, "shuffled", [4096 - 256 * i for i in range(16)]),     # config 4
+    (16, 32, 4096, 128, 16, "interleaved", [4096 - 256 * i - 7 for i in range(16)]),  # config 4, ragged tails
+    (3, 4, 300, 128, 32, "shuffled", [300, 17, 0]),       # two tiles per page
+    (2, 2, 64, 256, 16, "interleaved", [64, 63]),
+    (2, 2, 7, 64, 4, "contiguous", None),                 # generic path: page 4
+    (2, 3, 50, 48, 16, "shuffled", [50, 3]),              # generic path: head_dim 48
+])
+def test_paged_attention_matches_oracle(B, H, S, D, page, layout, lengths):
+    announce(f"paged B{B} H{H} S{S} D{D} page{page} {layout} lengths={lengths}")
+    q, cache = _paged_case(B, H, S, D, page, seed=B * 100 + S, layout=layout, lengths=lengths)
+    got, stats = fa.paged_quant_attention_triton(q.to(DEV), cache, return_stats=True)
+    sync()
+    assert stats["materializes_dense_kv"] == 0.0
+    ref = oracle_paged_attention(q, cache)
+    if lengths is not None and 0 in lengths:
+        keep = [i for i, L in enumerate(lengths) if L != 0]
+        assert (got[[i for i in range(B) if i not in keep]] == 0).all()
+        got, ref = got[keep], ref[keep]
+    assert_attention_close(got, ref, torch.float16, "paged")
+
+
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float32])
+def test_paged_attention_other_query_dtypes(q_dtype):
+    announce(f"paged dtype {q_dtype}")
+    q, cache = _paged_case(4, 8, 1000, 128, 16, seed=11, layout="shuffled", lengths=[1000, 999, 500, 16],
+                           q_dtype=q_dtype)
+    got = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    sync()
+    assert got.dtype == q_dtype
+    assert_attention_close(got, oracle_paged_attention(q, cache), q_dtype, str(q_dtype))
+
+
+def test_metric_shape_paged_b8_h32_s4096_d128_matches_oracle():
+    announce("metric paged B8 H32 S4096 D128")
+    q, cache = _paged_case(8, 32, 4096, 128, 16, seed=0)
+    got = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    sync()
+    assert_attention_close(got, oracle_paged_attention(q, cache), torch.float16, "metric")
+
+
+def test_layouts_and_fused_give_bit_identical_outputs():
+    """Same logical K/V in any physical layout (or contiguous) runs the same arithmetic."""
+
+    announce("layout invariance B4 H8 S1000 D128")
+    k, v, q = randn((4, 8, 1000, 128), 1), randn((4, 8, 1000, 128), 2), randn((4, 8, 128), 3).to(DEV)
+    lengths = torch.tensor([1000, 999, 512, 7], device=DEV)
+    outs = []
+    for layout in ("contiguous", "shuffled", "interleaved"):
+        cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), 16, lengths=lengths, block_table_pattern=layout)
+        outs.append(fa.paged_quant_attention_triton(q, cache))
+    kq = fa.quantize_int8_per_block(k.to(DEV), 16)
+    vq = fa.quantize_int8_per_block(v.to(DEV), 16)
+    outs.append(fa.fused_dequant_attention_triton(q, kq, vq, lengths=lengths))
+    sync()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+def test_inline_and_launched_split_merge_agree(monkeypatch):
+    announce("split merge inline vs launch")
+    q, cache = _paged_case(8, 32, 2048, 128, 16, seed=21, layout="shuffled",
+                           lengths=[2048, 2000, 1024, 1023, 512, 100, 17, 1])
+    inline = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    monkeypatch.setenv("FLASHSPEC_SPLIT_MERGE", "launch")
+    launched = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    sync()
+    assert torch.equal(inline, launched)
+    # repeated inline calls reuse the self-clearing arrival counters
+    monkeypatch.delenv("FLASHSPEC_SPLIT_MERGE")
+    for _ in range(3):
+        again = fa.paged_quant_attention_triton(q.to(DEV), cache)
+        sync()
+        assert torch.equal(again, inline)
+
+
+@pytest.mark.parametrize("warps", ["1", "2", "8"])
+def test_waves_per_block_knob(monkeypatch, warps):
+    announce(f"num_warps={warps}")
+    q, cache = _paged_case(2, 8, 900, 128, 16, seed=31, lengths=[900, 450])
+    base = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    monkeypatch.setenv("FLASHSPEC_NUM_WARPS", warps)
+    other = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    sync()
+    assert torch.equal(base, other)
+
+
+def test_unallocated_pages_and_lengths_past_the_table_are_masked():
+    """-1 table entries and lengths beyond max_seq_len follow the Triton kernel's masking."""
+
+    announce("table -1 entries / clamped lengths")
+    q, cache = _paged_case(2, 4, 64, 128, 16, seed=41)
+    table = cache.block_table.clone()
+    table[1, 2:] = -1  # row 1 keeps only 32 tokens of backing pages
+    lengths = torch.tensor([999, 32], device=DEV)  # row 0 clamps to max_seq_len
+    masked = fa.PagedKVCache(cache.k_quant, cache.v_quant, table, lengths, 16, 64)
+    got = fa.paged_quant_attention_triton(q.to(DEV), masked)
+    sync()
+    trimmed = fa.PagedKVCache(cache.k_quant, cache.v_quant, cache.block_table, torch.tensor([64, 32], device=DEV),
+                              16, 64)
+    assert_attention_close(got, oracle_paged_attention(q, trimmed), torch.float16, "masked")
+
+
+def test_graph_replay_matches_eager():
+    announce("graph capture/replay paged attention")
+    q, cache = _paged_case(8, 32, 1024, 128, 16, seed=51, layout="shuffled")
+    qd = q.to(DEV)
+    eager = fa.paged_quant_attention_triton(qd, cache)  # also creates the arrival counters
+    sync()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream(DEV)
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(stream):
+        fa.paged_quant_attention_triton(qd, cache)  # counters for this stream exist before capture
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            out = fa.paged_quant_attention_triton(qd, cache)
+    torch.cuda.current_stream(DEV).wait_stream(stream)
+    for i in range(4):
+        graph.replay()
+        sync()
+        scratch = torch.randn(1024, device=DEV).sum()  # eager work between replays
+        sync()
+        assert torch.equal(out, eager), f"replay {i}"
+        del scratch
+
+
+def test_gpu_validation_errors_before_launch():
+    announce("validation errors")
+    q, cache = _paged_case(2, 4, 64, 128, 16, seed=61)
+    with pytest.raises(ValueError):
+        fa.paged_quant_attention_triton(q[:, :2].to(DEV), cache)
+    with pytest.raises(ValueError):
+        fa.paged_quant_attention_triton(q.to(DEV).to(torch.float64), cache)
+    kq = fa.quantize_int8_per_block(randn((2, 4, 64, 128), 1).to(DEV))
+    with pytest.raises(ValueError):
+        fa.fused_dequant_attention_triton(q.to(DEV), kq, kq, lengths=torch.tensor([1, 2, 3], device=DEV))
+    with pytest.raises(RuntimeError):
+        fa.fused_dequant_attention_triton(q.to(DEV), kq, kq, lengths=torch.tensor([1, 2]))
