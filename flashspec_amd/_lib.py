@@ -23,17 +23,17 @@ _SIGNATURES = {
     "fs_last_error": (ctypes.c_char_p, []),
     "fs_abi_version": (c_int, []),
     "fs_decode_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "fs_decode_tiled_path": (c_int, [c_int, c_int, c_int]),
     "fs_fused_decode_i8": (
         c_int,
         [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-         c_void_p, c_int64, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int,
-         c_void_p],
+         c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
     ),
     "fs_paged_decode_i8": (
         c_int,
         [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
-         c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_int, c_int64, c_int, c_int, c_int,
-         c_float, c_int, c_int, c_int, c_void_p],
+         c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float,
+         c_int, c_int, c_int, c_void_p],
     ),
     "fs_combine_splits": (
         c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p]
@@ -92,7 +92,11 @@ def require():
 
 
 def reload() -> bool:
-    """Re-open the library after an in-process build."""
+    """Retry opening the library (e.g. after building it in this process).
+
+    A library already opened by this process is not re-read from disk: rebuild
+    before starting the process that uses it.
+    """
 
     _load()
     return available()

@@ -18,13 +18,10 @@ import torch
 from . import _lib
 from .quant import QuantizedTensor, build_compression_stats, estimate_quantized_bytes
 from .triton_utils import (
-    arrival_counters,
-    device_cu_count,
     dispatch_triton_or_fallback,
-    plan_splits,
+    launch_plan,
     resolve_block_n as _resolve_block_n,
     resolve_num_warps as _resolve_num_warps,
-    split_merge_mode,
     validate_decode_query,
 )
 
@@ -104,24 +101,21 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     seq_len = int(k_quant.original_shape[-2])
     n_blocks = int(kv[0].shape[-3])
     block_size = int(k_quant.block_size)
-    block_n = _resolve_block_n()
-    num_warps = _resolve_num_warps()
     out = torch.empty_like(q_c)
     sm_scale = 1.0 / math.sqrt(float(head_dim))
     rows = batch * heads
-    split_tiles, max_splits = plan_splits(seq_len, rows, block_n, device_cu_count(dev))
+    tiled, waves, split_tiles, max_splits, block_n = launch_plan(seq_len, rows, head_dim, block_size, block_size,
+                                                                 dev)
     stream = _lib.stream_ptr(dev)
-    workspace, ws_bytes, counters = None, 0, None
+    workspace, ws_bytes = None, 0
     if max_splits > 1:
         ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        if split_merge_mode() == "inline":
-            counters = arrival_counters(dev, stream, rows)
     _lib.check(lib.fs_fused_decode_i8(
         q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), _lib.ptr(lengths_c),
-        out.data_ptr(), _lib.ptr(workspace), ws_bytes, _lib.ptr(counters), batch, heads, head_dim, seq_len,
-        n_blocks, block_size, sm_scale, split_tiles, max_splits, num_warps, stream))
-    if max_splits > 1 and counters is None:
+        out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads, head_dim, seq_len, n_blocks, block_size,
+        sm_scale, split_tiles, max_splits, waves, stream))
+    if max_splits > 1:
         _lib.check(lib.fs_combine_splits(
             workspace.data_ptr(), _lib.ptr(lengths_c), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,
             head_dim, seq_len, split_tiles, max_splits, stream))
@@ -131,8 +125,8 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     quant_bytes = estimate_quantized_bytes(k_quant) + estimate_quantized_bytes(v_quant)
     return out, build_compression_stats(
         dense_bytes, quant_bytes, materializes_dense_kv=False,
-        num_splits=float(max_splits), block_n=float(block_n), num_warps=float(num_warps),
-        split_tiles=float(split_tiles),
+        num_splits=float(max_splits), block_n=float(block_n), num_warps=float(waves),
+        split_tiles=float(split_tiles), tiled_path=float(tiled),
     )
 
 

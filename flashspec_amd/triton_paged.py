@@ -2,10 +2,11 @@
 
 Drop-in for reference src/flashspec/triton_paged.py: same public entry
 ``paged_quant_attention_triton(q, cache, return_stats=False)``, same knob names
-and validation errors.  The launch goes to ``fs_paged_decode_i8``: each wave
-resolves its block_table entries once per page into a base offset (instead of
-per-token-lane table loads), streams the int8 pages with coalesced 16-byte
-loads, and splits long rows across waves with an fp32 log-sum-exp merge.
+and validation errors.  The launch goes to ``fs_paged_decode_i8``: a workgroup of
+cooperating waves resolves each block_table entry once per page into a base offset
+(instead of per-token-lane table loads), streams the int8 pages with coalesced
+16-byte loads and merges its waves in LDS; rows only split across workgroups when
+there are fewer rows than CUs (fp32 log-sum-exp merge in a second launch).
 """
 
 from __future__ import annotations
@@ -19,13 +20,10 @@ from . import _lib
 from .paged import PagedKVCache
 from .quant import build_compression_stats
 from .triton_utils import (
-    arrival_counters,
-    device_cu_count,
     dispatch_triton_or_fallback,
-    plan_splits,
+    launch_plan,
     resolve_block_n as _resolve_block_n,
     resolve_num_warps as _resolve_num_warps,
-    split_merge_mode,
     validate_decode_query,
 )
 
@@ -85,25 +83,22 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
     batch, heads, head_dim = (int(s) for s in q_c.shape)
     max_seq_len = int(cache.max_seq_len)
     num_pages = int(kq.original_shape[0])
-    block_n = _resolve_block_n()
-    num_warps = _resolve_num_warps()
     out = torch.empty_like(q_c)
     sm_scale = 1.0 / math.sqrt(float(head_dim))
     rows = batch * heads
-    split_tiles, max_splits = plan_splits(max_seq_len, rows, block_n, device_cu_count(dev))
+    tiled, waves, split_tiles, max_splits, block_n = launch_plan(
+        max_seq_len, rows, head_dim, int(cache.block_size), int(kq.block_size), dev)
     stream = _lib.stream_ptr(dev)
-    workspace, ws_bytes, counters = None, 0, None
+    workspace, ws_bytes = None, 0
     if max_splits > 1:
         ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        if split_merge_mode() == "inline":
-            counters = arrival_counters(dev, stream, rows)
     _lib.check(lib.fs_paged_decode_i8(
         q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), table.data_ptr(),
         table.element_size(), int(table.shape[1]), lengths.data_ptr(), out.data_ptr(), _lib.ptr(workspace),
-        ws_bytes, _lib.ptr(counters), batch, heads, head_dim, num_pages, int(cache.block_size),
-        int(kq.block_size), max_seq_len, sm_scale, split_tiles, max_splits, num_warps, stream))
-    if max_splits > 1 and counters is None:
+        ws_bytes, batch, heads, head_dim, num_pages, int(cache.block_size), int(kq.block_size), max_seq_len,
+        sm_scale, split_tiles, max_splits, waves, stream))
+    if max_splits > 1:
         _lib.check(lib.fs_combine_splits(
             workspace.data_ptr(), lengths.data_ptr(), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,
             head_dim, max_seq_len, split_tiles, max_splits, stream))
@@ -113,8 +108,8 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
     return out, build_compression_stats(
         dense_bytes, cache.estimated_bytes(), materializes_dense_kv=False,
         physical_blocks=float(cache.block_table.ge(0).sum().item()),
-        block_n=float(block_n), num_warps=float(num_warps), num_splits=float(max_splits),
-        split_tiles=float(split_tiles),
+        block_n=float(block_n), num_warps=float(waves), num_splits=float(max_splits),
+        split_tiles=float(split_tiles), tiled_path=float(tiled),
     )
 
 

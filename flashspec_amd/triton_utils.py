@@ -88,12 +88,18 @@ def resolve_num_warps() -> int:
 
 
 # ---- split-K planning for the HIP kernels ---------------------------------------------------
-# One wave streams one split.  The plan aims at WAVES_PER_CU resident waves per CU for
-# a uniform batch and bounds a split to [MIN, MAX] tiles so short rows are not
-# over-split and long rows of a ragged batch still spread over many waves.
-WAVES_PER_CU = 16
+# Tiled path: one split = one workgroup of W cooperating waves.  Rows split only when
+# there are fewer rows than CUs (the split count fills the GPU, each split keeping at
+# least MIN_SPLIT_TILES tiles); W is then the largest power of two up to 16 that leaves
+# every wave MIN_TILES_PER_WAVE tiles, unless FLASHSPEC_NUM_WARPS fixes it.  A split
+# holds at most 64 tiles per wave.  Generic path: one split = one wave of 8..64 tiles.
+MAX_TILED_WAVES = 16
 MIN_SPLIT_TILES = 8
-MAX_SPLIT_TILES = 64
+MIN_TILES_PER_WAVE = 4
+MAX_TILES_PER_WAVE = 64
+GENERIC_WAVES_PER_CU = 16
+GENERIC_MIN_SPLIT_TILES = 8
+GENERIC_MAX_SPLIT_TILES = 64
 
 _CU_CACHE: dict = {}
 
@@ -101,7 +107,8 @@ _CU_CACHE: dict = {}
 def device_cu_count(device) -> int:
     import torch
 
-    key = torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device()
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
     if key not in _CU_CACHE:
         _CU_CACHE[key] = int(torch.cuda.get_device_properties(key).multi_processor_count)
     return _CU_CACHE[key]
@@ -123,39 +130,65 @@ def forced_num_splits(seq_len: int, block_n: int) -> int | None:
     return max(1, min(forced, max_splits))
 
 
-def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int) -> tuple[int, int]:
-    """Return ``(split_tiles, max_splits)`` for a launch over ``rows`` rows of up to ``seq_len`` tokens."""
+def forced_tiled_waves() -> int | None:
+    """FLASHSPEC_NUM_WARPS as waves per workgroup on the tiled path (1/2/4/8/16), or None."""
+
+    override = os.environ.get("FLASHSPEC_NUM_WARPS")
+    if override is None:
+        return None
+    try:
+        v = int(override)
+    except ValueError:
+        return None
+    return v if v in (1, 2, 4, 8, 16) else None
+
+
+def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: bool = True,
+                waves: int | None = None, max_waves: int = MAX_TILED_WAVES) -> tuple[int, int, int]:
+    """Return ``(split_tiles, max_splits, waves_per_block)`` for one decode launch.
+
+    ``rows`` rows of up to ``seq_len`` tokens; ``waves`` fixes the workgroup size
+    (tiled path) or the waves grouped per workgroup (generic path).
+    """
 
     tiles = max(1, math.ceil(seq_len / TILE_TOKENS))
     forced = forced_num_splits(seq_len, block_n)
-    if forced is not None:
-        split_tiles = math.ceil(tiles / forced)
+    if tiled:
+        if forced is not None:
+            n = forced
+        else:
+            n = max(1, math.ceil(cu_count / max(1, rows)))
+            n = min(n, max(1, math.ceil(tiles / MIN_SPLIT_TILES)))
+        split_tiles = math.ceil(tiles / n)
+        if waves is None:
+            waves = 1
+            while waves < max_waves and 2 * waves * MIN_TILES_PER_WAVE <= split_tiles:
+                waves *= 2
+        cap = MAX_TILES_PER_WAVE * waves
+        if split_tiles > cap:
+            split_tiles = math.ceil(tiles / math.ceil(tiles / cap))
     else:
-        want = math.ceil(rows * tiles / max(1, cu_count * WAVES_PER_CU))
-        split_tiles = min(max(want, MIN_SPLIT_TILES), MAX_SPLIT_TILES)
-        split_tiles = min(split_tiles, tiles)
+        if forced is not None:
+            split_tiles = math.ceil(tiles / forced)
+        else:
+            want = math.ceil(rows * tiles / max(1, cu_count * GENERIC_WAVES_PER_CU))
+            split_tiles = min(max(want, GENERIC_MIN_SPLIT_TILES), GENERIC_MAX_SPLIT_TILES, tiles)
+        waves = waves or 4
     split_tiles = max(1, split_tiles)
-    return split_tiles, math.ceil(tiles / split_tiles)
+    return split_tiles, math.ceil(tiles / split_tiles), waves
 
 
-def split_merge_mode() -> str:
-    """``inline`` (last arriving wave merges; default) or ``launch`` (separate combine kernel)."""
+def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, device):
+    """(tiled, waves_per_block, split_tiles, max_splits, block_n) for one decode launch."""
 
-    mode = os.environ.get("FLASHSPEC_SPLIT_MERGE", "inline").strip().lower()
-    return mode if mode in ("inline", "launch") else "inline"
+    from . import _lib
 
-
-_COUNTERS: dict = {}
-
-
-def arrival_counters(device, stream_ptr: int, rows: int):
-    """Zeroed per-row arrival counters, cached per (device, stream) and left zero by the kernels."""
-
-    import torch
-
-    key = (torch.device(device).index, stream_ptr)
-    buf = _COUNTERS.get(key)
-    if buf is None or buf.numel() < rows:
-        buf = torch.zeros(max(rows, 1024), dtype=torch.int32, device=device)
-        _COUNTERS[key] = buf
-    return buf
+    tiled = bool(_lib.require().fs_decode_tiled_path(head_dim, page_size, quant_block))
+    max_waves = 8 if head_dim == 256 else MAX_TILED_WAVES  # register budget of the head_dim-256 kernel
+    waves = forced_tiled_waves() if tiled else resolve_num_warps()
+    if tiled and waves is not None:
+        waves = min(waves, max_waves)
+    block_n = resolve_block_n()
+    split_tiles, max_splits, waves = plan_splits(seq_len, rows, block_n, device_cu_count(device), tiled=tiled,
+                                                 waves=waves, max_waves=max_waves)
+    return tiled, waves, split_tiles, max_splits, block_n

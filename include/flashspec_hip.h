@@ -4,8 +4,8 @@
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t passed
  * as `void*` (NULL = the null stream).  The library never allocates device
- * memory: the caller owns every buffer, including the split-K workspace and
- * the per-row arrival counters.  Work is enqueued asynchronously on `stream`.
+ * memory: the caller owns every buffer, including the split-K workspace.
+ * Work is enqueued asynchronously on `stream`.
  *
  * Return value: FS_OK (0) on success.  FS_ERR_INVALID means a shape/layout
  * argument was rejected before launch (the reference raises ValueError);
@@ -45,12 +45,21 @@ int fs_abi_version(void);
 int64_t fs_decode_workspace_bytes(int64_t rows, int64_t max_splits, int64_t head_dim);
 
 /*
+ * Which decode kernel serves a shape: 1 = tiled path (head_dim 64/128/256, quant
+ * block 16, page a multiple of 16), 0 = generic path.  The split plan differs:
+ * on the tiled path one split is one workgroup of `waves_per_block` cooperating
+ * waves (split_tiles <= 64 * waves_per_block); on the generic path one split is
+ * one wave and `waves_per_block` only groups independent waves.
+ */
+int fs_decode_tiled_path(int head_dim, int page_size, int quant_block);
+
+/*
  * Contiguous INT8 decode attention (one query token per row), split-K with an
  * fp32 log-sum-exp merge.
  *
- * Replaces the launches of _fused_dequant_attention_kernel,
- * _fused_dequant_attention_split_kernel and _combine_splits_kernel in
- * reference src/flashspec/triton_fused.py:697-744 (launcher
+ * Replaces the launches of _fused_dequant_attention_kernel and
+ * _fused_dequant_attention_split_kernel in reference
+ * src/flashspec/triton_fused.py:697-734 (launcher
  * _run_fused_dequant_attention_triton, triton_fused.py:604-761).
  *
  *   q        [batch, heads, head_dim]            q_dtype
@@ -58,17 +67,18 @@ int64_t fs_decode_workspace_bytes(int64_t rows, int64_t max_splits, int64_t head
  *            scale  [batch, heads, n_blocks] fp32, zero [batch, heads, n_blocks] int16
  *   lengths  [batch] int64 or NULL (NULL = every row uses seq_len)
  *   out      [batch, heads, head_dim]            q_dtype
- *   workspace  >= fs_decode_workspace_bytes(batch*heads, max_splits, head_dim)
- *   counters   [batch*heads] uint32, all zero on entry; left zero on exit.
- *              NULL selects the two-launch path (split kernel + combine kernel).
- *   split_tiles  16-token tiles per split; max_splits = ceil(ceil(seq_len/16)/split_tiles)
- *   waves_per_block  1, 2, 4 or 8 (the reference's num_warps knob)
+ *   split_tiles  16-token tiles per split; max_splits >= ceil(ceil(seq_len/16)/split_tiles)
+ *   workspace    >= fs_decode_workspace_bytes(batch*heads, max_splits, head_dim) when
+ *                max_splits > 1 (else may be NULL).  Rows needing one split are written
+ *                to `out` directly; rows needing more leave partial states that
+ *                fs_combine_splits merges into `out`.
+ *   waves_per_block  1, 2, 4, 8 or 16
  */
 int fs_fused_decode_i8(const void* q, int q_dtype,
                        const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
                        const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
                        const int64_t* lengths, void* out,
-                       void* workspace, int64_t workspace_bytes, uint32_t* counters,
+                       void* workspace, int64_t workspace_bytes,
                        int batch, int heads, int head_dim, int seq_len,
                        int n_blocks, int block_size, float sm_scale,
                        int split_tiles, int max_splits, int waves_per_block, void* stream);
@@ -85,20 +95,21 @@ int fs_fused_decode_i8(const void* q, int q_dtype,
  *   block_table [batch, table_cols], int32 (table_index_bytes = 4) or int64 (8);
  *       entries < 0 or >= num_pages mark unallocated pages, whose tokens are masked.
  *   lengths [batch] int64; a row attends to min(lengths[b], max_seq_len) tokens.
+ *   Splits, workspace and fs_combine_splits as for fs_fused_decode_i8.
  */
 int fs_paged_decode_i8(const void* q, int q_dtype,
                        const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
                        const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
                        const void* block_table, int table_index_bytes, int64_t table_cols,
                        const int64_t* lengths, void* out,
-                       void* workspace, int64_t workspace_bytes, uint32_t* counters,
+                       void* workspace, int64_t workspace_bytes,
                        int batch, int heads, int head_dim, int64_t num_pages,
                        int page_size, int quant_block, int max_seq_len, float sm_scale,
                        int split_tiles, int max_splits, int waves_per_block, void* stream);
 
 /*
- * Merge per-split partial states written by a decode call made with
- * counters == NULL.  Replaces _combine_splits_kernel
+ * Merge the per-split partial states a decode call with max_splits > 1 left in
+ * `workspace`, for the rows that needed more than one split.  Replaces _combine_splits_kernel
  * (reference src/flashspec/triton_fused.py:445-503).  `lengths` may be NULL;
  * with it each row merges ceil(min(len,seq_len)/16/split_tiles) splits (>= 1).
  */

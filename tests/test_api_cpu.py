@@ -41,7 +41,7 @@ def _seed():
 
 @pytest.fixture
 def clean_env(monkeypatch):
-    for key in ("FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_WARPS", "FLASHSPEC_SPLIT_MERGE"):
+    for key in ("FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_WARPS"):
         monkeypatch.delenv(key, raising=False)
     return monkeypatch
 
@@ -108,18 +108,34 @@ def test_default_knobs_match_reference(clean_env):
 
 
 def test_split_plan_covers_every_tile(clean_env):
-    for seq_len in (1, 15, 16, 17, 129, 1500, 2048, 4096, 16384):
-        for rows in (1, 8, 128, 256, 2048):
-            split_tiles, max_splits = triton_utils.plan_splits(seq_len, rows, 128, 256)
-            tiles = -(-seq_len // 16)
-            assert split_tiles >= 1 and max_splits >= 1
-            assert split_tiles * max_splits >= tiles > split_tiles * (max_splits - 1)
-    # metric shape: 256 rows of 256 tiles -> 16 splits of 16 tiles on 256 CUs
-    assert triton_utils.plan_splits(4096, 256, 128, 256) == (16, 16)
+    for tiled in (True, False):
+        for seq_len in (1, 15, 16, 17, 129, 1500, 2048, 4096, 16384, 65536):
+            for rows in (1, 8, 128, 256, 2048):
+                for fixed in (None, 1, 16):
+                    split_tiles, max_splits, waves = triton_utils.plan_splits(seq_len, rows, 128, 256, tiled=tiled,
+                                                                              waves=fixed)
+                    tiles = -(-seq_len // 16)
+                    assert split_tiles >= 1 and max_splits >= 1 and waves in (1, 2, 4, 8, 16)
+                    assert split_tiles * max_splits >= tiles > split_tiles * (max_splits - 1)
+                    if tiled:
+                        assert split_tiles <= 64 * waves
+                        if fixed:
+                            assert waves == fixed
+    plan = triton_utils.plan_splits
+    # metric shape: 256 rows on 256 CUs -> one 16-wave workgroup per row, no second launch
+    assert plan(4096, 256, 128, 256) == (256, 1, 16)
+    # few rows: split rows to fill the GPU; workgroup size follows the split length
+    assert plan(2048, 128, 128, 256) == (64, 2, 16)
+    assert plan(1500, 8, 128, 256) == (8, 12, 2)   # the reference's split-K test shape splits
+    assert plan(4096, 8, 128, 256) == (8, 32, 2)
     clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1")
-    assert triton_utils.plan_splits(4096, 256, 128, 256) == (256, 1)
+    assert plan(4096, 256, 128, 256) == (256, 1, 16)
     clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1000")  # clamped to ceil(S/block_n)
-    assert triton_utils.plan_splits(4096, 256, 128, 256) == (8, 32)
+    assert plan(4096, 256, 128, 256) == (8, 32, 2)
+    clean_env.setenv("FLASHSPEC_NUM_WARPS", "8")
+    assert triton_utils.forced_tiled_waves() == 8
+    clean_env.setenv("FLASHSPEC_NUM_WARPS", "16")
+    assert triton_utils.forced_tiled_waves() == 16 and triton_utils.resolve_num_warps() == 4
 
 
 def test_paged_cache_reconstructs_dense_quantized_kv():

@@ -45,16 +45,22 @@ def test_abi_version_and_workspace_size():
 def test_invalid_arguments_are_rejected_before_launch():
     lib = _lib.require()
     # head_dim 0 -> FS_ERR_INVALID, message names the problem
-    rc = lib.fs_paged_decode_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, None, 0, None, 1, 1, 0, 4, 16, 16, 64,
+    rc = lib.fs_paged_decode_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, None, 0, 1, 1, 0, 4, 16, 16, 64,
                                 0.1, 4, 1, 4, None)
     assert rc == _lib.FS_ERR_INVALID
     assert "head_dim" in lib.fs_last_error().decode()
     with pytest.raises(ValueError):
         _lib.check(rc)
     # splits that do not cover the sequence
-    rc = lib.fs_fused_decode_i8(1, 1, 1, 1, 1, 1, 1, 1, None, 1, None, 0, None, 1, 1, 128, 4096, 256, 16, 0.1,
+    rc = lib.fs_fused_decode_i8(1, 1, 1, 1, 1, 1, 1, 1, None, 1, None, 0, 1, 1, 128, 4096, 256, 16, 0.1,
                                 4, 4, 4, None)
     assert rc == _lib.FS_ERR_INVALID and "cover" in lib.fs_last_error().decode()
+    # tiled path: more than 64 tiles per wave in one split
+    rc = lib.fs_fused_decode_i8(1, 1, 1, 1, 1, 1, 1, 1, None, 1, None, 0, 1, 1, 128, 4096, 256, 16, 0.1,
+                                256, 1, 2, None)
+    assert rc == _lib.FS_ERR_INVALID and "64" in lib.fs_last_error().decode()
+    assert lib.fs_decode_tiled_path(128, 16, 16) == 1 and lib.fs_decode_tiled_path(128, 32, 16) == 1
+    assert lib.fs_decode_tiled_path(48, 16, 16) == 0 and lib.fs_decode_tiled_path(128, 16, 8) == 0
     # unsupported dtype code in quantize
     rc = lib.fs_quantize_i8(1, 9, 1, 16, 128, 16, 1, 1, 1, None)
     assert rc == _lib.FS_ERR_INVALID
