@@ -1,0 +1,252 @@
+"""Benchmark: paged INT8 decode attention, B8 H32 S4096 D128 (BASELINE.json metric) on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+One step = one ``paged_quant_attention_triton`` call over one batch (8 requests x 32
+heads x 4096 cached tokens, 16-token pages, fp16 query, INT8 K/V with fp32 scale and
+int16 zero point per page and head).  Inputs are synthetic, resident in HBM before
+timing, and rotated over 3 independent sets (3 x 269 MB) so the 256 MB Infinity
+Cache cannot serve a step from the previous one.  Prints ONE JSON line.
+
+``value`` = algorithmic bytes per step / measured time per step (GB/s).
+Algorithmic bytes = int8 K+V (2*sum(L)*H*D) + fp32 scale and int16 zero per page and
+head for K and V + int64 table entries + int64 lengths + fp16 q and output.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode-attn µs/step + achieved HBM GB/s (% of peak), paged INT8 B8 H32 s4096 d128"
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+B, H, S, D, PAGE = 8, 32, 4096, 128, 16
+ROTATE = 3
+PMC_SUMMARY = ROOT / "profiles" / "paged_decode_b8h32s4096d128_pmc.json"
+
+
+def algorithmic_bytes(lengths, heads: int, head_dim: int, page: int, q_bytes: int = 2, idx_bytes: int = 8) -> int:
+    pages = sum(math.ceil(L / page) for L in lengths)
+    kv = 2 * sum(lengths) * heads * head_dim
+    params = 2 * pages * heads * (4 + 2)
+    table = pages * idx_bytes
+    return kv + params + table + 8 * len(lengths) + 2 * len(lengths) * heads * head_dim * q_bytes
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--layout", default="contiguous", choices=["contiguous", "shuffled", "interleaved"])
+    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy"],
+                    help="full: the JSON line; paged: only the timed paged steps (for rocprofv3); "
+                         "copy: a plain 256 MiB device copy, to calibrate rocprofv3 byte counters")
+    return ap.parse_args()
+
+
+def copy_calibration(torch, steps: int) -> int:
+    """`steps` copies of 256 MiB (read 256 MiB + write 256 MiB each) with torch's copy kernel."""
+
+    n = 256 * 1024 * 1024 // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "copy", "bytes_read_per_copy": n * 4, "bytes_written_per_copy": n * 4,
+                      "copies": steps}), flush=True)
+    return 0
+
+
+def make_inputs(torch, fa, dev, seed: int, layout: str):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((B, H, D), generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn((B, H, S, D), generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn((B, H, S, D), generator=g, device=dev, dtype=torch.float16)
+    cache = fa.PagedKVCache.from_dense(k, v, block_size=PAGE, block_table_pattern=layout, layout_seed=seed)
+    kq = fa.quantize_int8_per_block(k, PAGE)
+    vq = fa.quantize_int8_per_block(v, PAGE)
+    del k, v
+    return q, cache, kq, vq
+
+
+def time_loop(torch, fn, steps: int, warmup: int) -> float:
+    """Mean ms per call over `steps` calls bracketed by synchronize + events."""
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_durations_us(torch, fn, calls: int) -> list[float]:
+    """Per-launch duration: an event pair around each call on the launching stream."""
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(calls)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(i)
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e3 for a, b in evs]
+
+
+def cpu_baseline(seconds_budget: float = 20.0) -> dict:
+    """Time the numpy oracle (reference algorithm, one thread) on a 2-request sample."""
+
+    import numpy as np
+
+    from oracle import attention as oa
+    from oracle import paged as op
+
+    sample_b = 2
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((sample_b, H, S, D), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((sample_b, H, S, D), dtype=np.float32).astype(np.float16)
+    q = rng.standard_normal((sample_b, H, D), dtype=np.float32).astype(np.float16)
+    cache = op.from_dense(k.astype(np.float32), v.astype(np.float32), PAGE)
+    times = []
+    t_end = time.perf_counter() + seconds_budget
+    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        oa.paged_quant_attention(q.astype(np.float32), cache)
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    nbytes = algorithmic_bytes([S] * sample_b, H, D, PAGE)
+    return {
+        "value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"numpy oracle paged attention (dequantize whole store, gather, einsum, softmax, einsum) "
+                  f"on {sample_b} of the 8 requests (H32 S4096 D128), median of {len(times)} runs, "
+                  f"{sec * 1e3:.0f} ms per run",
+    }
+
+
+def load_traffic(config_key: str):
+    if not PMC_SUMMARY.exists():
+        return None
+    try:
+        d = json.loads(PMC_SUMMARY.read_text())
+    except (OSError, ValueError):
+        return None
+    if d.get("config_key") != config_key:
+        return None
+    return d.get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is sharded by "
+              "(batch, head) rows with no cross-GPU exchange, so run one process per GPU instead.",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    import flashspec_amd as fa
+    from flashspec_amd import _lib
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    _lib.require()
+    dev = torch.device("cuda", 0)
+    if args.mode == "copy":
+        return copy_calibration(torch, args.steps)
+    sets = [make_inputs(torch, fa, dev, seed, args.layout) for seed in range(ROTATE)]
+    torch.cuda.synchronize()
+    lengths = [S] * B
+    nbytes = algorithmic_bytes(lengths, H, D, PAGE)
+
+    def paged_step(i):
+        q, cache, _, _ = sets[i % ROTATE]
+        return fa.paged_quant_attention_triton(q, cache)
+
+    def paged_warm(i):
+        q, cache, _, _ = sets[0]
+        return fa.paged_quant_attention_triton(q, cache)
+
+    def fused_step(i):
+        q, _, kq, vq = sets[i % ROTATE]
+        return fa.fused_dequant_attention_triton(q, kq, vq)
+
+    _, stats = fa.paged_quant_attention_triton(sets[0][0], sets[0][1], return_stats=True)
+    ms = time_loop(torch, paged_step, args.steps, args.warmup)
+    if args.mode == "paged":
+        print(json.dumps({"mode": "paged", "us_per_step": round(ms * 1e3, 2), "steps": args.steps,
+                          "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
+    durs = kernel_durations_us(torch, paged_step, max(30, min(args.steps, 300)))
+    kern_us = statistics.fmean(durs)
+    warm_ms = time_loop(torch, paged_warm, args.steps, args.warmup)
+    fused_ms = time_loop(torch, fused_step, args.steps, args.warmup)
+
+    value = nbytes / (ms * 1e-3) / 1e9
+    achieved = nbytes / (kern_us * 1e-6) / 1e9
+    config_key = f"paged_b{B}_h{H}_s{S}_d{D}_page{PAGE}_{args.layout}"
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_GBPS, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"paged INT8 decode attention B{B} H{H} S{S} D{D}, {PAGE}-token pages, "
+                        f"{args.layout} page layout, uniform lengths, {ROTATE} rotated input sets",
+            "batch": B, "heads": H, "seq_len": S, "head_dim": D, "page_size": PAGE,
+            "q_dtype": "float16", "kv_dtype": "int8 (per-page fp32 scale, int16 zero point)",
+            "layout": args.layout, "rotated_input_sets": ROTATE, "parallelism": "single GPU",
+            "num_splits": stats.get("num_splits"), "waves_per_workgroup": stats.get("num_warps"),
+        },
+        "algorithmic_bytes_per_step": nbytes,
+        "warm_cache_us_per_step": round(warm_ms * 1e3, 2),
+        "warm_cache_gbps": round(nbytes / (warm_ms * 1e-3) / 1e9, 1),
+        "fused_contiguous_us_per_step": round(fused_ms * 1e3, 2),
+        "paged_vs_fused_time_ratio": round(ms / fused_ms, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBPS, 4),
+            "traffic": load_traffic(config_key),
+            "kernel": "decode_rows_kernel<128, __half, true> (paged_quant_attention)",
+            "kernel_avg_us": round(kern_us, 2),
+            "kernel_launches_timed": len(durs),
+        },
+        "device": torch.cuda.get_device_name(dev),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
