@@ -8,12 +8,14 @@ GPU call never silently falls back to another implementation.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_float, c_int, c_int64, c_void_p
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().with_name("libflashspec_hip.so")
+# FLASHSPEC_HIP_LIB may name another build of the same library (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("FLASHSPEC_HIP_LIB") or Path(__file__).resolve().with_name("libflashspec_hip.so"))
 
 FS_OK, FS_ERR_INVALID, FS_ERR_RUNTIME = 0, 1, 2
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}

@@ -1,10 +1,11 @@
 // INT8 KV decode attention for gfx950: contiguous ("fused") and paged layouts.
 //
 // Tiled path (head_dim 64/128/256, 16-token quant blocks): one workgroup of W waves
-// owns one (row = batch*heads + head, split) pair.  Wave w streams tiles
-// w, w+W, w+2W, ... of the split; a tile of one head is 16*D contiguous int8 bytes in
-// both layouts, read with 16*D/1024 coalesced 16-byte loads per tensor, and the next
-// tile's loads are issued before the current tile is consumed.  Dequantization is
+// owns one (row = batch*heads + head, split) pair; wave w takes tiles w, w+W, w+2W, ...
+// of the split, each block_table entry and quant parameter resolved once by one lane.  A
+// tile of one head is 16*D contiguous int8 bytes in both layouts, read with 16*D/1024
+// coalesced 16-byte non-temporal loads per tensor, and a wave's next tile is in flight
+// while it consumes the current one.  Dequantization is
 // folded into the dot products:
 //     score = scale * (sum_d q_d*u_d - zero * sum_d q_d)        (u = stored int8 + 128)
 //     acc_d += p*scale*u_d,  corrected once by - sum p*scale*zero at the end,
@@ -24,7 +25,7 @@
 namespace fs {
 
 constexpr int kMaxWaves = 16;       // waves per workgroup on the tiled path
-constexpr int kMaxTilesPerWave = 64;  // per split: one metadata lane per tile
+constexpr int kMaxTilesPerWave = 64;  // per split and wave: one metadata lane per tile
 constexpr float kRescaleSlack = 8.0f;  // running max may lag the true max by 2^8
 
 struct DecodeParams {
@@ -87,6 +88,65 @@ __device__ __forceinline__ float dot16_u8(const float* q, uint4 raw) {
   return a0 + a1;
 }
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// fp16 queries: q held as fp16 pairs (q0,q2),(q1,q3) per dword of K bytes.  Bytes become
+// fp16 pairs (1024+u_a, 1024+u_b) with one byte permute and one XOR: the permute puts the
+// raw bytes in the low halves (high bytes zero), and XOR 0x6480 flips the int8 sign bit
+// (u = raw ^ 0x80) while setting the fp16 exponent of 1024.  v_dot2_f32_f16 multiplies
+// exactly and accumulates in fp32; the caller removes 1024 * sum(q).
+__device__ __forceinline__ float dot16_u8_f16(const uint32_t* qp, uint4 raw) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t p02 = __builtin_amdgcn_perm(0u, w[k], 0x0c020c00u) ^ 0x64806480u;
+    const uint32_t p13 = __builtin_amdgcn_perm(0u, w[k], 0x0c030c01u) ^ 0x64806480u;
+    a0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, p02), __builtin_bit_cast(half2_t, qp[2 * k]), a0, false);
+    a1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, p13), __builtin_bit_cast(half2_t, qp[2 * k + 1]), a1, false);
+  }
+  return a0 + a1;
+}
+
+// Query slice of one lane (16 dims) in the form its K dot product wants.
+template <typename QT>
+struct QSlice {
+  static constexpr float kOffset = 0.f;  // dot16 returns sum q*u
+  float q[16];
+  __device__ __forceinline__ void load(const QT* qp) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) q[e] = to_f32(qp[e]);
+  }
+  __device__ __forceinline__ float sum() const {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += q[e];
+    return s;
+  }
+  __device__ __forceinline__ float dot(uint4 raw) const { return dot16_u8(q, raw); }
+};
+
+template <>
+struct QSlice<__half> {
+  static constexpr float kOffset = 1024.f;  // dot16 returns sum q*(1024+u)
+  uint32_t qp[8];  // (q0,q2),(q1,q3),(q4,q6),(q5,q7),...
+  float qsum_part;
+  __device__ __forceinline__ void load(const __half* q) {
+    const uint16_t* h = (const uint16_t*)q;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      qp[2 * k] = (uint32_t)h[4 * k] | ((uint32_t)h[4 * k + 2] << 16);
+      qp[2 * k + 1] = (uint32_t)h[4 * k + 1] | ((uint32_t)h[4 * k + 3] << 16);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s += __half2float(q[4 * k + c]);
+    }
+    qsum_part = s;
+  }
+  __device__ __forceinline__ float sum() const { return qsum_part; }
+  __device__ __forceinline__ float dot(uint4 raw) const { return dot16_u8_f16(qp, raw); }
+};
+
 __device__ __forceinline__ void axpy16_u8(float* acc, float wgt, uint4 raw) {
   const uint32_t w[4] = {raw.x ^ 0x80808080u, raw.y ^ 0x80808080u, raw.z ^ 0x80808080u,
                          raw.w ^ 0x80808080u};
@@ -123,9 +183,19 @@ struct TileRegs {
   uint4 v[LPTILE];
 };
 
-// Loads one tile.  An unbacked tile (base < 0) loads tile 0 instead and its tokens are
-// masked by the caller: a branch around the loads would make the compiler route the
-// registers through a pointer select into scratch memory.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// K/V bytes are read exactly once: non-temporal loads keep them from displacing the
+// cache lines the rest of the GPU is using (measured: ~7% faster than plain loads).
+__device__ __forceinline__ uint4 stream_load(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Loads one tile.  An unbacked or out-of-range tile (base < 0) loads tile 0 of the store
+// instead and its tokens are masked by the caller: a branch around the loads would make
+// the compiler route the registers through a pointer select into scratch memory, and
+// the repeated tile-0 reads are L2 hits.
 template <int D>
 __device__ __forceinline__ void load_tile(TileRegs<D>& t, const int8_t* kbase, const int8_t* vbase, int base,
                                           int lane) {
@@ -134,9 +204,9 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& t, const int8_t* kbase, c
   const uint4* kp = (const uint4*)(kbase + off) + lane;
   const uint4* vp = (const uint4*)(vbase + off) + lane;
 #pragma unroll
-  for (int r = 0; r < LPTILE; ++r) t.k[r] = kp[r * kWave];
+  for (int r = 0; r < LPTILE; ++r) t.k[r] = stream_load(kp + r * kWave);
 #pragma unroll
-  for (int r = 0; r < LPTILE; ++r) t.v[r] = vp[r * kWave];
+  for (int r = 0; r < LPTILE; ++r) t.v[r] = stream_load(vp + r * kWave);
 }
 
 // Online-softmax state of one lane: token rows `g` of every tile, dims [16j, 16j+16).
@@ -145,8 +215,8 @@ struct LaneState {
   float acc[16];
 };
 
-template <int D>
-__device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<D>& t, const float* q, float qsum,
+template <int D, typename QT>
+__device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<D>& t, const QSlice<QT>& q, float qsum,
                                              bool valid_tile, int token0, int len, int g, float ks, float kz,
                                              float vs, float vz) {
   constexpr int LPT = TileRegs<D>::LPT, RPL = TileRegs<D>::RPL, LPTILE = TileRegs<D>::LPTILE;
@@ -155,9 +225,9 @@ __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<D>& t
   float mnew = st.m;
 #pragma unroll
   for (int r = 0; r < LPTILE; ++r) {
-    const float dot = group_sum<LPT>(dot16_u8(q, t.k[r]));
+    const float dot = group_sum<LPT>(q.dot(t.k[r]));
     ok[r] = valid_tile && (token0 + r * RPL + g) < len;
-    s[r] = (dot - kz * qsum) * ks;
+    s[r] = (dot - (QSlice<QT>::kOffset + kz) * qsum) * ks;
     if (ok[r]) mnew = fmaxf(mnew, s[r]);
   }
   // Refresh the running max only when some lane's max grew by more than the slack;
@@ -191,47 +261,50 @@ decode_rows_kernel(const DecodeParams p) {
   __shared__ float s_acc[kMaxWaves * D];
   __shared__ float s_ml[2 * kMaxWaves];
 
+#ifdef FS_TRACE_WG
+  const uint64_t trace_t0 = __builtin_amdgcn_s_memrealtime();
+#endif
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
+  // wave-uniform by construction; readfirstlane lets the compiler keep everything derived
+  // from it (tile counts, tile offsets, load base addresses) in scalar registers
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int W = blockDim.x / kWave;
   const int row = blockIdx.x / p.max_splits;
   const int split = blockIdx.x - row * p.max_splits;
   const int b = row / p.heads;
   const int h = row - b * p.heads;
+  // Lane k of wave w resolves the wave's k-th tile, first + W*k, once: base index (-1 = not
+  // backed by a page or past the row) and (key scale * qk_scale, key zero, value scale,
+  // value zero).  Waves take tiles w, w+W, w+2W, ...: all waves of all workgroups sweep
+  // the store in step, which keeps page accesses dense, and the fixed order makes results
+  // bit-reproducible.  The table loads are sized by max_seq_len so they go out together
+  // with the row-length load.
+  const int first = split * p.split_tiles + w;
+  const int tiles_max = (p.seq_len + kTile - 1) / kTile;
+  const int end_max = min(tiles_max, (split + 1) * p.split_tiles);
+  const int nk_max = first < end_max ? (end_max - first + W - 1) / W : 0;
+  int my_base = -1;
+  if (lane < nk_max) my_base = tile_base<PAGED>(p, b, h, row, first + W * lane);
+
   const int len = row_length(p.lengths, b, p.seq_len);
   const int nsplit = row_splits(len, p.split_tiles);
   if (split >= nsplit) return;  // whole workgroup, before any barrier
-  const int ntiles = (len + kTile - 1) / kTile;
-  const int tile_end = min(ntiles, (split + 1) * p.split_tiles);
-  const int first = split * p.split_tiles + w;                  // this wave's tiles: first + W*k
+  const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
   const int nk = first < tile_end ? (tile_end - first + W - 1) / W : 0;  // <= kMaxTilesPerWave
+  if (lane >= nk) my_base = -1;
+  float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
+  if (my_base >= 0) {
+    my_ks = p.sc[0][my_base] * p.qk_scale;
+    my_kz = (float)p.zp[0][my_base];
+    my_vs = p.sc[1][my_base];
+    my_vz = (float)p.zp[1][my_base];
+  }
 
   const int j = lane % LPT;  // dim slice [16j, 16j+16)
   const int g = lane / LPT;  // token row within a load
-
-  float q[16];
-  {
-    const QT* qp = (const QT*)p.q + (size_t)row * D + 16 * j;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) q[e] = to_f32(qp[e]);
-  }
-  float qsum = 0.f;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) qsum += q[e];
-  qsum = group_sum<LPT>(qsum);
-
-  // lane k resolves tile first + W*k once: base index and the four quant parameters
-  int my_base = -1;
-  float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
-  if (lane < nk) {
-    my_base = tile_base<PAGED>(p, b, h, row, first + W * lane);
-    if (my_base >= 0) {
-      my_ks = p.sc[0][my_base] * p.qk_scale;
-      my_kz = (float)p.zp[0][my_base];
-      my_vs = p.sc[1][my_base];
-      my_vz = (float)p.zp[1][my_base];
-    }
-  }
+  QSlice<QT> q;
+  q.load((const QT*)p.q + (size_t)row * D + 16 * j);
+  const float qsum = group_sum<LPT>(q.sum());
 
   LaneState st;
   st.m = kNegBig;
@@ -242,27 +315,33 @@ decode_rows_kernel(const DecodeParams p) {
 
   const int8_t* kbase = p.kv[0];
   const int8_t* vbase = p.kv[1];
-  TileRegs<D> ta, tb;
-  int base_a = nk > 0 ? readlane_i32(my_base, 0) : -1;
-  if (nk > 0) load_tile<D>(ta, kbase, vbase, base_a, lane);
+  auto base_of = [&](int k) { return k < nk ? readlane_i32(my_base, k) : -1; };
+  auto consume = [&](const TileRegs<D>& t, int k) {
+    consume_tile<D, QT>(st, t, q, qsum, readlane_i32(my_base, k) >= 0, (first + W * k) * kTile, len, g,
+                        readlane_f32(my_ks, k), readlane_f32(my_kz, k), readlane_f32(my_vs, k),
+                        readlane_f32(my_vz, k));
+  };
+  // two register buffers: tile k+1 is in flight while tile k is consumed
+  TileRegs<D> ta, tb2;
+  load_tile<D>(ta, kbase, vbase, base_of(0), lane);
   for (int k = 0; k < nk; k += 2) {
-    int base_b = -1;
-    if (k + 1 < nk) {
-      base_b = readlane_i32(my_base, k + 1);
-      load_tile<D>(tb, kbase, vbase, base_b, lane);
-    }
-    consume_tile<D>(st, ta, q, qsum, base_a >= 0, (first + W * k) * kTile, len, g, readlane_f32(my_ks, k),
-                    readlane_f32(my_kz, k), readlane_f32(my_vs, k), readlane_f32(my_vz, k));
+    load_tile<D>(tb2, kbase, vbase, base_of(k + 1), lane);
+    consume(ta, k);
+#ifdef FS_TRACE_WG
+    if (k == 0 && w == 0 && lane == 0)
+      ((uint64_t*)p.part_ml)[(size_t)blockIdx.x * 20 + 1] = __builtin_amdgcn_s_memrealtime();
+#endif
     if (k + 1 >= nk) break;
-    if (k + 2 < nk) {
-      base_a = readlane_i32(my_base, k + 2);
-      load_tile<D>(ta, kbase, vbase, base_a, lane);
-    }
-    consume_tile<D>(st, tb, q, qsum, base_b >= 0, (first + W * (k + 1)) * kTile, len, g,
-                    readlane_f32(my_ks, k + 1), readlane_f32(my_kz, k + 1), readlane_f32(my_vs, k + 1),
-                    readlane_f32(my_vz, k + 1));
+    load_tile<D>(ta, kbase, vbase, base_of(k + 2), lane);
+    consume(tb2, k + 1);
   }
 
+#ifdef FS_TRACE_WG
+  // per-workgroup record: [start, wave0 first-data, 16 x wave end, merged end]
+  uint64_t* trace = (uint64_t*)p.part_ml + (size_t)blockIdx.x * 20;
+  if (lane == 0) trace[2 + w] = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) trace[0] = trace_t0;
+#endif
 #pragma unroll
   for (int e = 0; e < 16; ++e) st.acc[e] -= st.zacc;
   // merge the token-row groups of the wave (lanes sharing a dim slice)
@@ -299,6 +378,9 @@ decode_rows_kernel(const DecodeParams p) {
     }
     if (nsplit == 1) {
       ((QT*)p.out)[(size_t)row * D + d] = from_f32<QT>(L > 0.f ? a / L : 0.f);
+#ifdef FS_TRACE_WG
+      if (d == 0) ((uint64_t*)p.part_ml)[(size_t)blockIdx.x * 20 + 19] = __builtin_amdgcn_s_memrealtime();
+#endif
     } else {
       const size_t ws = (size_t)row * p.max_splits + split;
       p.part_acc[ws * D + d] = a;

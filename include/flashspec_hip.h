@@ -73,6 +73,7 @@ int fs_decode_tiled_path(int head_dim, int page_size, int quant_block);
  *                to `out` directly; rows needing more leave partial states that
  *                fs_combine_splits merges into `out`.
  *   waves_per_block  1, 2, 4, 8 or 16
+ * Results are bit-reproducible: every wave sums its tiles in a fixed order.
  */
 int fs_fused_decode_i8(const void* q, int q_dtype,
                        const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
