@@ -8,7 +8,9 @@ this file, where ``flashspec_amd._lib`` loads it.  No torch headers are used.
 from __future__ import annotations
 
 import argparse
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -41,21 +43,44 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; set HIPCC")
 
 
-def _compile(src: Path, extra: list[str]) -> Path:
+def _compile(src: Path, extra: list[str]) -> tuple[Path, str]:
     obj = BUILD / (src.stem + ".o")
     cmd = [hipcc(), *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr[-8000:]}")
-    if proc.stderr.strip():
-        lines = [ln for ln in proc.stderr.splitlines() if "packed-fp32-ops" not in ln]
-        if any(ln.strip() for ln in lines):
-            sys.stderr.write("\n".join(lines) + "\n")
-    return obj
+    lines = [ln for ln in proc.stderr.splitlines() if ("warning" in ln or "error" in ln)
+             and "packed-fp32-ops" not in ln]
+    if lines:
+        sys.stderr.write("\n".join(lines) + "\n")
+    return obj, proc.stderr
 
 
-def build(resource_usage: bool = False, jobs: int = 4) -> Path:
-    """Compile and link; returns the path of the shared library."""
+RESOURCES = PKG / "kernel_resources.json"
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|TotalSGPRs|ScratchSize \[bytes/lane\]|"
+                     r"Occupancy \[waves/SIMD\]|LDS Size \[bytes/block\]):\s+(\S+)")
+
+
+def _parse_resources(text: str) -> list[dict]:
+    """Per-kernel VGPR/SGPR/LDS/occupancy from clang's kernel-resource-usage remarks."""
+
+    kernels, cur = [], None
+    for m in _REMARK.finditer(text):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = {"kernel": val}
+            kernels.append(cur)
+        elif cur is not None:
+            cur[key.split(" [")[0].lower()] = int(val) if val.isdigit() else val
+    return kernels
+
+
+def build(resource_usage: bool = True, jobs: int = 4) -> Path:
+    """Compile and link; returns the path of the shared library.
+
+    With ``resource_usage`` the per-kernel register/LDS/occupancy table of the device
+    code is written to ``kernel_resources.json`` beside the library.
+    """
 
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
@@ -63,7 +88,11 @@ def build(resource_usage: bool = False, jobs: int = 4) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     extra = ["-Rpass-analysis=kernel-resource-usage"] if resource_usage else []
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        objs = list(pool.map(lambda s: _compile(s, extra), sources))
+        results = list(pool.map(lambda s: _compile(s, extra), sources))
+    objs = [o for o, _ in results]
+    if resource_usage:
+        table = [k for _, text in results for k in _parse_resources(text)]
+        RESOURCES.write_text(json.dumps({"arch": ARCH, "kernels": table}, indent=1) + "\n")
     lib = PKG / LIB_NAME
     tmp = PKG / (LIB_NAME + ".tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
@@ -76,10 +105,10 @@ def build(resource_usage: bool = False, jobs: int = 4) -> Path:
 
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--resource-usage", action="store_true", help="print per-kernel VGPR/SGPR/LDS/occupancy")
+    ap.add_argument("--no-resource-usage", action="store_true", help="skip the register/occupancy table")
     ap.add_argument("-j", "--jobs", type=int, default=4)
     args = ap.parse_args()
-    print(build(resource_usage=args.resource_usage, jobs=args.jobs))
+    print(build(resource_usage=not args.no_resource_usage, jobs=args.jobs))
 
 
 if __name__ == "__main__":

@@ -256,6 +256,18 @@ class PagedKVAllocator:
         for request in requests:
             request.length += tokens
 
+    def shuffle_free_blocks(self, seed: int) -> None:
+        """Put the free list in a seeded random order, so later allocations scatter over the pool.
+
+        Not in the reference allocator, whose free list stays sorted (lowest page first);
+        ``release_request`` restores that sorted order.
+        """
+
+        g = torch.Generator()
+        g.manual_seed(int(seed))
+        order = torch.randperm(len(self._free_blocks), generator=g).tolist()
+        self._free_blocks = [self._free_blocks[i] for i in order]
+
     def release_request(self, request_id: int) -> None:
         """Return a request's pages to the free list (kept sorted; paged.py:146-151)."""
 
