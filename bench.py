@@ -49,9 +49,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--layout", default="contiguous", choices=["contiguous", "shuffled", "interleaved"])
-    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy"],
+    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "serving"],
                     help="full: the JSON line; paged: only the timed paged steps (for rocprofv3); "
-                         "copy: a plain 256 MiB device copy, to calibrate rocprofv3 byte counters")
+                         "copy: a plain 256 MiB device copy, to calibrate rocprofv3 byte counters; "
+                         "serving: only the 64-request serving decode step")
     return ap.parse_args()
 
 
@@ -139,6 +140,61 @@ def cpu_baseline(seconds_budget: float = 20.0) -> dict:
     }
 
 
+SERVE_B, SERVE_LO, SERVE_HI = 64, 128, 16384
+
+
+def serving_step_bench(torch, fa, dev, steps: int, warmup: int) -> dict:
+    """Serving decode step at scale: 64 requests, lengths ~ U[128, 16384] (seeded CPU draw),
+    fragmented shuffled page pool, one fp16 token appended per request per step and paged
+    attention over the updated cache (device-resident table and lengths, two launches + the
+    split merge when a request needs it)."""
+
+    from flashspec_amd.serving import DecodeBatch, build_request_pool
+
+    g = torch.Generator().manual_seed(0)
+    lengths = torch.randint(SERVE_LO, SERVE_HI + 1, (SERVE_B,), generator=g).tolist()
+    total = warmup + steps
+    alloc, rids = build_request_pool(lengths, heads=H, head_dim=D, block_size=PAGE, headroom_tokens=total + 1,
+                                     seed=0, device=dev, dtype=torch.float16)
+    batch = DecodeBatch(alloc, rids, max_new_tokens=total, reserve_steps=total)
+    gd = torch.Generator(device=dev)
+    gd.manual_seed(1)
+    n_in = 4
+    qs = [torch.randn((SERVE_B, H, D), generator=gd, device=dev, dtype=torch.float16) for _ in range(n_in)]
+    ks = [torch.randn((SERVE_B, H, 1, D), generator=gd, device=dev, dtype=torch.float16) for _ in range(n_in)]
+    vs = [torch.randn((SERVE_B, H, 1, D), generator=gd, device=dev, dtype=torch.float16) for _ in range(n_in)]
+    for i in range(warmup):
+        batch.step(qs[i % n_in], ks[i % n_in], vs[i % n_in])
+    torch.cuda.synchronize()
+    len0 = list(batch.host_lengths)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        batch.step(qs[i % n_in], ks[i % n_in], vs[i % n_in])
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    _, stats = batch.attend(qs[0], return_stats=True)
+    # attention over lengths len0+1 .. len0+steps, averaged; the append reads and writes one
+    # K and one V page (int8 + scale + zero) per request and head and reads the new token
+    mean_len = [L + (steps + 1) / 2 for L in len0]
+    attn_bytes = algorithmic_bytes([round(L) for L in mean_len], H, D, PAGE)
+    append_bytes = 2 * SERVE_B * H * (2 * (PAGE * D + 6) + D * 2)
+    nbytes = attn_bytes + append_bytes
+    batch.close()
+    res = {
+        "workload": f"serving decode step: B{SERVE_B} ragged lengths ~U[{SERVE_LO},{SERVE_HI}] (seeded), H{H} D{D}, "
+                    f"{PAGE}-token pages in a shuffled pool, append one fp16 token per request + paged attention",
+        "sum_lengths": sum(len0), "us_per_step": round(ms * 1e3, 2),
+        "algorithmic_bytes_per_step": nbytes, "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "pct_of_peak": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
+        "num_splits": stats.get("num_splits"), "steps": steps, "warmup": warmup,
+    }
+    del batch, alloc
+    torch.cuda.empty_cache()
+    return res
+
+
 def load_traffic(config_key: str):
     if not PMC_SUMMARY.exists():
         return None
@@ -170,6 +226,10 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.mode == "copy":
         return copy_calibration(torch, args.steps)
+    if args.mode == "serving":
+        print(json.dumps({"mode": "serving", **serving_step_bench(torch, fa, dev, args.steps, args.warmup)}),
+              flush=True)
+        return 0
     sets = [make_inputs(torch, fa, dev, seed, args.layout) for seed in range(ROTATE)]
     torch.cuda.synchronize()
     lengths = [S] * B
@@ -250,6 +310,12 @@ def main() -> int:
         },
         "device": torch.cuda.get_device_name(dev),
     }
+    del sets
+    torch.cuda.empty_cache()
+    try:
+        result["serving_step"] = serving_step_bench(torch, fa, dev, steps=min(args.steps, 50), warmup=5)
+    except Exception as exc:  # reported, never hides the metric line
+        result["serving_step"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

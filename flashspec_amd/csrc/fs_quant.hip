@@ -116,6 +116,47 @@ update_pages_kernel(const int8_t* in_values, const float* in_scale, const int16_
   quantize_group(get, page, D, out_values + (size_t)og * page * D, out_scale + og, out_zero + og, lane);
 }
 
+struct PageStore {
+  int8_t* values;
+  float* scale;
+  int16_t* zero;
+};
+
+// One decode token per request (see fs_append_tokens_i8).  Group (kv, b, h): position
+// pos = lengths_in[b] lands in row pos % page of page table[b, pos / page]; the page is
+// dequantized (stale rows included), that row replaced, and the page requantized in place.
+template <typename XT, typename IT>
+__global__ void __launch_bounds__(256)
+append_tokens_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageStore vs, int64_t num_pages,
+                     const IT* table, int table_cols, const int64_t* lengths_in, int64_t* lengths_out, int B,
+                     int H, int page, int D) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int64_t rows = (int64_t)B * H;
+  if (grp >= 2 * rows) return;
+  const int kv = grp >= rows ? 1 : 0;
+  const int64_t bh = grp - kv * rows;
+  const int b = (int)(bh / H);
+  const int h = (int)(bh - (int64_t)b * H);
+  const int64_t pos = lengths_in[b];
+  const int64_t lp = pos >= 0 ? pos / page : -1;
+  const int64_t pg = (lp >= 0 && lp < table_cols) ? (int64_t)table[(size_t)b * table_cols + lp] : -1;
+  const bool ok = pg >= 0 && pg < num_pages;
+  if (kv == 0 && h == 0 && lane == 0) lengths_out[b] = ok ? pos + 1 : pos;
+  if (!ok) return;
+  const int off = (int)(pos - lp * page);
+  const PageStore st = kv ? vs : ks;
+  const XT* src = (kv ? v_new : k_new) + (size_t)bh * D;
+  const int64_t sidx = pg * H + h;
+  const int8_t* vals = st.values + (size_t)sidx * page * D;
+  auto get = [&](int r, int d) -> float {
+    if (r == off) return to_f32(src[d]);
+    const int u = (int)vals[(size_t)r * D + d] + 128;
+    return ((float)u - (float)st.zero[sidx]) * st.scale[sidx];
+  };
+  quantize_group(get, page, D, st.values + (size_t)sidx * page * D, st.scale + sidx, st.zero + sidx, lane);
+}
+
 template <typename OT>
 __global__ void __launch_bounds__(256)
 dequantize_kernel(const int8_t* values, const float* scale, const int16_t* zero, int64_t outer, int nb, int bs,
@@ -227,4 +268,41 @@ extern "C" int fs_update_pages_i8(const int8_t* in_values, const float* in_scale
     default: return set_error(FS_ERR_INVALID, "update_pages: dtype code must be 0, 1 or 2");
   }
   return check_launch("update_pages");
+}
+
+extern "C" int fs_append_tokens_i8(const void* k_new, const void* v_new, int src_dtype, int8_t* k_values,
+                                   float* k_scale, int16_t* k_zero, int8_t* v_values, float* v_scale,
+                                   int16_t* v_zero, int64_t num_pages, const void* block_table,
+                                   int table_index_bytes, int table_cols, const int64_t* lengths_in,
+                                   int64_t* lengths_out, int batch, int heads, int head_dim, int page_size,
+                                   void* stream) {
+  if (batch <= 0) return FS_OK;
+  if (heads <= 0 || head_dim <= 0 || page_size <= 0 || num_pages <= 0 || table_cols <= 0)
+    return set_error(FS_ERR_INVALID, "append_tokens: sizes must be positive");
+  if (table_index_bytes != 4 && table_index_bytes != 8)
+    return set_error(FS_ERR_INVALID, "append_tokens: block_table must be int32 or int64");
+  if (!k_new || !v_new || !k_values || !k_scale || !k_zero || !v_values || !v_scale || !v_zero || !block_table ||
+      !lengths_in || !lengths_out)
+    return set_error(FS_ERR_INVALID, "append_tokens: null pointer");
+  if (lengths_in == lengths_out)
+    return set_error(FS_ERR_INVALID, "append_tokens: lengths_in and lengths_out must be different buffers");
+  const PageStore ks{k_values, k_scale, k_zero}, vs{v_values, v_scale, v_zero};
+  const int64_t groups = 2LL * batch * heads;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+#define FS_APPEND(XT, IT)                                                                                       \
+  hipLaunchKernelGGL((append_tokens_kernel<XT, IT>), grid, block, 0, st, (const XT*)k_new, (const XT*)v_new, ks, \
+                     vs, num_pages, (const IT*)block_table, table_cols, lengths_in, lengths_out, batch, heads,   \
+                     page_size, head_dim)
+#define FS_APPEND_IDX(XT) \
+  if (table_index_bytes == 4) FS_APPEND(XT, int32_t); else FS_APPEND(XT, int64_t)
+  switch (src_dtype) {
+    case FS_F32: FS_APPEND_IDX(float); break;
+    case FS_F16: FS_APPEND_IDX(__half); break;
+    case FS_BF16: FS_APPEND_IDX(__hip_bfloat16); break;
+    default: return set_error(FS_ERR_INVALID, "append_tokens: dtype code must be 0, 1 or 2");
+  }
+#undef FS_APPEND_IDX
+#undef FS_APPEND
+  return check_launch("append_tokens");
 }

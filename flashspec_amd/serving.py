@@ -5,10 +5,11 @@ random-input draw order, timing points and result keys, with one change the
 reference's own design calls for: attention goes through
 ``paged_quant_attention_triton`` (the HIP kernel on GPU, the portable path on CPU)
 instead of the portable path only (serving.py:118,139 call ``paged_quant_attention``).
-The allocator's prompt writes and per-step appends run as batched HIP page-update
-launches on GPU.
+On GPU the prompt writes run as batched HIP page-update launches, and the decode loop
+keeps the block table and lengths on the device (``DecodeBatch``): one append launch
+and one attention launch per step, no per-step table rebuild on the host.
 
-``build_request_pool`` and ``decode_step`` are the serving-at-scale pieces: a
+``build_request_pool`` and ``DecodeBatch.step`` are the serving-at-scale pieces: a
 fragmented page pool of ragged requests, and one decode step that appends one token
 per request and then attends over the updated cache.
 
@@ -23,9 +24,12 @@ from dataclasses import dataclass
 from time import perf_counter
 from typing import Dict, Sequence
 
+import numpy as np
 import torch
 
-from .paged import PagedKVAllocator
+from . import _lib
+from .paged import PagedKVAllocator, PagedKVCache
+from .quant import QuantizedTensor, dequantize_int8_per_block, quantize_int8_per_block
 from .runtime import device_name, resolve_device, resolve_dtype, synchronize
 from .triton_paged import paged_quant_attention_triton
 
@@ -158,25 +162,40 @@ def run_decode_simulation(config: ServingConfig) -> Dict[str, float | int | str 
     decode_ms = 0.0
     generated_tokens = 0
     finishes = 0
-    for _step in range(config.decode_steps):
+    batch: DecodeBatch | None = None  # device-resident table and lengths while the active set is fixed
+    for step in range(config.decode_steps):
         if not active:
             break
         synchronize(device)
         t0 = perf_counter()
-        cache = allocator.to_cache(active)
+        if device.type == "cuda" and batch is None:
+            horizon = config.decode_steps - step
+            if config.request_life_steps > 0:
+                horizon = min(horizon, min(config.request_life_steps - generated[r] for r in active))
+            batch = DecodeBatch(allocator, active, max_new_tokens=horizon)
+        cache = batch.cache() if batch is not None else allocator.to_cache(active)
         q = torch.randn((len(active), config.heads, config.head_dim), generator=generator, device=device,
                         dtype=dtype)
         out = paged_quant_attention_triton(q, cache)
         next_k = out.unsqueeze(2).to(dtype=dtype)
         next_v = torch.tanh(out).unsqueeze(2).to(dtype=dtype)
-        allocator.append_batch(active, next_k, next_v)
+        if batch is not None:
+            batch.append(next_k, next_v)
+        else:
+            allocator.append_batch(active, next_k, next_v)
         synchronize(device)
         decode_ms += (perf_counter() - t0) * 1000.0
         for rid in active:
             generated[rid] += 1
         generated_tokens += len(active)
+        if batch is not None and batch.steps_done == batch.max_new_tokens:
+            batch.close()
+            batch = None
         if config.request_life_steps > 0:
             done = [rid for rid in active if generated[rid] >= config.request_life_steps]
+            if done and batch is not None:
+                batch.close()
+                batch = None
             for rid in done:
                 allocator.release_request(rid)
                 active.remove(rid)
@@ -184,6 +203,8 @@ def run_decode_simulation(config: ServingConfig) -> Dict[str, float | int | str 
                 finishes += 1
             for _ in done:
                 active.append(add_request(initial=False))
+    if batch is not None:
+        batch.close()
 
     stats = allocator.stats()
     return {
@@ -206,6 +227,170 @@ def run_decode_simulation(config: ServingConfig) -> Dict[str, float | int | str 
 
 
 # ---- serving at scale ----------------------------------------------------------------------------
+
+class DecodeBatch:
+    """Device-resident decode state for a fixed set of live requests of a ``PagedKVAllocator``.
+
+    The block table (int32) and the lengths stay on the device between steps.  ``append``
+    writes one token per request with a single ``fs_append_tokens_i8`` launch (K and V),
+    which reads each request's position from the device lengths and writes the advanced
+    lengths to a second buffer, so a decode step needs no host round trip.  ``attend`` runs
+    ``paged_quant_attention_triton`` over the current cache.
+
+    Page policy: pages are taken from the allocator's free list ``reserve_steps`` steps ahead,
+    step-major and in request order, the order in which the reference allocator takes them one
+    token at a time (paged.py:121-125), so the page ids are the same as step-by-step allocation
+    as long as nothing else allocates meanwhile.  ``close`` hands unused reserved pages back to
+    the front of the free list in the order they were taken, which restores the allocator's
+    state exactly.  While a batch is open, append to its requests only through it.
+    On CPU the same bookkeeping drives a portable torch append (dequantize page, replace row,
+    requantize), so the host logic is testable without a GPU.
+    """
+
+    def __init__(self, allocator: PagedKVAllocator, request_ids: Sequence[int], *, max_new_tokens: int,
+                 reserve_steps: int = 16) -> None:
+        if max_new_tokens < 0:
+            raise ValueError("max_new_tokens must be >= 0")
+        if reserve_steps <= 0:
+            raise ValueError("reserve_steps must be positive")
+        self.allocator = allocator
+        self.request_ids = [int(r) for r in request_ids]
+        if not self.request_ids:
+            raise ValueError("DecodeBatch needs at least one request")
+        if len(set(self.request_ids)) != len(self.request_ids):
+            raise ValueError("request_ids must be distinct")
+        self._requests = [allocator._get_request(r) for r in self.request_ids]
+        self.device = allocator.device
+        self.page = allocator.block_size
+        self.max_new_tokens = int(max_new_tokens)
+        self.reserve_steps = int(reserve_steps)
+        self.steps_done = 0
+        self._reserved_steps = 0
+        self._taken: list[int] = []  # pages reserved by this batch, in the order taken
+        self.host_lengths = [r.length for r in self._requests]
+        cols = max(1, max((L + self.max_new_tokens + self.page - 1) // self.page for L in self.host_lengths))
+        self._table_host = np.full((len(self._requests), cols), -1, dtype=np.int32)
+        for i, r in enumerate(self._requests):
+            self._table_host[i, : len(r.logical_blocks)] = r.logical_blocks
+        self._reserve(min(self.max_new_tokens, self.reserve_steps))
+        self.block_table = torch.empty((len(self._requests), cols), dtype=torch.int32, device=self.device)
+        self._upload_table()
+        lengths = torch.tensor(self.host_lengths, dtype=torch.int64)
+        self._lengths = [lengths.to(self.device), lengths.to(self.device).clone()]
+        self._cur = 0
+        self._open = True
+
+    # -- bookkeeping ----------------------------------------------------------------------
+    @property
+    def lengths(self) -> torch.Tensor:
+        return self._lengths[self._cur]
+
+    def _reserve(self, upto_step: int) -> None:
+        for s in range(self._reserved_steps, upto_step):
+            for i, r in enumerate(self._requests):
+                pos = self.host_lengths[i] + (s - self.steps_done)
+                lp = pos // self.page
+                if lp == len(r.logical_blocks):
+                    pg = self.allocator._allocate_block()
+                    r.logical_blocks.append(pg)
+                    self._taken.append(pg)
+                    self._table_host[i, lp] = pg
+        self._reserved_steps = max(self._reserved_steps, upto_step)
+
+    def _upload_table(self) -> None:
+        src = torch.from_numpy(self._table_host)
+        if self.device.type == "cuda":
+            self.block_table.copy_(src.pin_memory(), non_blocking=True)
+        else:
+            self.block_table.copy_(src)
+
+    def cache(self) -> PagedKVCache:
+        return PagedKVCache(k_quant=self.allocator.k_quant, v_quant=self.allocator.v_quant,
+                            block_table=self.block_table, lengths=self.lengths, block_size=self.page,
+                            max_seq_len=max(1, max(self.host_lengths)))
+
+    # -- decode ---------------------------------------------------------------------------
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """Append ``k_new``/``v_new`` ``[n, heads, 1, head_dim]`` (one token per request)."""
+
+        if not self._open:
+            raise RuntimeError("DecodeBatch is closed")
+        if self.steps_done >= self.max_new_tokens:
+            raise RuntimeError(f"DecodeBatch was opened for {self.max_new_tokens} new tokens")
+        n, a = len(self._requests), self.allocator
+        for t in (k_new, v_new):
+            if t.shape != (n, a.heads, 1, a.head_dim):
+                raise ValueError(f"expected new K/V of shape {(n, a.heads, 1, a.head_dim)}, got {tuple(t.shape)}")
+            if t.device != self.device:
+                raise ValueError("new K/V must be on the allocator's device")
+        if self.steps_done >= self._reserved_steps:
+            self._reserve(min(self.max_new_tokens, self.steps_done + self.reserve_steps))
+            self._upload_table()
+        nxt = 1 - self._cur
+        if self.device.type == "cuda":
+            self._append_hip(k_new, v_new, self._lengths[self._cur], self._lengths[nxt])
+        else:
+            self._append_portable(k_new, v_new)
+            self._lengths[nxt].copy_(self._lengths[self._cur] + 1)
+        self._cur = nxt
+        self.steps_done += 1
+        for i, r in enumerate(self._requests):
+            self.host_lengths[i] += 1
+            r.length += 1
+
+    def _append_hip(self, k_new, v_new, len_in, len_out) -> None:
+        lib = _lib.require()
+        if k_new.dtype != v_new.dtype:
+            raise ValueError("k_new and v_new must share a dtype")
+        k_c, v_c = k_new.contiguous(), v_new.contiguous()
+        ks, vs = self.allocator.k_quant, self.allocator.v_quant
+        _lib.check(lib.fs_append_tokens_i8(
+            k_c.data_ptr(), v_c.data_ptr(), _lib.dtype_code(k_c.dtype), ks.values.data_ptr(), ks.scale.data_ptr(),
+            ks.zero_point.data_ptr(), vs.values.data_ptr(), vs.scale.data_ptr(), vs.zero_point.data_ptr(),
+            int(ks.values.shape[0]), self.block_table.data_ptr(), 4, int(self.block_table.shape[1]),
+            len_in.data_ptr(), len_out.data_ptr(), len(self._requests), self.allocator.heads,
+            self.allocator.head_dim, self.page, _lib.stream_ptr(k_c.device)))
+
+    def _append_portable(self, k_new, v_new) -> None:
+        pos = torch.tensor(self.host_lengths, dtype=torch.int64)
+        pages = torch.from_numpy(self._table_host[np.arange(len(self._requests)), (pos // self.page).numpy()])
+        pages = pages.to(torch.int64)
+        rows = torch.arange(len(self._requests))
+        for store, src in ((self.allocator.k_quant, k_new), (self.allocator.v_quant, v_new)):
+            sub = QuantizedTensor(store.values[pages], store.scale[pages], store.zero_point[pages], self.page,
+                                  (len(pages), self.allocator.heads, self.page, self.allocator.head_dim))
+            block = dequantize_int8_per_block(sub, dtype=torch.float32)
+            block[rows, :, pos % self.page, :] = src[:, :, 0, :].to(torch.float32)
+            q = quantize_int8_per_block(block, block_size=self.page)
+            store.values[pages] = q.values
+            store.scale[pages] = q.scale
+            store.zero_point[pages] = q.zero_point
+
+    def attend(self, q: torch.Tensor, *, return_stats: bool = False):
+        """Paged INT8 decode attention of ``q [n, heads, head_dim]`` over the current cache."""
+
+        return paged_quant_attention_triton(q, self.cache(), return_stats=return_stats)
+
+    def step(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
+        """One serving decode step: append one token per request, then attend over the updated cache."""
+
+        self.append(k_new, v_new)
+        return self.attend(q)
+
+    def close(self) -> None:
+        """Return reserved pages that hold no token to the front of the free list, in taken order."""
+
+        if not self._open:
+            return
+        unused = []
+        for r in self._requests:
+            need = (r.length + self.page - 1) // self.page
+            unused.extend(r.logical_blocks[need:])
+            del r.logical_blocks[need:]
+        unused_set = set(unused)
+        self.allocator._free_blocks[:0] = [p for p in self._taken if p in unused_set]
+        self._open = False
+
 
 def build_request_pool(lengths: Sequence[int], *, heads: int, head_dim: int, block_size: int = 16,
                        headroom_tokens: int = 16, seed: int = 0, device: torch.device | str = "cuda",
@@ -233,18 +418,6 @@ def build_request_pool(lengths: Sequence[int], *, heads: int, head_dim: int, blo
         rids.append(rid)
         del k, v
     return alloc, rids
-
-
-def decode_step(allocator: PagedKVAllocator, request_ids: Sequence[int], q: torch.Tensor, k_new: torch.Tensor,
-                v_new: torch.Tensor) -> torch.Tensor:
-    """Append one token per request (one batched page-update launch per tensor), then attend.
-
-    ``q`` is ``[n, heads, head_dim]``; ``k_new``/``v_new`` are ``[n, heads, 1, head_dim]``.
-    Attention runs over the cache including the appended token.
-    """
-
-    allocator.append_batch(request_ids, k_new, v_new)
-    return paged_quant_attention_triton(q, allocator.to_cache(request_ids))
 
 
 def parse_args(argv=None) -> argparse.Namespace:

@@ -172,6 +172,23 @@ int fs_update_pages_i8(const int8_t* in_values, const float* in_scale, const int
                        const int32_t* row_src, const void* src, int src_dtype, int src_tokens,
                        int heads, int page_size, int head_dim, void* stream);
 
+/* One decode step's append, device-resident: for every request b, the token
+ * k_new/v_new[b] ([batch, heads, 1, head_dim], dtype src_dtype) goes to position
+ * pos = lengths_in[b], i.e. row pos % page_size of physical page block_table[b, pos / page_size];
+ * that page's [heads] groups are dequantized (stale rows included), the row is replaced and
+ * the page is requantized in place (quant block == page_size), for K and V in one launch.
+ * lengths_out[b] = pos + 1, or pos when the table entry is -1 / out of range (the token is
+ * then dropped and nothing is written).  lengths_in and lengths_out must differ; the caller
+ * fills the table entry of a page before the step that first writes it.
+ * Replaces PagedKVAllocator.append_batch for one token per request
+ * (reference src/flashspec/paged.py:108-144, with page reads at :226-245 and writes at :247-255). */
+int fs_append_tokens_i8(const void* k_new, const void* v_new, int src_dtype,
+                        int8_t* k_values, float* k_scale, int16_t* k_zero,
+                        int8_t* v_values, float* v_scale, int16_t* v_zero, int64_t num_pages,
+                        const void* block_table, int table_index_bytes, int table_cols,
+                        const int64_t* lengths_in, int64_t* lengths_out,
+                        int batch, int heads, int head_dim, int page_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

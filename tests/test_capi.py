@@ -67,3 +67,8 @@ def test_invalid_arguments_are_rejected_before_launch():
     # in-place page update with a different quant block
     rc = lib.fs_update_pages_i8(1, 1, 1, 4, 8, 1, 1, 1, None, None, 4, 1, 1, 0, 1, 2, 16, 64, None)
     assert rc == _lib.FS_ERR_INVALID and "in-place" in lib.fs_last_error().decode()
+    # append: the two lengths buffers must differ, and the table index width is 4 or 8 bytes
+    rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 4, 7, 7, 2, 2, 64, 16, None)
+    assert rc == _lib.FS_ERR_INVALID and "differ" in lib.fs_last_error().decode()
+    rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 2, 4, 7, 9, 2, 2, 64, 16, None)
+    assert rc == _lib.FS_ERR_INVALID and "int32 or int64" in lib.fs_last_error().decode()
