@@ -103,11 +103,38 @@ def build(resource_usage: bool = True, jobs: int = 4) -> Path:
     return lib
 
 
+def _demangle(names: list[str]) -> list[str]:
+    tool = shutil.which("llvm-cxxfilt") or shutil.which("c++filt") or "c++filt"
+    try:
+        out = subprocess.run([tool], input="\n".join(names), capture_output=True, text=True, check=True).stdout
+        return out.splitlines()
+    except (OSError, subprocess.CalledProcessError):
+        return names
+
+
+def resources_markdown() -> str:
+    """The register/LDS/occupancy table of ``kernel_resources.json`` as Markdown."""
+
+    data = json.loads(RESOURCES.read_text())
+    kernels = data["kernels"]
+    names = _demangle([k["kernel"] for k in kernels])
+    lines = [f"| kernel ({data['arch']}) | VGPRs | AGPRs | SGPRs | scratch B/lane | LDS B/block | waves/SIMD |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for k, name in zip(kernels, names):
+        lines.append(f"| `{name.replace('fs::DecodeParams', 'DecodeParams')}` | {k.get('vgprs')} | {k.get('agprs')} | "
+                     f"{k.get('totalsgprs')} | {k.get('scratchsize')} | {k.get('lds size')} | {k.get('occupancy')} |")
+    return "\n".join(lines) + "\n"
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--no-resource-usage", action="store_true", help="skip the register/occupancy table")
+    ap.add_argument("--print-resources", action="store_true", help="print the last table as Markdown and exit")
     ap.add_argument("-j", "--jobs", type=int, default=4)
     args = ap.parse_args()
+    if args.print_resources:
+        print(resources_markdown(), end="")
+        return
     print(build(resource_usage=not args.no_resource_usage, jobs=args.jobs))
 
 

@@ -13,13 +13,14 @@ from __future__ import annotations
 import sys
 
 import flashspec_amd
-from flashspec_amd import attention, paged, quant, runtime, triton_fused, triton_paged, triton_utils
+from flashspec_amd import attention, paged, quant, runtime, serving, triton_fused, triton_paged, triton_utils
 
 _SUBMODULES = {
     "attention": attention,
     "paged": paged,
     "quant": quant,
     "runtime": runtime,
+    "serving": serving,
     "triton_fused": triton_fused,
     "triton_paged": triton_paged,
     "triton_utils": triton_utils,
