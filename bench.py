@@ -195,6 +195,22 @@ def serving_step_bench(torch, fa, dev, steps: int, warmup: int) -> dict:
     return res
 
 
+def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
+    """quantize_int8_per_block of one fp16 K tensor of the metric workload ([8, 32, 4096, 128],
+    16-token blocks), input resident in HBM; bytes = fp16 read + int8 write + scale/zero write."""
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    xs = [torch.randn((B, H, S, D), generator=g, device=dev, dtype=torch.float16) for _ in range(2)]
+    ms = time_loop(torch, lambda i: fa.quantize_int8_per_block(xs[i % 2], PAGE), calls, 3)
+    groups = B * H * (S // PAGE)
+    nbytes = B * H * S * D * (2 + 1) + groups * 6
+    del xs
+    return {"workload": f"quantize_int8_per_block fp16 [{B}, {H}, {S}, {D}], block {PAGE}",
+            "us_per_call": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+            "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1)}
+
+
 def load_traffic(config_key: str):
     if not PMC_SUMMARY.exists():
         return None
@@ -311,6 +327,11 @@ def main() -> int:
         "device": torch.cuda.get_device_name(dev),
     }
     del sets
+    torch.cuda.empty_cache()
+    try:
+        result["quantize"] = quantize_bench(torch, fa, dev)
+    except Exception as exc:  # reported, never hides the metric line
+        result["quantize"] = {"error": f"{type(exc).__name__}: {exc}"}
     torch.cuda.empty_cache()
     try:
         result["serving_step"] = serving_step_bench(torch, fa, dev, steps=min(args.steps, 50), warmup=5)

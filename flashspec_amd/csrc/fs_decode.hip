@@ -27,6 +27,7 @@ namespace fs {
 constexpr int kMaxWaves = 16;       // waves per workgroup on the tiled path
 constexpr int kMaxTilesPerWave = 64;  // per split and wave: one metadata lane per tile
 constexpr float kRescaleSlack = 8.0f;  // running max may lag the true max by 2^8
+constexpr int kXcds = 8;  // MI355X: accelerator complex dies, each with its own L2
 
 struct DecodeParams {
   const void* q;
@@ -49,6 +50,39 @@ struct DecodeParams {
   int split_tiles, max_splits;
   float qk_scale;  // sm_scale * log2(e)
 };
+
+// The dispatcher hands workgroups to the XCDs round-robin (workgroup i to XCD i % 8).
+// decode_unit renumbers them so that XCD x owns heads [x*H/8, (x+1)*H/8) of every batch
+// (all their splits): an XCD then streams an H/8-head slab of each page instead of one
+// 2 KiB head slice of every page, while every XCD still gets the same share of each
+// request, so ragged lengths stay balanced across XCDs.  Measured on one MI355X against the
+// plain order: B8 H32 S4096 paged 46.1 vs 46.9 us, 64 ragged requests 616 vs 624 us.
+// Giving each XCD whole batches instead is as fast on uniform lengths but 1.35x slower
+// when lengths descend across the batch.  Heads not divisible by 8 keep the plain order.
+__device__ __forceinline__ int xcd_chunked_unit(int bid, int units) {
+  const int per = units / kXcds, rem = units - per * kXcds;
+  const int x = bid % kXcds, k = bid / kXcds;
+  return x * per + min(x, rem) + k;
+}
+
+struct Unit {
+  int row, split;
+};
+
+__device__ __forceinline__ Unit decode_unit(const DecodeParams& p, int bid, int units) {
+  // pos = ((x * batch + b) * hg + hh) * max_splits + split with head h = x * hg + hh; with
+  // hg = heads (heads not divisible by 8) the same formula is the plain order, x = 0.
+  const bool grouped = p.heads % kXcds == 0;
+  const int hg = grouped ? p.heads / kXcds : p.heads;
+  const int pos = grouped ? xcd_chunked_unit(bid, units) : bid;
+  const int batch = p.rows / p.heads;
+  const int split = pos % p.max_splits;
+  int t = pos / p.max_splits;
+  const int hh = t % hg;
+  t /= hg;
+  const int b = t % batch, x = t / batch;
+  return {b * p.heads + x * hg + hh, split};
+}
 
 __device__ __forceinline__ int row_length(const int64_t* lengths, int b, int seq_len) {
   if (lengths == nullptr) return seq_len;
@@ -269,8 +303,8 @@ decode_rows_kernel(const DecodeParams p) {
   // from it (tile counts, tile offsets, load base addresses) in scalar registers
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int W = blockDim.x / kWave;
-  const int row = blockIdx.x / p.max_splits;
-  const int split = blockIdx.x - row * p.max_splits;
+  const Unit unit = decode_unit(p, blockIdx.x, gridDim.x);
+  const int row = unit.row, split = unit.split;
   const int b = row / p.heads;
   const int h = row - b * p.heads;
   // Lane k of wave w resolves the wave's k-th tile, first + W*k, once: base index (-1 = not

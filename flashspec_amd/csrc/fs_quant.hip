@@ -42,6 +42,121 @@ __device__ __forceinline__ void quantize_group(const Get& get, int rows, int D, 
   }
 }
 
+// ---- vectorized group quantizer --------------------------------------------------------------
+// Same arithmetic as quantize_group, for a group of `rows` contiguous source rows of D values
+// with rows*D = CH*512 and D % 8 == 0: lane l holds values [c*512 + 8l, c*512 + 8l + 8) of
+// every chunk c in registers, read once from HBM with 16-byte loads (non-temporal: the source
+// is read exactly once) and written back as 8-byte packed int8 stores.
+
+typedef uint32_t q_u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ q_u32x4_t nt_load16(const void* p) {
+  return __builtin_nontemporal_load((const q_u32x4_t*)p);
+}
+
+__device__ __forceinline__ void load8(const float* p, float* f) {
+  const q_u32x4_t a = nt_load16(p), b = nt_load16(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = __uint_as_float(a[i]);
+    f[4 + i] = __uint_as_float(b[i]);
+  }
+}
+
+__device__ __forceinline__ void load8(const __half* p, float* f) {
+  const q_u32x4_t a = nt_load16(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __half2float(__ushort_as_half((unsigned short)(a[i] & 0xffffu)));
+    f[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(a[i] >> 16)));
+  }
+}
+
+__device__ __forceinline__ void load8(const __hip_bfloat16* p, float* f) {
+  const q_u32x4_t a = nt_load16(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(a[i] << 16);
+    f[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+  }
+}
+
+template <int CH, typename XT>
+__device__ __forceinline__ void quantize_group_vec(const XT* src, int valid_rows, int D, int8_t* dst,
+                                                   float* scale_out, int16_t* zero_out, int lane) {
+  float x[CH][8];
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int e = c * 512 + lane * 8;
+    if (e / D < valid_rows) {
+      load8(src + e, x[c]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      mn = fminf(mn, x[c][i]);
+      mx = fmaxf(mx, x[c][i]);
+    }
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
+  const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float qv = fminf(fmaxf(__builtin_rintf(x[c][i] / scale + zero), 0.0f), 255.0f);
+      w[i / 4] |= (((uint32_t)(int)qv) ^ 0x80u) << (8 * (i % 4));  // q - 128 as a byte
+    }
+    *(uint2*)(dst + c * 512 + lane * 8) = make_uint2(w[0], w[1]);
+  }
+  if (lane == 0) {
+    *scale_out = scale;
+    *zero_out = (int16_t)zero;
+  }
+}
+
+// Chunks of 512 values per group when the vectorized quantizer applies, else 0.
+__host__ __device__ constexpr int vec_chunks(int rows, int D) {
+  return (D % 8 == 0 && (rows * D) % 512 == 0 && rows * D / 512 <= 8) ? rows * D / 512 : 0;
+}
+
+// x [outer, S, D] -> values [outer, nb, bs, D]; one wave per group (o, block), vectorized.
+template <int CH, typename XT>
+__global__ void __launch_bounds__(256)
+quantize_blocks_vec_kernel(const XT* x, int64_t outer, int S, int D, int bs, int nb, int8_t* values, float* scale,
+                           int16_t* zero) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (grp >= outer * nb) return;
+  const int64_t o = grp / nb;
+  const int blk = (int)(grp - o * nb);
+  const XT* src = x + ((size_t)o * S + (size_t)blk * bs) * D;
+  quantize_group_vec<CH>(src, S - blk * bs, D, values + (size_t)grp * bs * D, scale + grp, zero + grp, lane);
+}
+
+// dense [B, H, S, D] -> page store [P, H, page, D], vectorized (see quantize_pages_kernel).
+template <int CH, typename XT>
+__global__ void __launch_bounds__(256)
+quantize_pages_vec_kernel(const XT* x, int H, int S, int D, int page, int nbps, const int64_t* page_src, int64_t P,
+                          int8_t* values, float* scale, int16_t* zero) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (grp >= P * H) return;
+  const int64_t j = grp / H;
+  const int h = (int)(grp - j * H);
+  const int64_t o = page_src ? page_src[j] : j;
+  const int64_t b = o / nbps;
+  const int lb = (int)(o - b * nbps);
+  const XT* src = x + (((size_t)(b * H + h) * S) + (size_t)lb * page) * D;
+  quantize_group_vec<CH>(src, S - lb * page, D, values + (size_t)grp * page * D, scale + grp, zero + grp, lane);
+}
+
 // x [outer, S, D] -> values [outer, nb, bs, D]; group = (o, block); rows past S read as 0.
 template <typename XT>
 __global__ void __launch_bounds__(256)
@@ -177,6 +292,34 @@ dequantize_kernel(const int8_t* values, const float* scale, const int16_t* zero,
 
 static dim3 wave_grid(int64_t groups) { return dim3((unsigned)((groups + 3) / 4)); }
 
+static bool is_pow2_chunks(int ch) { return ch == 1 || ch == 2 || ch == 4 || ch == 8; }
+
+template <typename XT>
+static int launch_vec_blocks(int ch, dim3 grid, hipStream_t st, const XT* x, int64_t outer, int S, int D, int bs,
+                             int nb, int8_t* values, float* scale, int16_t* zero) {
+  const dim3 block(256);
+  switch (ch) {
+    case 1: hipLaunchKernelGGL((quantize_blocks_vec_kernel<1, XT>), grid, block, 0, st, x, outer, S, D, bs, nb, values, scale, zero); break;
+    case 2: hipLaunchKernelGGL((quantize_blocks_vec_kernel<2, XT>), grid, block, 0, st, x, outer, S, D, bs, nb, values, scale, zero); break;
+    case 4: hipLaunchKernelGGL((quantize_blocks_vec_kernel<4, XT>), grid, block, 0, st, x, outer, S, D, bs, nb, values, scale, zero); break;
+    default: hipLaunchKernelGGL((quantize_blocks_vec_kernel<8, XT>), grid, block, 0, st, x, outer, S, D, bs, nb, values, scale, zero); break;
+  }
+  return check_launch("quantize_int8_per_block");
+}
+
+template <typename XT>
+static int launch_vec_pages(int ch, dim3 grid, hipStream_t st, const XT* x, int H, int S, int D, int page, int nbps,
+                            const int64_t* page_src, int64_t P, int8_t* values, float* scale, int16_t* zero) {
+  const dim3 block(256);
+  switch (ch) {
+    case 1: hipLaunchKernelGGL((quantize_pages_vec_kernel<1, XT>), grid, block, 0, st, x, H, S, D, page, nbps, page_src, P, values, scale, zero); break;
+    case 2: hipLaunchKernelGGL((quantize_pages_vec_kernel<2, XT>), grid, block, 0, st, x, H, S, D, page, nbps, page_src, P, values, scale, zero); break;
+    case 4: hipLaunchKernelGGL((quantize_pages_vec_kernel<4, XT>), grid, block, 0, st, x, H, S, D, page, nbps, page_src, P, values, scale, zero); break;
+    default: hipLaunchKernelGGL((quantize_pages_vec_kernel<8, XT>), grid, block, 0, st, x, H, S, D, page, nbps, page_src, P, values, scale, zero); break;
+  }
+  return check_launch("quantize_pages");
+}
+
 }  // namespace fs
 
 using namespace fs;
@@ -191,6 +334,15 @@ extern "C" int fs_quantize_i8(const void* x, int x_dtype, int64_t outer, int seq
   if ((groups + 3) / 4 > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "quantize: too many groups");
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid = wave_grid(groups), block(256);
+  const int ch = vec_chunks(block_size, head_dim);
+  if (is_pow2_chunks(ch) && ((uintptr_t)x % 16) == 0 && ((uintptr_t)values % 8) == 0) {
+    switch (x_dtype) {
+      case FS_F32: return launch_vec_blocks<float>(ch, grid, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
+      case FS_F16: return launch_vec_blocks<__half>(ch, grid, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
+      case FS_BF16: return launch_vec_blocks<__hip_bfloat16>(ch, grid, st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
+      default: return set_error(FS_ERR_INVALID, "quantize: dtype code must be 0, 1 or 2");
+    }
+  }
   switch (x_dtype) {
     case FS_F32: hipLaunchKernelGGL(quantize_blocks_kernel<float>, grid, block, 0, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
     case FS_F16: hipLaunchKernelGGL(quantize_blocks_kernel<__half>, grid, block, 0, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
@@ -234,6 +386,15 @@ extern "C" int fs_quantize_pages_i8(const void* x, int x_dtype, int batch, int h
   const int64_t groups = num_pages * heads;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid = wave_grid(groups), block(256);
+  const int ch = vec_chunks(page_size, head_dim);
+  if (is_pow2_chunks(ch) && ((uintptr_t)x % 16) == 0 && ((uintptr_t)values % 8) == 0) {
+    switch (x_dtype) {
+      case FS_F32: return launch_vec_pages<float>(ch, grid, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
+      case FS_F16: return launch_vec_pages<__half>(ch, grid, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
+      case FS_BF16: return launch_vec_pages<__hip_bfloat16>(ch, grid, st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
+      default: return set_error(FS_ERR_INVALID, "quantize_pages: dtype code must be 0, 1 or 2");
+    }
+  }
   switch (x_dtype) {
     case FS_F32: hipLaunchKernelGGL(quantize_pages_kernel<float>, grid, block, 0, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;
     case FS_F16: hipLaunchKernelGGL(quantize_pages_kernel<__half>, grid, block, 0, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;

@@ -80,6 +80,9 @@ def test_quantize_matches_reference_golden_vectors_bit_exact():
     ((2, 4, 50, 64), 16, torch.bfloat16),
     ((3, 1, 16, 256), 32, torch.float16),
     ((5, 7, 24), 4, torch.float32),
+    ((2, 3, 40, 32), 16, torch.float32),
+    ((1, 2, 33, 256), 16, torch.float32),
+    ((2, 2, 20, 128), 32, torch.bfloat16),
 ])
 def test_quantize_bit_exact_against_oracle(shape, bs, dtype):
     announce(f"quantize shape={shape} bs={bs} dtype={dtype}")
@@ -93,6 +96,28 @@ def test_quantize_bit_exact_against_oracle(shape, bs, dtype):
     half = fa.dequantize_int8_per_block(q, dtype=torch.float16)
     assert half.dtype == torch.float16
     assert torch.equal(half.cpu(), torch.from_numpy(oq.dequantize_int8_per_block(ref)).to(torch.float16))
+
+
+def test_quantize_unaligned_source_bit_exact():
+    """A source pointer that is not 16-byte aligned takes the element-wise kernel."""
+
+    announce("quantize via C ABI from a 2-byte-offset fp16 source")
+    S, D, bs = 37, 128, 16
+    base = randn((2 * S * D + 1,), seed=5)
+    x = base[1:].reshape(2, S, D)
+    xd = base.to(DEV)
+    nb = -(-S // bs)
+    values = torch.empty((2, nb, bs, D), dtype=torch.int8, device=DEV)
+    scale = torch.empty((2, nb), dtype=torch.float32, device=DEV)
+    zero = torch.empty((2, nb), dtype=torch.int16, device=DEV)
+    lib = _lib.require()
+    _lib.check(lib.fs_quantize_i8(xd.data_ptr() + 2, _lib.dtype_code(torch.float16), 2, S, D, bs, values.data_ptr(),
+                                  scale.data_ptr(), zero.data_ptr(), _lib.stream_ptr(DEV)))
+    sync()
+    ref = oq.quantize_int8_per_block(np_of(x.float()), bs)
+    assert np.array_equal(np_of(values), ref.values)
+    assert np.array_equal(np_of(scale).view(np.uint32), ref.scale.reshape(2, nb).view(np.uint32))
+    assert np.array_equal(np_of(zero), ref.zero_point.reshape(2, nb))
 
 
 # ---- paged cache construction, append, allocator ----------------------------------------------
