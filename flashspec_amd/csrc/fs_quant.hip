@@ -81,6 +81,37 @@ __device__ __forceinline__ void load8(const __hip_bfloat16* p, float* f) {
   }
 }
 
+// x / scale correctly rounded, from rcp = RN(1 / scale) and one FMA correction step
+// (Markstein's theorem: with rcp correctly rounded and q0 = RN(x * rcp) within one ulp,
+// r = x - q0 * scale is exact and RN(q0 + r * rcp) = RN(x / scale)).  A brute-force check
+// over every fp16 input and random fp32 inputs against IEEE division (tests/cdiv) finds no
+// difference except the sign of a zero quotient, which `+ zero` erases.  Valid while
+// x * rcp stays finite; the caller checks that once per group.
+__device__ __forceinline__ float div_by_scale(float x, float scale, float rcp) {
+  const float q0 = x * rcp;
+  const float r = __builtin_fmaf(-q0, scale, x);
+  return __builtin_fmaf(r, rcp, q0);
+}
+
+// Quantize CH chunks of 8 values held by this lane and store them as packed bytes.
+template <int CH, bool RCP>
+__device__ __forceinline__ void store_chunks(const float (&x)[CH][8], float scale, float rcp, float zero,
+                                             int8_t* dst, int lane) {
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float qd = RCP ? div_by_scale(x[c][i], scale, rcp) : x[c][i] / scale;
+      const float qv = fminf(fmaxf(__builtin_rintf(qd + zero), 0.0f), 255.0f);
+      // qv is an integer in [0, 255]: the byte conversion is exact
+      w[i / 4] = __builtin_amdgcn_cvt_pk_u8_f32(qv, i % 4, w[i / 4]);
+    }
+    // stored as q - 128: flip the top bit of every byte
+    *(uint2*)(dst + c * 512 + lane * 8) = make_uint2(w[0] ^ 0x80808080u, w[1] ^ 0x80808080u);
+  }
+}
+
 template <int CH, typename XT>
 __device__ __forceinline__ void quantize_group_vec(const XT* src, int valid_rows, int D, int8_t* dst,
                                                    float* scale_out, int16_t* zero_out, int lane) {
@@ -105,16 +136,13 @@ __device__ __forceinline__ void quantize_group_vec(const XT* src, int valid_rows
   mx = wave_max(mx);
   const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
   const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    uint32_t w[2] = {0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float qv = fminf(fmaxf(__builtin_rintf(x[c][i] / scale + zero), 0.0f), 255.0f);
-      w[i / 4] |= (((uint32_t)(int)qv) ^ 0x80u) << (8 * (i % 4));  // q - 128 as a byte
-    }
-    *(uint2*)(dst + c * 512 + lane * 8) = make_uint2(w[0], w[1]);
-  }
+  const float rcp = 1.0f / scale;  // correctly rounded
+  // |x| <= max(|mn|, |mx|) for every value of the group, and rounding is monotonic: if the
+  // largest product is finite, all are (wave-uniform test)
+  if (__builtin_isfinite(fmaxf(fabsf(mn), fabsf(mx)) * rcp))
+    store_chunks<CH, true>(x, scale, rcp, zero, dst, lane);
+  else
+    store_chunks<CH, false>(x, scale, rcp, zero, dst, lane);
   if (lane == 0) {
     *scale_out = scale;
     *zero_out = (int16_t)zero;
