@@ -300,6 +300,77 @@ append_tokens_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageStore v
   quantize_group(get, page, D, st.values + (size_t)sidx * page * D, st.scale + sidx, st.zero + sidx, lane);
 }
 
+// Vectorized append_tokens_kernel for page * D = CH * 512, D % 8 == 0: the page is read once
+// into registers (8 bytes per lane and chunk), the new row comes straight from the token, and
+// the requantized page is written back with the register-resident quantizer.  block_table
+// entries are int32 (table_bytes 4) or int64.
+template <int CH, typename XT>
+__global__ void __launch_bounds__(256)
+append_tokens_vec_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageStore vs, int64_t num_pages,
+                         const void* table, int table_bytes, int table_cols, const int64_t* lengths_in,
+                         int64_t* lengths_out, int B, int H, int page, int D) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int64_t rows = (int64_t)B * H;
+  if (grp >= 2 * rows) return;
+  const int kv = grp >= rows ? 1 : 0;
+  const int64_t bh = grp - kv * rows;
+  const int b = (int)(bh / H);
+  const int h = (int)(bh - (int64_t)b * H);
+  const int64_t pos = lengths_in[b];
+  const int64_t lp = pos >= 0 ? pos / page : -1;
+  int64_t pg = -1;
+  if (lp >= 0 && lp < table_cols) {
+    const size_t ti = (size_t)b * table_cols + lp;
+    pg = table_bytes == 4 ? (int64_t)((const int32_t*)table)[ti] : ((const int64_t*)table)[ti];
+  }
+  const bool ok = pg >= 0 && pg < num_pages;
+  if (kv == 0 && h == 0 && lane == 0) lengths_out[b] = ok ? pos + 1 : pos;
+  if (!ok) return;
+  const int off = (int)(pos - lp * page);
+  const PageStore st = kv ? vs : ks;
+  const XT* src = (kv ? v_new : k_new) + (size_t)bh * D;
+  const int64_t sidx = pg * H + h;
+  int8_t* vals = st.values + (size_t)sidx * page * D;
+  const float s_old = st.scale[sidx], z_old = (float)st.zero[sidx];
+  float x[CH][8];
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int e = c * 512 + lane * 8;
+    const int r = e / D;
+    if (r == off) {
+      load8(src + (e - r * D), x[c]);
+    } else {
+      const uint2 raw = *(const uint2*)(vals + e);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t wv = i < 4 ? raw.x : raw.y;
+        const int u = (int)((wv >> (8 * (i % 4))) & 0xffu) ^ 0x80;  // stored int8 + 128
+        x[c][i] = ((float)u - z_old) * s_old;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      mn = fminf(mn, x[c][i]);
+      mx = fmaxf(mx, x[c][i]);
+    }
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
+  const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
+  const float rcp = 1.0f / scale;
+  if (__builtin_isfinite(fmaxf(fabsf(mn), fabsf(mx)) * rcp))
+    store_chunks<CH, true>(x, scale, rcp, zero, vals, lane);
+  else
+    store_chunks<CH, false>(x, scale, rcp, zero, vals, lane);
+  if (lane == 0) {
+    st.scale[sidx] = scale;
+    st.zero[sidx] = (int16_t)zero;
+  }
+}
+
 template <typename OT>
 __global__ void __launch_bounds__(256)
 dequantize_kernel(const int8_t* values, const float* scale, const int16_t* zero, int64_t outer, int nb, int bs,
@@ -333,6 +404,20 @@ static int launch_vec_blocks(int ch, dim3 grid, hipStream_t st, const XT* x, int
     default: hipLaunchKernelGGL((quantize_blocks_vec_kernel<8, XT>), grid, block, 0, st, x, outer, S, D, bs, nb, values, scale, zero); break;
   }
   return check_launch("quantize_int8_per_block");
+}
+
+template <typename XT>
+static int launch_vec_append(int ch, dim3 grid, hipStream_t st, const XT* k_new, const XT* v_new, PageStore ks,
+                             PageStore vs, int64_t num_pages, const void* table, int table_bytes, int table_cols,
+                             const int64_t* lengths_in, int64_t* lengths_out, int B, int H, int page, int D) {
+  const dim3 block(256);
+  switch (ch) {
+    case 1: hipLaunchKernelGGL((append_tokens_vec_kernel<1, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
+    case 2: hipLaunchKernelGGL((append_tokens_vec_kernel<2, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
+    case 4: hipLaunchKernelGGL((append_tokens_vec_kernel<4, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
+    default: hipLaunchKernelGGL((append_tokens_vec_kernel<8, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
+  }
+  return check_launch("append_tokens");
 }
 
 template <typename XT>
@@ -479,6 +564,16 @@ extern "C" int fs_append_tokens_i8(const void* k_new, const void* v_new, int src
   const int64_t groups = 2LL * batch * heads;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid = wave_grid(groups), block(256);
+  const int ch = vec_chunks(page_size, head_dim);
+  if (is_pow2_chunks(ch) && ((uintptr_t)k_new % 16) == 0 && ((uintptr_t)v_new % 16) == 0 &&
+      ((uintptr_t)k_values % 8) == 0 && ((uintptr_t)v_values % 8) == 0) {
+    switch (src_dtype) {
+      case FS_F32: return launch_vec_append<float>(ch, grid, st, (const float*)k_new, (const float*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, batch, heads, page_size, head_dim);
+      case FS_F16: return launch_vec_append<__half>(ch, grid, st, (const __half*)k_new, (const __half*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, batch, heads, page_size, head_dim);
+      case FS_BF16: return launch_vec_append<__hip_bfloat16>(ch, grid, st, (const __hip_bfloat16*)k_new, (const __hip_bfloat16*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, batch, heads, page_size, head_dim);
+      default: return set_error(FS_ERR_INVALID, "append_tokens: dtype code must be 0, 1 or 2");
+    }
+  }
 #define FS_APPEND(XT, IT)                                                                                       \
   hipLaunchKernelGGL((append_tokens_kernel<XT, IT>), grid, block, 0, st, (const XT*)k_new, (const XT*)v_new, ks, \
                      vs, num_pages, (const IT*)block_table, table_cols, lengths_in, lengths_out, batch, heads,   \

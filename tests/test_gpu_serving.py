@@ -51,9 +51,12 @@ def _assert_stores_equal(alloc, ora, what):
         assert np.array_equal(got.zero_point, ref.zero_point), f"{what}: {name} zero point"
 
 
-@pytest.mark.parametrize("src_dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_decode_batch_bit_exact_against_oracle_allocator(src_dtype):
-    H, D, bs, cap = 4, 128, 16, 96
+@pytest.mark.parametrize("src_dtype,D", [(torch.float16, 128), (torch.bfloat16, 128), (torch.float32, 128),
+                                         (torch.float16, 48), (torch.float32, 64)])
+def test_decode_batch_bit_exact_against_oracle_allocator(src_dtype, D):
+    """D 128 and 64 take the register-resident append kernel, D 48 the element-wise one."""
+
+    H, bs, cap = 4, 16, 96
     announce(f"decode batch H{H} D{D} page{bs} src {src_dtype}")
     alloc = fa.PagedKVAllocator(capacity_blocks=cap, heads=H, head_dim=D, block_size=bs, device=DEV,
                                 dtype=torch.float16)
