@@ -34,10 +34,12 @@ ROTATE = 3
 PMC_SUMMARY = ROOT / "profiles" / "paged_decode_b8h32s4096d128_pmc.json"
 
 
-def algorithmic_bytes(lengths, heads: int, head_dim: int, page: int, q_bytes: int = 2, idx_bytes: int = 8) -> int:
+def algorithmic_bytes(lengths, heads: int, head_dim: int, page: int, q_bytes: int = 2, idx_bytes: int = 8,
+                      quant_block: int | None = None) -> int:
     pages = sum(math.ceil(L / page) for L in lengths)
+    blocks = sum(math.ceil(L / (quant_block or page)) for L in lengths)
     kv = 2 * sum(lengths) * heads * head_dim
-    params = 2 * pages * heads * (4 + 2)
+    params = 2 * blocks * heads * (4 + 2)
     table = pages * idx_bytes
     return kv + params + table + 8 * len(lengths) + 2 * len(lengths) * heads * head_dim * q_bytes
 
@@ -49,10 +51,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--layout", default="contiguous", choices=["contiguous", "shuffled", "interleaved"])
-    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "serving"],
+    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "serving", "shapes"],
                     help="full: the JSON line; paged: only the timed paged steps (for rocprofv3); "
                          "copy: a plain 256 MiB device copy, to calibrate rocprofv3 byte counters; "
-                         "serving: only the 64-request serving decode step")
+                         "serving: only the 64-request serving decode step; shapes: the SHAPES table")
     return ap.parse_args()
 
 
@@ -211,6 +213,91 @@ def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
             "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1)}
 
 
+# Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths)
+SHAPES = [
+    ("metric", 8, 32, 4096, 128, 16, 16, "float16", None),
+    ("c3_s2048", 8, 32, 2048, 128, 16, 16, "float16", None),
+    ("c4_descending_tail", 16, 32, 4096, 128, 16, 16, "float16", [4096 - 256 * i - 7 for i in range(16)]),
+    ("head_dim_64", 8, 32, 4096, 64, 16, 16, "float16", None),
+    ("head_dim_256", 8, 32, 4096, 256, 16, 16, "float16", None),
+    ("page_32_quant_16", 8, 32, 4096, 128, 32, 16, "float16", None),
+    ("q_bfloat16", 8, 32, 4096, 128, 16, 16, "bfloat16", None),
+    ("q_float32", 8, 32, 4096, 128, 16, 16, "float32", None),
+    ("block_32", 8, 32, 4096, 128, 32, 32, "float16", None),
+    ("page_64_quant_32", 8, 32, 4096, 128, 64, 32, "float16", None),
+    ("head_dim_96", 8, 32, 4096, 96, 16, 16, "float16", None),
+    ("head_dim_192", 8, 32, 4096, 192, 16, 16, "float16", None),
+    ("block_8", 8, 32, 4096, 128, 8, 8, "float16", None),
+    ("page_16_quant_8", 8, 32, 4096, 128, 16, 8, "float16", None),
+    ("head_dim_40_generic", 8, 32, 4096, 40, 16, 16, "float16", None),
+    ("batch_1_splitk", 1, 32, 16384, 128, 16, 16, "float16", None),
+]
+
+
+def paged_from_blocks(torch, fa, k, v, page: int, qb: int, lengths):
+    """Contiguous-layout page store whose pages hold page // qb quant blocks (page != quant block):
+    physical page b * pages_per_seq + j = logical page j of request b."""
+
+    b, h, s, d = k.shape
+    nbps = (s + page - 1) // page
+    per = page // qb
+
+    def pages(x):
+        xq = fa.quantize_int8_per_block(torch.nn.functional.pad(x, (0, 0, 0, nbps * page - s)), qb)
+        vals = xq.values.reshape(b, h, nbps, per, qb, d).permute(0, 2, 1, 3, 4, 5).reshape(b * nbps, h, per, qb, d)
+        sc = xq.scale.reshape(b, h, nbps, per).permute(0, 2, 1, 3).reshape(b * nbps, h, per, 1, 1)
+        zp = xq.zero_point.reshape(b, h, nbps, per).permute(0, 2, 1, 3).reshape(b * nbps, h, per, 1, 1)
+        return fa.QuantizedTensor(vals.contiguous(), sc.contiguous(), zp.contiguous(), qb, (b * nbps, h, page, d))
+
+    table = torch.arange(b * nbps, dtype=torch.int64, device=k.device).reshape(b, nbps)
+    lens = lengths if lengths is not None else torch.full((b,), s, dtype=torch.int64, device=k.device)
+    return fa.PagedKVCache(k_quant=pages(k), v_quant=pages(v), block_table=table, lengths=lens, block_size=page,
+                           max_seq_len=s)
+
+
+def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
+    """Paged and contiguous decode over the SHAPES table, 3 rotated input sets each; prints one
+    JSON object per shape."""
+
+    out = []
+    for name, b, h, s, d, page, qb, qdt, lens in SHAPES:
+        g = torch.Generator(device=dev)
+        g.manual_seed(11)
+        qdtype = getattr(torch, qdt)
+        sets = []
+        for _ in range(ROTATE):
+            q = torch.randn((b, h, d), generator=g, device=dev, dtype=torch.float16).to(qdtype)
+            k = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
+            v = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
+            lt = None if lens is None else torch.tensor(lens, dtype=torch.int64, device=dev)
+            if qb == page:
+                cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt)
+            else:
+                cache = paged_from_blocks(torch, fa, k, v, page, qb, lt)
+            kq = fa.quantize_int8_per_block(k, qb)
+            vq = fa.quantize_int8_per_block(v, qb)
+            del k, v
+            sets.append((q, cache, kq, vq, lt))
+        lengths = lens or [s] * b
+        nbytes = algorithmic_bytes(lengths, h, d, page, q_bytes=torch.finfo(qdtype).bits // 8, quant_block=qb)
+        ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(sets[i % ROTATE][0], sets[i % ROTATE][1]),
+                       steps, warmup)
+        _, st = fa.paged_quant_attention_triton(sets[0][0], sets[0][1], return_stats=True)
+        row = {"shape": name, "batch": b, "heads": h, "seq_len": s, "head_dim": d, "page": page, "quant_block": qb,
+               "q_dtype": qdt, "paged_us": round(ms * 1e3, 2), "paged_pct_of_peak": round(
+                   100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
+               "tiled_path": bool(st["tiled_path"]), "num_splits": st["num_splits"], "waves": st["num_warps"]}
+        fms = time_loop(torch, lambda i: fa.fused_dequant_attention_triton(
+            sets[i % ROTATE][0], sets[i % ROTATE][2], sets[i % ROTATE][3], lengths=sets[i % ROTATE][4]), steps, warmup)
+        row["fused_us"] = round(fms * 1e3, 2)
+        row["paged_vs_fused"] = round(ms / fms, 3)
+        out.append(row)
+        print(json.dumps({"mode": "shapes", **row}), flush=True)
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
 def load_traffic(config_key: str):
     if not PMC_SUMMARY.exists():
         return None
@@ -242,6 +329,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.mode == "copy":
         return copy_calibration(torch, args.steps)
+    if args.mode == "shapes":
+        shapes_bench(torch, fa, dev, min(args.steps, 100), min(args.warmup, 10))
+        return 0
     if args.mode == "serving":
         print(json.dumps({"mode": "serving", **serving_step_bench(torch, fa, dev, args.steps, args.warmup)}),
               flush=True)

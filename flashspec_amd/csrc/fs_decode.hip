@@ -151,6 +151,10 @@ struct QSlice {
 #pragma unroll
     for (int e = 0; e < 16; ++e) q[e] = to_f32(qp[e]);
   }
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) q[e] = 0.f;
+  }
   __device__ __forceinline__ float sum() const {
     float s = 0.f;
 #pragma unroll
@@ -177,6 +181,11 @@ struct QSlice<__half> {
     }
     qsum_part = s;
   }
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qp[k] = 0u;
+    qsum_part = 0.f;
+  }
   __device__ __forceinline__ float sum() const { return qsum_part; }
   __device__ __forceinline__ float dot(uint4 raw) const { return dot16_u8_f16(qp, raw); }
 };
@@ -191,26 +200,56 @@ __device__ __forceinline__ void axpy16_u8(float* acc, float wgt, uint4 raw) {
   }
 }
 
-// Index (in units of 16*D value bytes and of scale entries) of sequence tile `tile` of
-// (b, h); -1 when the tile is not backed by an allocated page.
+// Sequence tile `tile` (16 tokens) of (b, h): `data` indexes 16*D-byte tiles of the value
+// store, `meta` the scale / zero entries (one per quant block; a quant block is a multiple
+// of 16 tokens on this path, so a tile never straddles two).  data = -1 when the tile is
+// not backed by an allocated page.
+struct TileIndex {
+  int data, meta;
+};
+
 template <bool PAGED>
-__device__ __forceinline__ int tile_base(const DecodeParams& p, int b, int h, int row, int tile) {
+__device__ __forceinline__ TileIndex tile_index(const DecodeParams& p, int b, int h, int row, int tile) {
+  const int tpq = p.quant_block / kTile;  // tiles per quant block
   if constexpr (PAGED) {
     const int tpp = p.page_size / kTile;
     const int lp = tile / tpp;
     const int sub = tile - lp * tpp;
-    if (lp >= p.table_cols) return -1;
+    if (lp >= p.table_cols) return {-1, 0};
     const int64_t pg = table_entry(p, b, lp);
-    if (pg < 0 || pg >= p.num_pages) return -1;
-    return (int)((pg * p.heads + h) * tpp + sub);
+    if (pg < 0 || pg >= p.num_pages) return {-1, 0};
+    const int64_t ph = pg * p.heads + h;
+    return {(int)(ph * tpp + sub), (int)(ph * (tpp / tpq) + sub / tpq)};
   } else {
-    return row * p.n_blocks + tile;
+    return {row * p.n_blocks * tpq + tile, row * p.n_blocks + tile / tpq};
   }
 }
 
-template <int D>
+// 8-token sub-tile `u` of (b, h) for stores whose quant block or page is 8 tokens (an odd
+// multiple of 8): `data` in units of 8*D value bytes, `meta` the scale / zero entry of the
+// quant block holding it; data = -1 when not backed by an allocated page.
+template <bool PAGED>
+__device__ __forceinline__ TileIndex sub_index(const DecodeParams& p, int b, int h, int row, int u) {
+  const int token0 = 8 * u;
+  if constexpr (PAGED) {
+    const int lp = token0 / p.page_size;
+    const int within = token0 - lp * p.page_size;
+    if (lp >= p.table_cols) return {-1, 0};
+    const int64_t pg = table_entry(p, b, lp);
+    if (pg < 0 || pg >= p.num_pages) return {-1, 0};
+    const int64_t ph = pg * p.heads + h;
+    return {(int)(ph * (p.page_size / 8) + within / 8), (int)(ph * (p.page_size / p.quant_block) + within / p.quant_block)};
+  } else {
+    return {row * p.n_blocks * (p.quant_block / 8) + u, row * p.n_blocks + token0 / p.quant_block};
+  }
+}
+
+// Register layout for head dims up to DP (64, 128 or 256): DP/16 lanes share a token row,
+// each holding 16 of its dims; a head_dim D < DP (a multiple of 16) leaves the lanes with
+// 16j >= D idle.
+template <int DP>
 struct TileRegs {
-  static constexpr int LPT = D / 16;          // lanes per token row (16 bytes each)
+  static constexpr int LPT = DP / 16;         // lanes per token row (16 bytes each)
   static constexpr int RPL = kWave / LPT;     // token rows per 16-byte-per-lane load
   static constexpr int LPTILE = kTile / RPL;  // loads per tile per tensor
   uint4 k[LPTILE];
@@ -229,19 +268,45 @@ __device__ __forceinline__ uint4 stream_load(const uint4* p) {
 // Loads one tile.  An unbacked or out-of-range tile (base < 0) loads tile 0 of the store
 // instead and its tokens are masked by the caller: a branch around the loads would make
 // the compiler route the registers through a pointer select into scratch memory, and
-// the repeated tile-0 reads are L2 hits.
-template <int D>
-__device__ __forceinline__ void load_tile(TileRegs<D>& t, const int8_t* kbase, const int8_t* vbase, int base,
-                                          int lane) {
-  constexpr int LPTILE = TileRegs<D>::LPTILE;
-  const size_t off = (size_t)(base < 0 ? 0 : base) * (kTile * D);
-  const uint4* kp = (const uint4*)(kbase + off) + lane;
-  const uint4* vp = (const uint4*)(vbase + off) + lane;
+// the repeated tile-0 reads are L2 hits.  `lane_off` is the lane's byte offset inside a
+// group of RPL token rows (g * D + 16 j), `rstride` = RPL * D bytes; with D = DP the
+// lanes of one load cover 64 contiguous 16-byte chunks.
+template <int DP>
+__device__ __forceinline__ void load_tile(TileRegs<DP>& t, const int8_t* kbase, const int8_t* vbase, int base,
+                                          int D, int lane_off, int rstride) {
+  constexpr int LPTILE = TileRegs<DP>::LPTILE;
+  const size_t off = (size_t)(base < 0 ? 0 : base) * (kTile * D) + lane_off;
+  const int8_t* kp = kbase + off;
+  const int8_t* vp = vbase + off;
 #pragma unroll
-  for (int r = 0; r < LPTILE; ++r) t.k[r] = stream_load(kp + r * kWave);
+  for (int r = 0; r < LPTILE; ++r) t.k[r] = stream_load((const uint4*)(kp + r * rstride));
 #pragma unroll
-  for (int r = 0; r < LPTILE; ++r) t.v[r] = stream_load(vp + r * kWave);
+  for (int r = 0; r < LPTILE; ++r) t.v[r] = stream_load((const uint4*)(vp + r * rstride));
 }
+
+// Loads one tile made of two 8-token sub-tiles with their own bases (units of 8*D bytes);
+// row r*RPL + g of the tile lies in sub-tile (r*RPL + g) / 8.  Lanes past head_dim read
+// column 0.  A negative base loads sub-tile 0 of the store (masked by the caller).
+template <int DP>
+__device__ __forceinline__ void load_tile_sub(TileRegs<DP>& t, const int8_t* kbase, const int8_t* vbase, int base0,
+                                              int base1, int D, int g, int col) {
+  constexpr int LPTILE = TileRegs<DP>::LPTILE, RPL = TileRegs<DP>::RPL;
+#pragma unroll
+  for (int r = 0; r < LPTILE; ++r) {
+    const int rowt = r * RPL + g;
+    const int bs = (rowt >> 3) ? base1 : base0;
+    const size_t off = (size_t)(bs < 0 ? 0 : bs) * (8 * D) + (size_t)(rowt & 7) * D + col;
+    t.k[r] = stream_load((const uint4*)(kbase + off));
+    t.v[r] = stream_load((const uint4*)(vbase + off));
+  }
+}
+
+// Per-token-row quantization parameters of one tile: entry [0] for its first 8 tokens,
+// [1] for the last 8 (equal unless the store uses 8-token quant blocks or pages).
+struct TileMeta {
+  float ks[2], kz[2], vs[2], vz[2];
+  bool valid[2];
+};
 
 // Online-softmax state of one lane: token rows `g` of every tile, dims [16j, 16j+16).
 struct LaneState {
@@ -249,19 +314,19 @@ struct LaneState {
   float acc[16];
 };
 
-template <int D, typename QT>
-__device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<D>& t, const QSlice<QT>& q, float qsum,
-                                             bool valid_tile, int token0, int len, int g, float ks, float kz,
-                                             float vs, float vz) {
-  constexpr int LPT = TileRegs<D>::LPT, RPL = TileRegs<D>::RPL, LPTILE = TileRegs<D>::LPTILE;
+template <int DP, typename QT>
+__device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& t, const QSlice<QT>& q, float qsum,
+                                             const TileMeta& mt, int token0, int len, int g) {
+  constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
   float s[LPTILE];
   bool ok[LPTILE];
   float mnew = st.m;
 #pragma unroll
   for (int r = 0; r < LPTILE; ++r) {
+    const bool hi = ((r * RPL + g) >> 3) != 0;  // second 8-token half; compile-time for DP >= 128
     const float dot = group_sum<LPT>(q.dot(t.k[r]));
-    ok[r] = valid_tile && (token0 + r * RPL + g) < len;
-    s[r] = (dot - (QSlice<QT>::kOffset + kz) * qsum) * ks;
+    ok[r] = (hi ? mt.valid[1] : mt.valid[0]) && (token0 + r * RPL + g) < len;
+    s[r] = (dot - (QSlice<QT>::kOffset + (hi ? mt.kz[1] : mt.kz[0])) * qsum) * (hi ? mt.ks[1] : mt.ks[0]);
     if (ok[r]) mnew = fmaxf(mnew, s[r]);
   }
   // Refresh the running max only when some lane's max grew by more than the slack;
@@ -276,23 +341,27 @@ __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<D>& t
   }
 #pragma unroll
   for (int r = 0; r < LPTILE; ++r) {
+    const bool hi = ((r * RPL + g) >> 3) != 0;
     const float pr = ok[r] ? fast_exp2(s[r] - st.m) : 0.f;
     st.l += pr;
-    const float w = pr * vs;
-    st.zacc = fmaf(w, vz, st.zacc);
+    const float w = pr * (hi ? mt.vs[1] : mt.vs[0]);
+    st.zacc = fmaf(w, hi ? mt.vz[1] : mt.vz[0], st.zacc);
     axpy16_u8(st.acc, w, t.v[r]);
   }
 }
 
 // Waves per workgroup the tiled kernel may run with: 16, or 8 for head_dim 256 so
 // that its 128-float registers per lane fit without spilling.
-constexpr int max_tiled_waves(int D) { return D == 256 ? 8 : kMaxWaves; }
+constexpr int max_tiled_waves(int DP) { return DP == 256 ? 8 : kMaxWaves; }
 
-template <int D, typename QT, bool PAGED>
-__global__ void __launch_bounds__(kWave * max_tiled_waves(D))
+// Register layout (64, 128 or 256 dims) that serves a head_dim on the tiled path.
+__host__ __device__ constexpr int padded_head_dim(int D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
+
+template <int DP, typename QT, bool PAGED, bool SUB>
+__global__ void __launch_bounds__(kWave * max_tiled_waves(DP))
 decode_rows_kernel(const DecodeParams p) {
-  constexpr int LPT = TileRegs<D>::LPT;
-  __shared__ float s_acc[kMaxWaves * D];
+  constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL;
+  __shared__ float s_acc[kMaxWaves * DP];
   __shared__ float s_ml[2 * kMaxWaves];
 
 #ifdef FS_TRACE_WG
@@ -317,27 +386,58 @@ decode_rows_kernel(const DecodeParams p) {
   const int tiles_max = (p.seq_len + kTile - 1) / kTile;
   const int end_max = min(tiles_max, (split + 1) * p.split_tiles);
   const int nk_max = first < end_max ? (end_max - first + W - 1) / W : 0;
-  int my_base = -1;
-  if (lane < nk_max) my_base = tile_base<PAGED>(p, b, h, row, first + W * lane);
+  // SUB (8-token quant blocks or pages): each tile is two sub-tiles with their own base and
+  // quantization parameters, held as a second set of lane registers.
+  int my_base = -1, my_meta = 0, my_base1 = -1, my_meta1 = 0;
+  if (lane < nk_max) {
+    if constexpr (SUB) {
+      const TileIndex t0 = sub_index<PAGED>(p, b, h, row, 2 * (first + W * lane));
+      const TileIndex t1 = sub_index<PAGED>(p, b, h, row, 2 * (first + W * lane) + 1);
+      my_base = t0.data;
+      my_meta = t0.meta;
+      my_base1 = t1.data;
+      my_meta1 = t1.meta;
+    } else {
+      const TileIndex ti = tile_index<PAGED>(p, b, h, row, first + W * lane);
+      my_base = ti.data;
+      my_meta = ti.meta;
+    }
+  }
 
   const int len = row_length(p.lengths, b, p.seq_len);
   const int nsplit = row_splits(len, p.split_tiles);
   if (split >= nsplit) return;  // whole workgroup, before any barrier
   const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
   const int nk = first < tile_end ? (tile_end - first + W - 1) / W : 0;  // <= kMaxTilesPerWave
-  if (lane >= nk) my_base = -1;
+  if (lane >= nk) my_base = my_base1 = -1;
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
   if (my_base >= 0) {
-    my_ks = p.sc[0][my_base] * p.qk_scale;
-    my_kz = (float)p.zp[0][my_base];
-    my_vs = p.sc[1][my_base];
-    my_vz = (float)p.zp[1][my_base];
+    my_ks = p.sc[0][my_meta] * p.qk_scale;
+    my_kz = (float)p.zp[0][my_meta];
+    my_vs = p.sc[1][my_meta];
+    my_vz = (float)p.zp[1][my_meta];
+  }
+  float my_ks1 = 0.f, my_kz1 = 0.f, my_vs1 = 0.f, my_vz1 = 0.f;
+  if constexpr (SUB) {
+    if (my_base1 >= 0) {
+      my_ks1 = p.sc[0][my_meta1] * p.qk_scale;
+      my_kz1 = (float)p.zp[0][my_meta1];
+      my_vs1 = p.sc[1][my_meta1];
+      my_vz1 = (float)p.zp[1][my_meta1];
+    }
   }
 
+  const int D = p.head_dim;
   const int j = lane % LPT;  // dim slice [16j, 16j+16)
   const int g = lane / LPT;  // token row within a load
+  const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
+  const int lane_off = g * D + (active ? 16 * j : 0);
+  const int rstride = RPL * D;
   QSlice<QT> q;
-  q.load((const QT*)p.q + (size_t)row * D + 16 * j);
+  if (active)
+    q.load((const QT*)p.q + (size_t)row * D + 16 * j);
+  else
+    q.clear();
   const float qsum = group_sum<LPT>(q.sum());
 
   LaneState st;
@@ -350,23 +450,47 @@ decode_rows_kernel(const DecodeParams p) {
   const int8_t* kbase = p.kv[0];
   const int8_t* vbase = p.kv[1];
   auto base_of = [&](int k) { return k < nk ? readlane_i32(my_base, k) : -1; };
-  auto consume = [&](const TileRegs<D>& t, int k) {
-    consume_tile<D, QT>(st, t, q, qsum, readlane_i32(my_base, k) >= 0, (first + W * k) * kTile, len, g,
-                        readlane_f32(my_ks, k), readlane_f32(my_kz, k), readlane_f32(my_vs, k),
-                        readlane_f32(my_vz, k));
+  auto base1_of = [&](int k) { return k < nk ? readlane_i32(my_base1, k) : -1; };
+  auto load = [&](TileRegs<DP>& t, int k) {
+    if constexpr (SUB)
+      load_tile_sub<DP>(t, kbase, vbase, base_of(k), base1_of(k), D, g, active ? 16 * j : 0);
+    else
+      load_tile<DP>(t, kbase, vbase, base_of(k), D, lane_off, rstride);
+  };
+  auto consume = [&](const TileRegs<DP>& t, int k) {
+    TileMeta mt;
+    mt.ks[0] = readlane_f32(my_ks, k);
+    mt.kz[0] = readlane_f32(my_kz, k);
+    mt.vs[0] = readlane_f32(my_vs, k);
+    mt.vz[0] = readlane_f32(my_vz, k);
+    mt.valid[0] = readlane_i32(my_base, k) >= 0;
+    if constexpr (SUB) {
+      mt.ks[1] = readlane_f32(my_ks1, k);
+      mt.kz[1] = readlane_f32(my_kz1, k);
+      mt.vs[1] = readlane_f32(my_vs1, k);
+      mt.vz[1] = readlane_f32(my_vz1, k);
+      mt.valid[1] = readlane_i32(my_base1, k) >= 0;
+    } else {
+      mt.ks[1] = mt.ks[0];
+      mt.kz[1] = mt.kz[0];
+      mt.vs[1] = mt.vs[0];
+      mt.vz[1] = mt.vz[0];
+      mt.valid[1] = mt.valid[0];
+    }
+    consume_tile<DP, QT>(st, t, q, qsum, mt, (first + W * k) * kTile, len, g);
   };
   // two register buffers: tile k+1 is in flight while tile k is consumed
-  TileRegs<D> ta, tb2;
-  load_tile<D>(ta, kbase, vbase, base_of(0), lane);
+  TileRegs<DP> ta, tb2;
+  load(ta, 0);
   for (int k = 0; k < nk; k += 2) {
-    load_tile<D>(tb2, kbase, vbase, base_of(k + 1), lane);
+    load(tb2, k + 1);
     consume(ta, k);
 #ifdef FS_TRACE_WG
     if (k == 0 && w == 0 && lane == 0)
       ((uint64_t*)p.part_ml)[(size_t)blockIdx.x * 20 + 1] = __builtin_amdgcn_s_memrealtime();
 #endif
     if (k + 1 >= nk) break;
-    load_tile<D>(ta, kbase, vbase, base_of(k + 2), lane);
+    load(ta, k + 2);
     consume(tb2, k + 1);
   }
 
@@ -394,7 +518,7 @@ decode_rows_kernel(const DecodeParams p) {
   // merge the W waves through LDS
   if (g == 0) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s_acc[w * D + 16 * j + e] = st.acc[e];
+    for (int e = 0; e < 16; ++e) s_acc[w * DP + 16 * j + e] = st.acc[e];
   }
   if (lane == 0) {
     s_ml[2 * w] = m;
@@ -408,7 +532,7 @@ decode_rows_kernel(const DecodeParams p) {
     for (int ww = 0; ww < W; ++ww) {
       const float e = fast_exp2(s_ml[2 * ww] - M);
       L = fmaf(s_ml[2 * ww + 1], e, L);
-      a = fmaf(s_acc[ww * D + d], e, a);
+      a = fmaf(s_acc[ww * DP + d], e, a);
     }
     if (nsplit == 1) {
       ((QT*)p.out)[(size_t)row * D + d] = from_f32<QT>(L > 0.f ? a / L : 0.f);
@@ -561,8 +685,21 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
 
 // ---- host launchers --------------------------------------------------------------------------
 
+// Tiled path: head_dim a multiple of 16 up to 256 (served by the 64-, 128- or 256-dim
+// register layout), quant blocks a multiple of 8 tokens, whole quant blocks per page.  Quant
+// blocks that are an odd multiple of 8 take the sub-tile form of the kernel.
 static bool tiled_path(int head_dim, int page_size, int quant_block) {
-  return quant_block == kTile && page_size % kTile == 0 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+  return head_dim >= 16 && head_dim <= 256 && head_dim % 16 == 0 && quant_block >= 8 && quant_block % 8 == 0 &&
+         page_size > 0 && page_size % quant_block == 0;
+}
+
+template <typename QT, bool PAGED, bool SUB>
+static void launch_tiled(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
+  switch (padded_head_dim(p.head_dim)) {
+    case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, SUB>), grid, block, 0, st, p); break;
+    case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, SUB>), grid, block, 0, st, p); break;
+    default: hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, SUB>), grid, block, 0, st, p); break;
+  }
 }
 
 template <typename QT, bool PAGED>
@@ -570,12 +707,10 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
   const dim3 block(kWave * waves_per_block);
   if (tiled) {
     const dim3 grid((unsigned)((int64_t)p.rows * p.max_splits));
-    switch (p.head_dim) {
-      case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED>), grid, block, 0, st, p); break;
-      case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED>), grid, block, 0, st, p); break;
-      case 256: hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED>), grid, block, 0, st, p); break;
-      default: return set_error(FS_ERR_INVALID, "tiled decode path needs head_dim 64, 128 or 256");
-    }
+    if (p.quant_block % kTile != 0)
+      launch_tiled<QT, PAGED, true>(p, grid, block, st);
+    else
+      launch_tiled<QT, PAGED, false>(p, grid, block, st);
   } else {
     const int64_t waves = (int64_t)p.rows * p.max_splits;
     const dim3 grid((unsigned)((waves + waves_per_block - 1) / waves_per_block));
@@ -612,8 +747,8 @@ static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, 
   if (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4 && waves_per_block != 8 &&
       waves_per_block != 16)
     return set_error(FS_ERR_INVALID, "waves_per_block must be 1, 2, 4, 8 or 16");
-  if (tiled && waves_per_block > max_tiled_waves(p.head_dim))
-    return set_error(FS_ERR_INVALID, "waves_per_block must be <= 8 for head_dim 256 on the tiled path");
+  if (tiled && waves_per_block > max_tiled_waves(padded_head_dim(p.head_dim)))
+    return set_error(FS_ERR_INVALID, "waves_per_block must be <= 8 for head_dim > 128 on the tiled path");
   if (tiled && p.split_tiles > kMaxTilesPerWave * waves_per_block)
     return set_error(FS_ERR_INVALID, "split_tiles must be <= 64 * waves_per_block on the tiled path");
   if ((int64_t)p.rows * p.max_splits > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "decode grid too large");
@@ -664,7 +799,8 @@ extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_va
   if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes)) return rc;
   if (block_size <= 0 || n_blocks <= 0 || (int64_t)n_blocks * block_size < seq_len)
     return set_error(FS_ERR_INVALID, "n_blocks * block_size must cover seq_len");
-  if ((int64_t)p.rows * n_blocks > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "K/V store too large for 32-bit tile ids");
+  if ((int64_t)p.rows * n_blocks * ((block_size + kTile - 1) / kTile) > 0x7fffffffLL)
+    return set_error(FS_ERR_INVALID, "K/V store too large for 32-bit tile ids");
   return launch_decode<false>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }
 

@@ -184,7 +184,7 @@ def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_bl
     from . import _lib
 
     tiled = bool(_lib.require().fs_decode_tiled_path(head_dim, page_size, quant_block))
-    max_waves = 8 if head_dim == 256 else MAX_TILED_WAVES  # register budget of the head_dim-256 kernel
+    max_waves = 8 if head_dim > 128 else MAX_TILED_WAVES  # register budget of the 256-dim register layout
     waves = forced_tiled_waves() if tiled else resolve_num_warps()
     if tiled and waves is not None:
         waves = min(waves, max_waves)

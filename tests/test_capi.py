@@ -60,7 +60,10 @@ def test_invalid_arguments_are_rejected_before_launch():
                                 256, 1, 2, None)
     assert rc == _lib.FS_ERR_INVALID and "64" in lib.fs_last_error().decode()
     assert lib.fs_decode_tiled_path(128, 16, 16) == 1 and lib.fs_decode_tiled_path(128, 32, 16) == 1
-    assert lib.fs_decode_tiled_path(48, 16, 16) == 0 and lib.fs_decode_tiled_path(128, 16, 8) == 0
+    assert lib.fs_decode_tiled_path(48, 16, 16) == 1 and lib.fs_decode_tiled_path(96, 32, 32) == 1
+    assert lib.fs_decode_tiled_path(128, 16, 8) == 1 and lib.fs_decode_tiled_path(128, 24, 24) == 1
+    assert lib.fs_decode_tiled_path(128, 4, 4) == 0 and lib.fs_decode_tiled_path(72, 16, 16) == 0
+    assert lib.fs_decode_tiled_path(128, 48, 32) == 0 and lib.fs_decode_tiled_path(512, 16, 16) == 0
     # unsupported dtype code in quantize
     rc = lib.fs_quantize_i8(1, 9, 1, 16, 128, 16, 1, 1, 1, None)
     assert rc == _lib.FS_ERR_INVALID

@@ -250,8 +250,14 @@ def _fused_case(B, H, S, D, bs, seed, q_dtype=torch.float16, lengths=None):
     (2, 8, 700, 128, 16, torch.bfloat16, [700, 1]),
     (2, 8, 300, 128, 16, torch.float32, [0, 300]),
     (1, 2, 517, 256, 16, torch.float16, None),
-    (2, 2, 77, 32, 16, torch.float16, [77, 40]),          # generic path: head_dim 32
-    (2, 3, 200, 64, 8, torch.float16, [200, 99]),         # generic path: quant block 8
+    (2, 2, 77, 32, 16, torch.float16, [77, 40]),          # head_dim 32 on the 64-dim layout
+    (2, 4, 333, 96, 16, torch.float16, [333, 200]),       # head_dim 96 on the 128-dim layout
+    (2, 2, 260, 192, 32, torch.bfloat16, [260, 31]),      # head_dim 192, quant block 32
+    (2, 3, 130, 80, 64, torch.float32, None),             # head_dim 80, quant block 64
+    (2, 3, 200, 64, 8, torch.float16, [200, 99]),         # 8-token quant blocks (sub-tiles), 64-dim layout
+    (2, 4, 301, 128, 8, torch.float16, [301, 150]),       # 8-token quant blocks, 128-dim layout
+    (1, 2, 90, 256, 24, torch.bfloat16, [90]),            # 24-token quant blocks, 256-dim layout
+    (1, 2, 100, 40, 16, torch.float16, [100]),            # generic path: head_dim 40
 ])
 def test_fused_attention_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     announce(f"fused B{B} H{H} S{S} D{D} bs{bs} {q_dtype} lengths={lengths}")
@@ -302,7 +308,13 @@ def _paged_case(B, H, S, D, page, seed, layout="contiguous", lengths=None, q_dty
     (3, 4, 300, 128, 32, "shuffled", [300, 17, 0]),       # two tiles per page
     (2, 2, 64, 256, 16, "interleaved", [64, 63]),
     (2, 2, 7, 64, 4, "contiguous", None),                 # generic path: page 4
-    (2, 3, 50, 48, 16, "shuffled", [50, 3]),              # generic path: head_dim 48
+    (2, 3, 50, 48, 16, "shuffled", [50, 3]),              # head_dim 48 on the 64-dim layout
+    (2, 3, 300, 96, 32, "shuffled", [300, 45]),           # head_dim 96, page = quant block 32
+    (2, 2, 200, 112, 64, "interleaved", [200, 64]),       # head_dim 112, page 64
+    (2, 2, 50, 24, 16, "contiguous", [50, 9]),            # generic path: head_dim 24
+    (3, 4, 200, 128, 8, "shuffled", [200, 17, 9]),        # 8-token pages: two pages per tile
+    (2, 2, 100, 64, 8, "interleaved", [100, 8]),          # 8-token pages, 64-dim layout
+    (2, 3, 150, 96, 24, "shuffled", [150, 50]),           # 24-token pages
 ])
 def test_paged_attention_matches_oracle(B, H, S, D, page, layout, lengths):
     announce(f"paged B{B} H{H} S{S} D{D} page{page} {layout} lengths={lengths}")
@@ -316,6 +328,35 @@ def test_paged_attention_matches_oracle(B, H, S, D, page, layout, lengths):
         assert (got[[i for i in range(B) if i not in keep]] == 0).all()
         got, ref = got[keep], ref[keep]
     assert_attention_close(got, ref, torch.float16, "paged")
+
+
+@pytest.mark.parametrize("page,qb,D", [(32, 16, 128), (64, 16, 64), (64, 32, 256), (128, 64, 96), (16, 8, 128),
+                                       (32, 8, 64), (48, 24, 128)])
+def test_paged_pages_holding_several_quant_blocks(page, qb, D):
+    """Pages of page // qb quant blocks each (reference triton_paged.py:242-246), shuffled table."""
+
+    announce(f"paged page{page} quant block {qb} D{D}")
+    B, H, S = 3, 4, 5 * page + 3
+    lengths = np.array([S, page + 1, 2 * page - 5], dtype=np.int64)
+    k = np_of(randn((B, H, S, D), 71).float())
+    v = np_of(randn((B, H, S, D), 72).float())
+    n = -(-S // page)
+    rng = np.random.default_rng(page + qb)
+    perm = rng.permutation(B * n)
+    pk = op.dense_to_pages(k, page)[perm]
+    pv = op.dense_to_pages(v, page)[perm]
+    table = np.empty(B * n, dtype=np.int64)
+    table[perm] = np.arange(B * n)
+    cache = op.OracleCache(oq.quantize_int8_per_block(pk, qb), oq.quantize_int8_per_block(pv, qb),
+                           table.reshape(B, n), lengths, page, S)
+    q = randn((B, H, D), 73)
+    got = fa.paged_quant_attention_triton(q.to(DEV), to_cache(cache, DEV))
+    assert lib_tiled(D, page, qb)
+    assert_attention_close(got, oa.paged_quant_attention(np_of(q), cache), torch.float16, f"page{page} qb{qb}")
+
+
+def lib_tiled(D, page, qb):
+    return bool(_lib.require().fs_decode_tiled_path(D, page, qb))
 
 
 @pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float32])
