@@ -213,7 +213,8 @@ def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
             "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1)}
 
 
-# Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths)
+# Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths);
+# quant block 1 = symmetric absmax INT8 with one scale per token (quantize_int8_symmetric_per_token).
 SHAPES = [
     ("metric", 8, 32, 4096, 128, 16, 16, "float16", None),
     ("c3_s2048", 8, 32, 2048, 128, 16, 16, "float16", None),
@@ -231,6 +232,8 @@ SHAPES = [
     ("page_16_quant_8", 8, 32, 4096, 128, 16, 8, "float16", None),
     ("head_dim_40_generic", 8, 32, 4096, 40, 16, 16, "float16", None),
     ("batch_1_splitk", 1, 32, 16384, 128, 16, 16, "float16", None),
+    ("c1_symmetric_per_token", 4, 32, 2048, 128, 16, 1, "float16", None),
+    ("c2_symmetric_per_token", 8, 32, 4096, 128, 16, 1, "float16", None),
 ]
 
 
@@ -270,12 +273,16 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
             k = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
             v = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
             lt = None if lens is None else torch.tensor(lens, dtype=torch.int64, device=dev)
-            if qb == page:
-                cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt)
+            if qb == 1:
+                cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt, kv_format="symmetric_token")
+                kq, vq = fa.quantize_int8_symmetric_per_token(k), fa.quantize_int8_symmetric_per_token(v)
             else:
-                cache = paged_from_blocks(torch, fa, k, v, page, qb, lt)
-            kq = fa.quantize_int8_per_block(k, qb)
-            vq = fa.quantize_int8_per_block(v, qb)
+                if qb == page:
+                    cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt)
+                else:
+                    cache = paged_from_blocks(torch, fa, k, v, page, qb, lt)
+                kq = fa.quantize_int8_per_block(k, qb)
+                vq = fa.quantize_int8_per_block(v, qb)
             del k, v
             sets.append((q, cache, kq, vq, lt))
         lengths = lens or [s] * b

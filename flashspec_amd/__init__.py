@@ -7,7 +7,7 @@ to make ``import flashspec`` resolve here).
 
 from .attention import fused_dequant_attention, paged_quant_attention, reference_attention
 from .paged import PagedKVAllocator, PagedKVCache
-from .quant import QuantizedTensor, dequantize_int8_per_block, quantize_int8_per_block
+from .quant import QuantizedTensor, dequantize_int8_per_block, quantize_int8_per_block, quantize_int8_symmetric_per_token
 from .triton_fused import fused_dequant_attention_triton
 from .triton_paged import paged_quant_attention_triton
 
@@ -21,5 +21,6 @@ __all__ = [
     "paged_quant_attention",
     "paged_quant_attention_triton",
     "quantize_int8_per_block",
+    "quantize_int8_symmetric_per_token",
     "reference_attention",
 ]

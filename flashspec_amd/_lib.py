@@ -56,6 +56,9 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
          c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p],
     ),
+    "fs_quantize_sym_i8": (
+        c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p]
+    ),
     "fs_append_tokens_i8": (
         c_int,
         [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,

@@ -29,6 +29,13 @@ constexpr int kMaxTilesPerWave = 64;  // per split and wave: one metadata lane p
 constexpr float kRescaleSlack = 8.0f;  // running max may lag the true max by 2^8
 constexpr int kXcds = 8;  // MI355X: accelerator complex dies, each with its own L2
 
+// How a tile finds its quantization parameters (scale / zero point).
+enum QuantMode : int {
+  kQmBlock = 0,  // quant block a multiple of 16 tokens: one entry per tile
+  kQmSub = 1,    // quant block an odd multiple of 8 tokens (or 8-token pages): one per 8-token half
+  kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
+};
+
 struct DecodeParams {
   const void* q;
   const int8_t* kv[2];
@@ -244,6 +251,23 @@ __device__ __forceinline__ TileIndex sub_index(const DecodeParams& p, int b, int
   }
 }
 
+// Token mode: first token of tile `tile` of (b, h) in the value store (units of D bytes, the
+// same index as its per-token scale / zero), -1 when not backed by an allocated page.
+template <bool PAGED>
+__device__ __forceinline__ int token_index(const DecodeParams& p, int b, int h, int row, int tile) {
+  if constexpr (PAGED) {
+    const int tpp = p.page_size / kTile;
+    const int lp = tile / tpp;
+    const int sub = tile - lp * tpp;
+    if (lp >= p.table_cols) return -1;
+    const int64_t pg = table_entry(p, b, lp);
+    if (pg < 0 || pg >= p.num_pages) return -1;
+    return (int)((pg * p.heads + h) * p.page_size + sub * kTile);
+  } else {
+    return row * p.n_blocks + tile * kTile;
+  }
+}
+
 // Register layout for head dims up to DP (64, 128 or 256): DP/16 lanes share a token row,
 // each holding 16 of its dims; a head_dim D < DP (a multiple of 16) leaves the lanes with
 // 16j >= D idle.
@@ -254,6 +278,7 @@ struct TileRegs {
   static constexpr int LPTILE = kTile / RPL;  // loads per tile per tensor
   uint4 k[LPTILE];
   uint4 v[LPTILE];
+  float ks[LPTILE], kz[LPTILE], vs[LPTILE], vz[LPTILE];  // per-row parameters (token mode only)
 };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -301,11 +326,34 @@ __device__ __forceinline__ void load_tile_sub(TileRegs<DP>& t, const int8_t* kba
   }
 }
 
-// Per-token-row quantization parameters of one tile: entry [0] for its first 8 tokens,
-// [1] for the last 8 (equal unless the store uses 8-token quant blocks or pages).
-struct TileMeta {
-  float ks[2], kz[2], vs[2], vz[2];
-  bool valid[2];
+// Token mode: `base` is the tile's first token in the store (units of D bytes), which also
+// indexes the per-token scale / zero arrays; rows at or past `avail` (stored tokens left from
+// `base`, short only at the end of a contiguous row) read row 0 and are masked by the caller.
+template <int DP>
+__device__ __forceinline__ void load_tile_tok(TileRegs<DP>& t, const DecodeParams& p, const int8_t* kbase,
+                                              const int8_t* vbase, int base, int avail, int D, int g, int col) {
+  constexpr int LPTILE = TileRegs<DP>::LPTILE, RPL = TileRegs<DP>::RPL;
+  const int b0 = base < 0 ? 0 : base;
+#pragma unroll
+  for (int r = 0; r < LPTILE; ++r) {
+    int rowt = r * RPL + g;
+    if (base < 0 || rowt >= avail) rowt = 0;
+    const size_t off = ((size_t)b0 + rowt) * D + col;
+    t.k[r] = stream_load((const uint4*)(kbase + off));
+    t.v[r] = stream_load((const uint4*)(vbase + off));
+    const int idx = b0 + rowt;
+    t.ks[r] = p.sc[0][idx] * p.qk_scale;
+    t.kz[r] = (float)p.zp[0][idx];
+    t.vs[r] = p.sc[1][idx];
+    t.vz[r] = (float)p.zp[1][idx];
+  }
+}
+
+// Quantization parameters of the LPTILE token rows a lane holds in one tile.
+template <int N>
+struct RowMeta {
+  float ks[N], kz[N], vs[N], vz[N];
+  bool valid[N];
 };
 
 // Online-softmax state of one lane: token rows `g` of every tile, dims [16j, 16j+16).
@@ -316,17 +364,16 @@ struct LaneState {
 
 template <int DP, typename QT>
 __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& t, const QSlice<QT>& q, float qsum,
-                                             const TileMeta& mt, int token0, int len, int g) {
+                                             const RowMeta<TileRegs<DP>::LPTILE>& rm, int token0, int len, int g) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
   float s[LPTILE];
   bool ok[LPTILE];
   float mnew = st.m;
 #pragma unroll
   for (int r = 0; r < LPTILE; ++r) {
-    const bool hi = ((r * RPL + g) >> 3) != 0;  // second 8-token half; compile-time for DP >= 128
     const float dot = group_sum<LPT>(q.dot(t.k[r]));
-    ok[r] = (hi ? mt.valid[1] : mt.valid[0]) && (token0 + r * RPL + g) < len;
-    s[r] = (dot - (QSlice<QT>::kOffset + (hi ? mt.kz[1] : mt.kz[0])) * qsum) * (hi ? mt.ks[1] : mt.ks[0]);
+    ok[r] = rm.valid[r] && (token0 + r * RPL + g) < len;
+    s[r] = (dot - (QSlice<QT>::kOffset + rm.kz[r]) * qsum) * rm.ks[r];
     if (ok[r]) mnew = fmaxf(mnew, s[r]);
   }
   // Refresh the running max only when some lane's max grew by more than the slack;
@@ -341,11 +388,10 @@ __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& 
   }
 #pragma unroll
   for (int r = 0; r < LPTILE; ++r) {
-    const bool hi = ((r * RPL + g) >> 3) != 0;
     const float pr = ok[r] ? fast_exp2(s[r] - st.m) : 0.f;
     st.l += pr;
-    const float w = pr * (hi ? mt.vs[1] : mt.vs[0]);
-    st.zacc = fmaf(w, hi ? mt.vz[1] : mt.vz[0], st.zacc);
+    const float w = pr * rm.vs[r];
+    st.zacc = fmaf(w, rm.vz[r], st.zacc);
     axpy16_u8(st.acc, w, t.v[r]);
   }
 }
@@ -357,10 +403,11 @@ constexpr int max_tiled_waves(int DP) { return DP == 256 ? 8 : kMaxWaves; }
 // Register layout (64, 128 or 256 dims) that serves a head_dim on the tiled path.
 __host__ __device__ constexpr int padded_head_dim(int D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
 
-template <int DP, typename QT, bool PAGED, bool SUB>
+template <int DP, typename QT, bool PAGED, int QM>
 __global__ void __launch_bounds__(kWave * max_tiled_waves(DP))
 decode_rows_kernel(const DecodeParams p) {
-  constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL;
+  constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
+  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken;
   __shared__ float s_acc[kMaxWaves * DP];
   __shared__ float s_ml[2 * kMaxWaves];
 
@@ -397,6 +444,8 @@ decode_rows_kernel(const DecodeParams p) {
       my_meta = t0.meta;
       my_base1 = t1.data;
       my_meta1 = t1.meta;
+    } else if constexpr (TOK) {
+      my_base = token_index<PAGED>(p, b, h, row, first + W * lane);
     } else {
       const TileIndex ti = tile_index<PAGED>(p, b, h, row, first + W * lane);
       my_base = ti.data;
@@ -411,7 +460,7 @@ decode_rows_kernel(const DecodeParams p) {
   const int nk = first < tile_end ? (tile_end - first + W - 1) / W : 0;  // <= kMaxTilesPerWave
   if (lane >= nk) my_base = my_base1 = -1;
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
-  if (my_base >= 0) {
+  if (!TOK && my_base >= 0) {
     my_ks = p.sc[0][my_meta] * p.qk_scale;
     my_kz = (float)p.zp[0][my_meta];
     my_vs = p.sc[1][my_meta];
@@ -451,33 +500,54 @@ decode_rows_kernel(const DecodeParams p) {
   const int8_t* vbase = p.kv[1];
   auto base_of = [&](int k) { return k < nk ? readlane_i32(my_base, k) : -1; };
   auto base1_of = [&](int k) { return k < nk ? readlane_i32(my_base1, k) : -1; };
+  // stored tokens from a tile's first token to the end of its contiguous run (token mode)
+  auto avail_of = [&](int k) {
+    if constexpr (PAGED) return kTile;
+    else return p.n_blocks - (first + W * k) * kTile;
+  };
   auto load = [&](TileRegs<DP>& t, int k) {
     if constexpr (SUB)
       load_tile_sub<DP>(t, kbase, vbase, base_of(k), base1_of(k), D, g, active ? 16 * j : 0);
+    else if constexpr (TOK)
+      load_tile_tok<DP>(t, p, kbase, vbase, base_of(k), avail_of(k), D, g, active ? 16 * j : 0);
     else
       load_tile<DP>(t, kbase, vbase, base_of(k), D, lane_off, rstride);
   };
   auto consume = [&](const TileRegs<DP>& t, int k) {
-    TileMeta mt;
-    mt.ks[0] = readlane_f32(my_ks, k);
-    mt.kz[0] = readlane_f32(my_kz, k);
-    mt.vs[0] = readlane_f32(my_vs, k);
-    mt.vz[0] = readlane_f32(my_vz, k);
-    mt.valid[0] = readlane_i32(my_base, k) >= 0;
-    if constexpr (SUB) {
-      mt.ks[1] = readlane_f32(my_ks1, k);
-      mt.kz[1] = readlane_f32(my_kz1, k);
-      mt.vs[1] = readlane_f32(my_vs1, k);
-      mt.vz[1] = readlane_f32(my_vz1, k);
-      mt.valid[1] = readlane_i32(my_base1, k) >= 0;
+    RowMeta<LPTILE> rm;
+    const bool v0 = readlane_i32(my_base, k) >= 0;
+    if constexpr (TOK) {
+#pragma unroll
+      for (int r = 0; r < LPTILE; ++r) {
+        rm.ks[r] = t.ks[r];
+        rm.kz[r] = t.kz[r];
+        rm.vs[r] = t.vs[r];
+        rm.vz[r] = t.vz[r];
+        rm.valid[r] = v0;
+      }
     } else {
-      mt.ks[1] = mt.ks[0];
-      mt.kz[1] = mt.kz[0];
-      mt.vs[1] = mt.vs[0];
-      mt.vz[1] = mt.vz[0];
-      mt.valid[1] = mt.valid[0];
+      const float ks0 = readlane_f32(my_ks, k), kz0 = readlane_f32(my_kz, k);
+      const float vs0 = readlane_f32(my_vs, k), vz0 = readlane_f32(my_vz, k);
+      float ks1 = ks0, kz1 = kz0, vs1 = vs0, vz1 = vz0;
+      bool v1 = v0;
+      if constexpr (SUB) {
+        ks1 = readlane_f32(my_ks1, k);
+        kz1 = readlane_f32(my_kz1, k);
+        vs1 = readlane_f32(my_vs1, k);
+        vz1 = readlane_f32(my_vz1, k);
+        v1 = readlane_i32(my_base1, k) >= 0;
+      }
+#pragma unroll
+      for (int r = 0; r < LPTILE; ++r) {
+        const bool hi = SUB && ((r * RPL + g) >> 3) != 0;  // second 8-token half; compile-time for DP >= 128
+        rm.ks[r] = hi ? ks1 : ks0;
+        rm.kz[r] = hi ? kz1 : kz0;
+        rm.vs[r] = hi ? vs1 : vs0;
+        rm.vz[r] = hi ? vz1 : vz0;
+        rm.valid[r] = hi ? v1 : v0;
+      }
     }
-    consume_tile<DP, QT>(st, t, q, qsum, mt, (first + W * k) * kTile, len, g);
+    consume_tile<DP, QT>(st, t, q, qsum, rm, (first + W * k) * kTile, len, g);
   };
   // two register buffers: tile k+1 is in flight while tile k is consumed
   TileRegs<DP> ta, tb2;
@@ -686,19 +756,20 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
 // ---- host launchers --------------------------------------------------------------------------
 
 // Tiled path: head_dim a multiple of 16 up to 256 (served by the 64-, 128- or 256-dim
-// register layout), quant blocks a multiple of 8 tokens, whole quant blocks per page.  Quant
-// blocks that are an odd multiple of 8 take the sub-tile form of the kernel.
+// register layout), quant blocks a multiple of 8 tokens with whole quant blocks per page, or
+// one parameter set per token (quant block 1) on contiguous rows or pages of 16k tokens.
 static bool tiled_path(int head_dim, int page_size, int quant_block) {
-  return head_dim >= 16 && head_dim <= 256 && head_dim % 16 == 0 && quant_block >= 8 && quant_block % 8 == 0 &&
-         page_size > 0 && page_size % quant_block == 0;
+  if (head_dim < 16 || head_dim > 256 || head_dim % 16 != 0 || page_size <= 0) return false;
+  if (quant_block == 1) return page_size == 1 || page_size % kTile == 0;  // contiguous rows, or 16-token pages
+  return quant_block % 8 == 0 && page_size % quant_block == 0;
 }
 
-template <typename QT, bool PAGED, bool SUB>
+template <typename QT, bool PAGED, int QM>
 static void launch_tiled(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
   switch (padded_head_dim(p.head_dim)) {
-    case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, SUB>), grid, block, 0, st, p); break;
-    case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, SUB>), grid, block, 0, st, p); break;
-    default: hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, SUB>), grid, block, 0, st, p); break;
+    case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, QM>), grid, block, 0, st, p); break;
+    case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, QM>), grid, block, 0, st, p); break;
+    default: hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, QM>), grid, block, 0, st, p); break;
   }
 }
 
@@ -707,10 +778,12 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
   const dim3 block(kWave * waves_per_block);
   if (tiled) {
     const dim3 grid((unsigned)((int64_t)p.rows * p.max_splits));
-    if (p.quant_block % kTile != 0)
-      launch_tiled<QT, PAGED, true>(p, grid, block, st);
+    if (p.quant_block == 1)
+      launch_tiled<QT, PAGED, kQmToken>(p, grid, block, st);
+    else if (p.quant_block % kTile != 0)
+      launch_tiled<QT, PAGED, kQmSub>(p, grid, block, st);
     else
-      launch_tiled<QT, PAGED, false>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmBlock>(p, grid, block, st);
   } else {
     const int64_t waves = (int64_t)p.rows * p.max_splits;
     const dim3 grid((unsigned)((waves + waves_per_block - 1) / waves_per_block));
@@ -834,7 +907,7 @@ extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_va
   if (num_pages <= 0) return set_error(FS_ERR_INVALID, "num_pages must be positive");
   if (page_size <= 0 || quant_block <= 0 || page_size % quant_block != 0)
     return set_error(FS_ERR_INVALID, "page_size must be a positive multiple of the quant block");
-  if (tiled && num_pages * heads * (page_size / kTile) > 0x7fffffffLL)
+  if (tiled && num_pages * heads * (quant_block == 1 ? page_size : page_size / kTile) > 0x7fffffffLL)
     return set_error(FS_ERR_INVALID, "page store too large for 32-bit tile ids");
   return launch_decode<true>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }

@@ -371,6 +371,65 @@ append_tokens_vec_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageSto
   }
 }
 
+// Symmetric absmax INT8, one scale per token row: scale = max(absmax / 127, 1e-8),
+// q = clamp(rint(x / scale), -127, 127), stored in the affine layout with block 1 and zero
+// point 128 (dequantized value (q + 128 - 128) * scale).  LPR = head_dim / 8 lanes per row,
+// each holding 8 contiguous values; 64 / LPR rows per wave.
+template <int LPR, typename XT>
+__global__ void __launch_bounds__(256)
+quantize_sym_rows_kernel(const XT* x, int64_t rows, int D, int8_t* values, float* scale, int16_t* zero) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int64_t r = wave * (kWave / LPR) + lane / LPR;
+  const int c = lane % LPR;
+  const bool live = r < rows;
+  float v[8];
+  if (live) {
+    load8(x + (size_t)r * D + 8 * c, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  }
+  float am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+#pragma unroll
+  for (int off = 1; off < LPR; off <<= 1) am = fmaxf(am, __shfl_xor(am, off, kWave));
+  const float s = fmaxf(am / 127.0f, 1.0e-8f);
+  if (!live) return;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float qv = fminf(fmaxf(__builtin_rintf(v[i] / s), -127.0f), 127.0f);
+    w[i / 4] |= ((uint32_t)(int)qv & 0xffu) << (8 * (i % 4));
+  }
+  *(uint2*)(values + (size_t)r * D + 8 * c) = make_uint2(w[0], w[1]);
+  if (c == 0) {
+    scale[r] = s;
+    zero[r] = 128;
+  }
+}
+
+// Same quantizer, one wave per row, for head dims that are not a power-of-two multiple of 8.
+template <typename XT>
+__global__ void __launch_bounds__(256)
+quantize_sym_rows_generic_kernel(const XT* x, int64_t rows, int D, int8_t* values, float* scale, int16_t* zero) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (r >= rows) return;
+  const XT* src = x + (size_t)r * D;
+  float am = 0.0f;
+  for (int d = lane; d < D; d += kWave) am = fmaxf(am, fabsf(to_f32(src[d])));
+  am = wave_max(am);
+  const float s = fmaxf(am / 127.0f, 1.0e-8f);
+  for (int d = lane; d < D; d += kWave)
+    values[(size_t)r * D + d] = (int8_t)(int)fminf(fmaxf(__builtin_rintf(to_f32(src[d]) / s), -127.0f), 127.0f);
+  if (lane == 0) {
+    scale[r] = s;
+    zero[r] = 128;
+  }
+}
+
 template <typename OT>
 __global__ void __launch_bounds__(256)
 dequantize_kernel(const int8_t* values, const float* scale, const int16_t* zero, int64_t outer, int nb, int bs,
@@ -589,4 +648,42 @@ extern "C" int fs_append_tokens_i8(const void* k_new, const void* v_new, int src
 #undef FS_APPEND_IDX
 #undef FS_APPEND
   return check_launch("append_tokens");
+}
+
+template <typename XT>
+static int launch_quantize_sym(const XT* x, int64_t rows, int D, int8_t* values, float* scale, int16_t* zero,
+                               hipStream_t st) {
+  const int lpr = D / 8;
+  const bool vec = D % 8 == 0 && lpr <= kWave && (lpr & (lpr - 1)) == 0 && ((uintptr_t)x % 16) == 0 &&
+                   ((uintptr_t)values % 8) == 0;
+  const dim3 block(256);
+  if (!vec) {
+    hipLaunchKernelGGL(quantize_sym_rows_generic_kernel<XT>, wave_grid(rows), block, 0, st, x, rows, D, values, scale, zero);
+    return check_launch("quantize_symmetric_per_token");
+  }
+  const int64_t waves = (rows + (kWave / lpr) - 1) / (kWave / lpr);
+  const dim3 grid = wave_grid(waves);
+  switch (lpr) {
+    case 1: hipLaunchKernelGGL((quantize_sym_rows_kernel<1, XT>), grid, block, 0, st, x, rows, D, values, scale, zero); break;
+    case 2: hipLaunchKernelGGL((quantize_sym_rows_kernel<2, XT>), grid, block, 0, st, x, rows, D, values, scale, zero); break;
+    case 4: hipLaunchKernelGGL((quantize_sym_rows_kernel<4, XT>), grid, block, 0, st, x, rows, D, values, scale, zero); break;
+    case 8: hipLaunchKernelGGL((quantize_sym_rows_kernel<8, XT>), grid, block, 0, st, x, rows, D, values, scale, zero); break;
+    case 16: hipLaunchKernelGGL((quantize_sym_rows_kernel<16, XT>), grid, block, 0, st, x, rows, D, values, scale, zero); break;
+    case 32: hipLaunchKernelGGL((quantize_sym_rows_kernel<32, XT>), grid, block, 0, st, x, rows, D, values, scale, zero); break;
+    default: hipLaunchKernelGGL((quantize_sym_rows_kernel<64, XT>), grid, block, 0, st, x, rows, D, values, scale, zero); break;
+  }
+  return check_launch("quantize_symmetric_per_token");
+}
+
+extern "C" int fs_quantize_sym_i8(const void* x, int x_dtype, int64_t rows, int head_dim, int8_t* values,
+                                  float* scale, int16_t* zero, void* stream) {
+  if (rows <= 0 || head_dim <= 0) return set_error(FS_ERR_INVALID, "quantize_symmetric: sizes must be positive");
+  if (!x || !values || !scale || !zero) return set_error(FS_ERR_INVALID, "quantize_symmetric: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  switch (x_dtype) {
+    case FS_F32: return launch_quantize_sym((const float*)x, rows, head_dim, values, scale, zero, st);
+    case FS_F16: return launch_quantize_sym((const __half*)x, rows, head_dim, values, scale, zero, st);
+    case FS_BF16: return launch_quantize_sym((const __hip_bfloat16*)x, rows, head_dim, values, scale, zero, st);
+    default: return set_error(FS_ERR_INVALID, "quantize_symmetric: dtype code must be 0, 1 or 2");
+  }
 }

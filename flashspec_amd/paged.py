@@ -21,7 +21,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from .quant import QuantizedTensor, dequantize_int8_per_block, estimate_quantized_bytes, quantize_int8_per_block
+from .quant import (QuantizedTensor, dequantize_int8_per_block, estimate_quantized_bytes, quantize_int8_per_block,
+                    quantize_int8_symmetric_per_token)
 
 _SCALE_FLOOR = 1.0e-8  # quantizing an all-zero block gives int8 -128, scale fp32(1e-8), zero 0
 
@@ -407,13 +408,20 @@ class PagedKVCache:
     @classmethod
     def from_dense(cls, k: torch.Tensor, v: torch.Tensor, block_size: int = 16, *,
                    lengths: torch.Tensor | None = None, block_table_pattern: str = "contiguous",
-                   layout_seed: int = 0) -> "PagedKVCache":
+                   layout_seed: int = 0, kv_format: str = "affine_block") -> "PagedKVCache":
         """Build a paged cache from dense ``[batch, heads, seq, dim]`` K/V (paged.py:302-419).
 
         Layouts: ``contiguous`` (batch-major), ``shuffled``/``random`` (seeded
         ``torch.randperm`` on k's device) and ``interleaved`` (logical-page-major).
         Only the physical placement changes; the logical K/V is identical.
+
+        ``kv_format`` (not in the reference): ``affine_block`` quantizes each page per head
+        as the reference does; ``symmetric_token`` stores symmetric absmax INT8 with one scale
+        per token (``quantize_int8_symmetric_per_token``, quant block 1).
         """
+
+        if kv_format not in ("affine_block", "symmetric_token"):
+            raise ValueError("kv_format must be affine_block or symmetric_token")
 
         if k.ndim != 4 or v.ndim != 4:
             raise ValueError("k and v must be [batch, heads, seq_len, head_dim]")
@@ -444,7 +452,10 @@ class PagedKVCache:
             if bool((effective_lengths < 0).any().item()) or bool((effective_lengths > seq_len).any().item()):
                 raise ValueError("lengths must lie in [0, seq_len]")
 
-        if k.device.type == "cuda":
+        if kv_format == "symmetric_token":
+            k_quant = quantize_int8_symmetric_per_token(cls._physical_pages(k, block_size, perm))
+            v_quant = quantize_int8_symmetric_per_token(cls._physical_pages(v, block_size, perm))
+        elif k.device.type == "cuda":
             k_quant = cls._quantize_pages(k, block_size, perm, total)
             v_quant = cls._quantize_pages(v, block_size, perm, total)
         else:

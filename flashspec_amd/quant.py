@@ -105,6 +105,49 @@ def quantize_int8_per_block(x: torch.Tensor, block_size: int = 16) -> QuantizedT
     return _quantize_portable(x, block_size)
 
 
+def _quantize_sym_portable(x: torch.Tensor) -> QuantizedTensor:
+    xf = x.detach().to(torch.float32)
+    lead, seq, dim = tuple(xf.shape[:-2]), xf.shape[-2], xf.shape[-1]
+    scale = (xf.abs().amax(dim=-1, keepdim=True) / 127.0).clamp_min(1.0e-8)
+    codes = torch.round(xf / scale).clamp(-127, 127).to(torch.int8)
+    zero = torch.full((*lead, seq, 1, 1), 128, dtype=torch.int16, device=xf.device)
+    return QuantizedTensor(codes.reshape(*lead, seq, 1, dim), scale.reshape(*lead, seq, 1, 1), zero, 1,
+                           tuple(x.shape))
+
+
+def _quantize_sym_hip(x: torch.Tensor) -> QuantizedTensor:
+    lib = _lib.require()
+    xd = x.detach()
+    if xd.dtype not in _lib.DTYPE_CODE:
+        xd = xd.to(torch.float32)
+    xd = xd.contiguous()
+    lead, seq, dim = tuple(xd.shape[:-2]), int(xd.shape[-2]), int(xd.shape[-1])
+    rows = math.prod(lead) * seq if lead else seq
+    dev = xd.device
+    values = torch.empty((*lead, seq, 1, dim), dtype=torch.int8, device=dev)
+    scale = torch.empty((*lead, seq, 1, 1), dtype=torch.float32, device=dev)
+    zero = torch.empty((*lead, seq, 1, 1), dtype=torch.int16, device=dev)
+    if rows > 0:
+        _lib.check(lib.fs_quantize_sym_i8(xd.data_ptr(), _lib.dtype_code(xd.dtype), rows, dim, values.data_ptr(),
+                                          scale.data_ptr(), zero.data_ptr(), _lib.stream_ptr(dev)))
+    return QuantizedTensor(values, scale, zero, 1, tuple(x.shape))
+
+
+def quantize_int8_symmetric_per_token(x: torch.Tensor) -> QuantizedTensor:
+    """Symmetric absmax INT8 with one fp32 scale per token row (per head).
+
+    ``scale = max(absmax(row) / 127, 1e-8)``, ``q = clamp(round(x / scale), -127, 127)``.
+    Not in the reference (its quantizer is ``quantize_int8_per_block``); returned in the
+    same affine layout with ``block_size = 1`` and zero point 128, so ``dequantize_int8_per_block``,
+    the portable attention paths and the HIP decode kernels all read it unchanged.
+    """
+
+    _validate_block_tensor(x, 1)
+    if x.device.type == "cuda":
+        return _quantize_sym_hip(x)
+    return _quantize_sym_portable(x)
+
+
 def _dequantize_hip(q: QuantizedTensor, dtype: torch.dtype | None) -> torch.Tensor:
     lib = _lib.require()
     lead = tuple(q.original_shape[:-2])

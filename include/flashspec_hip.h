@@ -134,6 +134,18 @@ int fs_quantize_i8(const void* x, int x_dtype, int64_t outer, int seq_len, int h
  * reference src/flashspec/quant.py:168-204.
  *   out [outer, seq_len, head_dim] out_dtype
  */
+/*
+ * Symmetric absmax INT8 with one fp32 scale per token row (per head):
+ *   scale = max(absmax(row) / 127, 1e-8), q = clamp(rint(x / scale), -127, 127)
+ * written in the affine layout of fs_quantize_i8 with block size 1 and zero point 128, so
+ * every decode entry point reads it (the tiled kernels with one parameter set per token).
+ *   x [rows, head_dim] x_dtype; values [rows, head_dim] int8 (= q); scale / zero [rows].
+ * No counterpart in the reference, whose quantizer is the affine per-block one: a second
+ * KV format offered beside it (symmetric absmax INT8, one fp32 scale per token per head).
+ */
+int fs_quantize_sym_i8(const void* x, int x_dtype, int64_t rows, int head_dim,
+                       int8_t* values, float* scale, int16_t* zero, void* stream);
+
 int fs_dequantize_i8(const int8_t* values, const float* scale, const int16_t* zero,
                      int64_t outer, int n_blocks, int block_size, int head_dim, int seq_len,
                      void* out, int out_dtype, void* stream);

@@ -83,3 +83,32 @@ def estimate_quantized_bytes(q: OracleQuant) -> int:
     """values + 4 B per scale + 2 B per zero point (quant.py:232-247)."""
 
     return int(q.values.size + q.scale.size * 4 + q.zero_point.size * 2)
+
+
+def quantize_int8_symmetric_per_token(x: np.ndarray) -> OracleQuant:
+    """Symmetric absmax INT8, one fp32 scale per token row (per head): a KV format offered
+    beside the reference's.  Not a reference function (the reference quantizer is the affine
+    per-block one above); pinned by closed forms and a brute-force nearest-code check in
+    tests/test_oracle.py.
+
+        scale = max(absmax(row) / 127, 1e-8)      (float32 division)
+        q     = clamp(rint(x / scale), -127, 127) (float32 division, half-even)
+
+    Expressed in the affine layout with block_size 1 and zero point 128, so that
+    dequantize_int8_per_block gives q * scale and every affine consumer reads it unchanged.
+    """
+
+    if x.ndim < 2:
+        raise ValueError("x needs sequence and feature axes")
+    if x.shape[-1] <= 0 or x.shape[-2] <= 0:
+        raise ValueError("sequence and feature axes must be non-empty")
+    original_shape = tuple(int(s) for s in x.shape)
+    xf = np.asarray(x, dtype=F32)
+    am = np.abs(xf).max(axis=-1, keepdims=True)
+    scale = np.maximum(am / F32(127.0), SCALE_FLOOR).astype(F32)
+    q = np.clip(np.rint(xf / scale), F32(-127), F32(127)).astype(np.int8)
+    lead = xf.shape[:-2]
+    S, D = xf.shape[-2], xf.shape[-1]
+    values = q.reshape(*lead, S, 1, D)
+    zero = np.full((*lead, S, 1, 1), 128, dtype=np.int16)
+    return OracleQuant(values, scale.reshape(*lead, S, 1, 1), zero, 1, original_shape)

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+import flashspec_amd as fa
 import flashspec_amd.triton_fused as triton_fused
 import flashspec_amd.triton_paged as triton_paged
 from flashspec_amd import (
@@ -254,6 +255,30 @@ def test_portable_allocator_is_bit_exact_with_reference_vectors():
             alloc.release_request(int(rid))
         assert np.array_equal(np_of(alloc.k_quant.values), d[f"s{step}_kvalues"]), step
         assert np.array_equal(np_of(alloc.v_quant.scale).view(np.uint32), d[f"s{step}_vscale"].view(np.uint32))
+
+
+def test_symmetric_per_token_format_portable_paths():
+    """quantize_int8_symmetric_per_token is bit-exact with the oracle, and the block-1 affine
+    layout it returns flows through fused, paged (all layouts) and dequantize unchanged."""
+
+    g = torch.Generator().manual_seed(21)
+    k = torch.randn((2, 3, 37, 32), generator=g) * 2
+    v = torch.randn((2, 3, 37, 32), generator=g)
+    q = torch.randn((2, 3, 32), generator=g)
+    kq = fa.quantize_int8_symmetric_per_token(k)
+    ref = oq.quantize_int8_symmetric_per_token(k.numpy())
+    assert np.array_equal(kq.values.numpy(), ref.values)
+    assert np.array_equal(kq.scale.numpy().view(np.uint32), ref.scale.view(np.uint32))
+    assert np.array_equal(kq.zero_point.numpy(), ref.zero_point)
+    assert np.array_equal(fa.dequantize_int8_per_block(kq).numpy(), oq.dequantize_int8_per_block(ref))
+    vq = fa.quantize_int8_symmetric_per_token(v)
+    fused = fa.fused_dequant_attention_triton(q, kq, vq)
+    for pattern in ("contiguous", "shuffled", "interleaved"):
+        cache = fa.PagedKVCache.from_dense(k, v, 16, block_table_pattern=pattern, kv_format="symmetric_token")
+        assert cache.k_quant.block_size == 1
+        torch.testing.assert_close(fa.paged_quant_attention_triton(q, cache), fused, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        fa.PagedKVCache.from_dense(k, v, 16, kv_format="fp8")
 
 
 def test_validation_errors_match_reference_classes():

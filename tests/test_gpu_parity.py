@@ -120,6 +120,94 @@ def test_quantize_unaligned_source_bit_exact():
     assert np.array_equal(np_of(zero), ref.zero_point.reshape(2, nb))
 
 
+@pytest.mark.parametrize("shape,dtype", [
+    ((2, 4, 37, 128), torch.float16),
+    ((3, 50, 64), torch.bfloat16),
+    ((2, 2, 33, 96), torch.float32),     # 12 lanes per row: the one-wave-per-row kernel
+    ((1, 1, 7, 256), torch.float16),
+    ((2, 3, 19, 40), torch.float16),
+])
+def test_symmetric_per_token_quantize_bit_exact(shape, dtype):
+    announce(f"symmetric per-token quantize shape={shape} dtype={dtype}")
+    x = randn(shape, seed=sum(shape) + 1, dtype=dtype) * 4.0
+    q = fa.quantize_int8_symmetric_per_token(x.to(DEV))
+    ref = oq.quantize_int8_symmetric_per_token(np_of(x.to(torch.float32)))
+    sync()
+    assert_quant_equal(from_qt(q), ref, str(shape))
+    assert q.block_size == 1
+
+
+def _sym_fused_case(B, H, S, D, seed, q_dtype):
+    q = randn((B, H, D), seed, q_dtype)
+    k = randn((B, H, S, D), seed + 1)
+    v = randn((B, H, S, D), seed + 2)
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,H,S,D,q_dtype,lengths", [
+    (2, 4, 129, 128, torch.float16, [129, 100]),      # ragged last tile of a contiguous row
+    (4, 32, 2048, 128, torch.float16, None),          # config 1 shape
+    (2, 2, 77, 64, torch.bfloat16, [77, 5]),
+    (1, 2, 300, 256, torch.float16, None),
+    (2, 3, 50, 96, torch.float32, [50, 17]),
+])
+def test_fused_symmetric_per_token_matches_oracle(B, H, S, D, q_dtype, lengths):
+    announce(f"fused symmetric per-token B{B} H{H} S{S} D{D} {q_dtype} lengths={lengths}")
+    q, k, v = _sym_fused_case(B, H, S, D, B * 7 + S, q_dtype)
+    kq = fa.quantize_int8_symmetric_per_token(k.to(DEV))
+    vq = fa.quantize_int8_symmetric_per_token(v.to(DEV))
+    lens = None if lengths is None else torch.tensor(lengths, dtype=torch.int64)
+    got, stats = fa.fused_dequant_attention_triton(q.to(DEV), kq, vq, lengths=None if lens is None else lens.to(DEV),
+                                                   return_stats=True)
+    sync()
+    assert stats["tiled_path"] == 1.0
+    rk = oq.quantize_int8_symmetric_per_token(np_of(k.float()))
+    rv = oq.quantize_int8_symmetric_per_token(np_of(v.float()))
+    ref = oa.fused_dequant_attention(np_of(q.float()), rk, rv, None if lens is None else np_of(lens))
+    assert_attention_close(got, ref, q_dtype, "fused symmetric")
+
+
+@pytest.mark.parametrize("layout,page", [("contiguous", 16), ("shuffled", 16), ("interleaved", 32)])
+def test_paged_symmetric_per_token_matches_oracle(layout, page):
+    announce(f"paged symmetric per-token {layout} page{page}")
+    B, H, S, D = 3, 4, 300, 128
+    q, k, v = _sym_fused_case(B, H, S, D, 40 + page, torch.float16)
+    lens = torch.tensor([300, 31, 16], dtype=torch.int64)
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=page, lengths=lens.to(DEV),
+                                       block_table_pattern=layout, layout_seed=5, kv_format="symmetric_token")
+    got, stats = fa.paged_quant_attention_triton(q.to(DEV), cache, return_stats=True)
+    sync()
+    assert stats["tiled_path"] == 1.0
+    assert_attention_close(got, oracle_paged_attention(q, cache), torch.float16, "paged symmetric")
+    rk = oq.quantize_int8_symmetric_per_token(np_of(k.float()))
+    rv = oq.quantize_int8_symmetric_per_token(np_of(v.float()))
+    ref = oa.fused_dequant_attention(np_of(q.float()), rk, rv, np_of(lens))
+    assert_attention_close(got, ref, torch.float16, "paged symmetric vs contiguous oracle")
+
+
+def test_config2_symmetric_per_token_split_k(monkeypatch):
+    """B8 H32 S4096 D128, symmetric per-token INT8, num_splits=4 with the fp32 LSE merge;
+    rows of two requests checked against the oracle."""
+
+    announce("config 2 symmetric per-token split-K B8 H32 S4096 D128")
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", "4")
+    B, H, S, D = 8, 32, 4096, 128
+    g = torch.Generator(device=DEV)
+    g.manual_seed(4)
+    q = torch.randn((B, H, D), generator=g, device=DEV, dtype=torch.float16)
+    k = torch.randn((B, H, S, D), generator=g, device=DEV, dtype=torch.float16)
+    v = torch.randn((B, H, S, D), generator=g, device=DEV, dtype=torch.float16)
+    kq, vq = fa.quantize_int8_symmetric_per_token(k), fa.quantize_int8_symmetric_per_token(v)
+    got, stats = fa.fused_dequant_attention_triton(q, kq, vq, return_stats=True)
+    sync()
+    assert stats["num_splits"] == 4.0
+    for b in (0, 5):
+        rk = oq.quantize_int8_symmetric_per_token(np_of(k[b:b + 1].float()))
+        rv = oq.quantize_int8_symmetric_per_token(np_of(v[b:b + 1].float()))
+        ref = oa.fused_dequant_attention(np_of(q[b:b + 1].float()), rk, rv, None)
+        assert_attention_close(got[b:b + 1], ref, torch.float16, f"request {b}")
+
+
 # ---- paged cache construction, append, allocator ----------------------------------------------
 
 @pytest.mark.parametrize("layout", ["contiguous", "shuffled", "interleaved"])

@@ -79,6 +79,42 @@ def test_quantize_codes_are_nearest_with_two_roundings():
             assert code == min(max(want, 0), 255)
 
 
+def test_symmetric_per_token_closed_forms():
+    """Symmetric absmax INT8 per token: the extreme of each row maps to +-127, zero rows keep
+    the 1e-8 floor, negation negates the codes, and the layout reads back through the affine
+    dequantizer as q * scale."""
+
+    x = np.array([[[[0.5, -2.0, 1.0, 0.0], [0.0, 0.0, 0.0, 0.0], [3.0, 3.0, -3.0, 1.5]]]], F32)
+    q = oq.quantize_int8_symmetric_per_token(x)
+    assert q.block_size == 1 and q.values.shape == (1, 1, 3, 1, 4) and (q.zero_point == 128).all()
+    s = q.scale.reshape(3)
+    assert s[0] == F32(2.0) / F32(127.0) and s[1] == F32(1e-8) and s[2] == F32(3.0) / F32(127.0)
+    codes = q.values.reshape(3, 4).astype(np.int64)
+    assert codes[0, 1] == -127 and codes[2, 0] == 127 and codes[2, 2] == -127
+    assert (codes[1] == 0).all()
+    qn = oq.quantize_int8_symmetric_per_token(-x)
+    assert (qn.values.astype(np.int64) == -q.values.astype(np.int64)).all()
+    deq = oq.dequantize_int8_per_block(q)
+    assert np.array_equal(deq.reshape(3, 4), (codes.astype(F32) * s[:, None]).astype(F32))
+
+
+def test_symmetric_per_token_codes_are_nearest():
+    """Brute force: every code is the half-even nearest integer of fl(x / s), |code| <= 127."""
+
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((2, 3, 17, 24)) * rng.uniform(0.01, 50, (2, 3, 17, 1))).astype(F32)
+    q = oq.quantize_int8_symmetric_per_token(x)
+    s = q.scale.reshape(2, 3, 17, 1)
+    assert np.array_equal(s, np.maximum(np.abs(x).max(-1, keepdims=True) / F32(127.0), F32(1e-8)))
+    t = (x / s).astype(F32)
+    codes = q.values.reshape(2, 3, 17, 24).astype(np.int64)
+    for val, code in zip(t.ravel()[::5], codes.ravel()[::5]):
+        lo = math.floor(val)
+        frac = float(val) - lo
+        want = lo + 1 if frac > 0.5 or (frac == 0.5 and lo % 2 == 1) else lo
+        assert code == min(max(want, -127), 127)
+
+
 def test_dequantize_error_bound_and_padding_crop():
     rng = np.random.default_rng(5)
     x = rng.standard_normal((2, 3, 19, 16)).astype(F32)
