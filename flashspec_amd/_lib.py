@@ -37,6 +37,12 @@ _SIGNATURES = {
          c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float,
          c_int, c_int, c_int, c_void_p],
     ),
+    "fs_tree_verify_i8": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
+         c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int,
+         c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+    ),
     "fs_combine_splits": (
         c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p]
     ),

@@ -13,7 +13,7 @@ from __future__ import annotations
 import sys
 
 import flashspec_amd
-from flashspec_amd import attention, paged, quant, runtime, serving, triton_fused, triton_paged, triton_utils
+from flashspec_amd import attention, paged, quant, runtime, serving, tree, triton_fused, triton_paged, triton_utils
 
 _SUBMODULES = {
     "attention": attention,
@@ -21,6 +21,7 @@ _SUBMODULES = {
     "quant": quant,
     "runtime": runtime,
     "serving": serving,
+    "tree": tree,
     "triton_fused": triton_fused,
     "triton_paged": triton_paged,
     "triton_utils": triton_utils,

@@ -56,7 +56,13 @@ struct DecodeParams {
   int page_size;
   int split_tiles, max_splits;
   float qk_scale;  // sm_scale * log2(e)
+  // Tree verification: nq query rows per (request, head), rows ordered (b, n, h); the decode
+  // writes split partials for every row (force_partials) for the tree-tail merge.
+  int nq;
+  int force_partials;
 };
+
+__device__ __forceinline__ int queries_per_head(const DecodeParams& p) { return p.nq > 1 ? p.nq : 1; }
 
 // The dispatcher hands workgroups to the XCDs round-robin (workgroup i to XCD i % 8).
 // decode_unit renumbers them so that XCD x owns heads [x*H/8, (x+1)*H/8) of every batch
@@ -77,18 +83,23 @@ struct Unit {
 };
 
 __device__ __forceinline__ Unit decode_unit(const DecodeParams& p, int bid, int units) {
-  // pos = ((x * batch + b) * hg + hh) * max_splits + split with head h = x * hg + hh; with
-  // hg = heads (heads not divisible by 8) the same formula is the plain order, x = 0.
+  // pos = (((x * batch + b) * hg + hh) * nq + n) * max_splits + split with head h = x * hg + hh
+  // and row = (b * nq + n) * heads + h; with hg = heads (heads not divisible by 8) the same
+  // formula is the plain order, x = 0.  The nq query rows of one (request, head) are adjacent
+  // on one XCD, so they read the same pages at the same time (L2 hits after the first).
   const bool grouped = p.heads % kXcds == 0;
   const int hg = grouped ? p.heads / kXcds : p.heads;
+  const int nq = queries_per_head(p);
   const int pos = grouped ? xcd_chunked_unit(bid, units) : bid;
-  const int batch = p.rows / p.heads;
+  const int batch = p.rows / (p.heads * nq);
   const int split = pos % p.max_splits;
   int t = pos / p.max_splits;
+  const int n = t % nq;
+  t /= nq;
   const int hh = t % hg;
   t /= hg;
   const int b = t % batch, x = t / batch;
-  return {b * p.heads + x * hg + hh, split};
+  return {(b * nq + n) * p.heads + x * hg + hh, split};
 }
 
 __device__ __forceinline__ int row_length(const int64_t* lengths, int b, int seq_len) {
@@ -421,8 +432,8 @@ decode_rows_kernel(const DecodeParams p) {
   const int W = blockDim.x / kWave;
   const Unit unit = decode_unit(p, blockIdx.x, gridDim.x);
   const int row = unit.row, split = unit.split;
-  const int b = row / p.heads;
-  const int h = row - b * p.heads;
+  const int b = row / (p.heads * queries_per_head(p));
+  const int h = row % p.heads;
   // Lane k of wave w resolves the wave's k-th tile, first + W*k, once: base index (-1 = not
   // backed by a page or past the row) and (key scale * qk_scale, key zero, value scale,
   // value zero).  Waves take tiles w, w+W, w+2W, ...: all waves of all workgroups sweep
@@ -604,7 +615,7 @@ decode_rows_kernel(const DecodeParams p) {
       L = fmaf(s_ml[2 * ww + 1], e, L);
       a = fmaf(s_acc[ww * DP + d], e, a);
     }
-    if (nsplit == 1) {
+    if (nsplit == 1 && !p.force_partials) {
       ((QT*)p.out)[(size_t)row * D + d] = from_f32<QT>(L > 0.f ? a / L : 0.f);
 #ifdef FS_TRACE_WG
       if (d == 0) ((uint64_t*)p.part_ml)[(size_t)blockIdx.x * 20 + 19] = __builtin_amdgcn_s_memrealtime();
@@ -630,8 +641,8 @@ decode_generic_kernel(const DecodeParams p) {
   if (wave >= p.rows * p.max_splits) return;
   const int row = wave / p.max_splits;
   const int split = wave - row * p.max_splits;
-  const int b = row / p.heads;
-  const int h = row - b * p.heads;
+  const int b = row / (p.heads * queries_per_head(p));
+  const int h = row % p.heads;
   const int D = p.head_dim;
   const int len = row_length(p.lengths, b, p.seq_len);
   const int nsplit = row_splits(len, p.split_tiles);
@@ -687,7 +698,7 @@ decode_generic_kernel(const DecodeParams p) {
     m = mn;
   }
 
-  if (nsplit == 1) {
+  if (nsplit == 1 && !p.force_partials) {
     QT* o = (QT*)p.out + (size_t)row * D;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -750,6 +761,78 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
   for (int c = 0; c < 4; ++c) {
     const int d = lane + c * kWave;
     if (d < D) o[d] = from_f32<OT>(L > 0.f ? acc[c] / L : 0.f);
+  }
+}
+
+// ---- tree verification tail -------------------------------------------------------------------
+
+// Row = (b * nq + n) * heads + h of a tree verification: merges the prefix partial states the
+// decode kernel left for the row (one per split the row's length needs), then walks node n's
+// path to the root over the draft K/V (parents[b, a]; a well-formed parent precedes its child,
+// -1 ends the path, at most nq steps) with the same online softmax, and writes the output.
+template <typename QT, typename DT>
+__global__ void __launch_bounds__(256)
+tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* lengths, const QT* q, const DT* dk,
+                 const DT* dv, const int64_t* parents, QT* out, int rows, int heads, int nq, int D, int seq_len,
+                 int split_tiles, int max_splits, float qk_scale) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+  if (row >= rows) return;
+  const int h = row % heads;
+  const int bn = row / heads;
+  const int b = bn / nq;
+  const int n = bn - b * nq;
+  const int nsplit = row_splits(row_length(lengths, b, seq_len), split_tiles);
+  const float* ml = part_ml + (size_t)row * max_splits * 2;
+  const float* pacc = part_acc + (size_t)row * max_splits * D;
+  float M = kNegBig;
+  for (int sp = lane; sp < nsplit; sp += kWave) M = fmaxf(M, ml[2 * sp]);
+  M = wave_max(M);
+  float L = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float wgt = fast_exp2(ml[2 * sp] - M);
+    L = fmaf(ml[2 * sp + 1], wgt, L);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = lane + c * kWave;
+      if (d < D) acc[c] = fmaf(pacc[(size_t)sp * D + d], wgt, acc[c]);
+    }
+  }
+  float qv[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int d = lane + c * kWave;
+    qv[c] = d < D ? to_f32(q[(size_t)row * D + d]) : 0.f;
+  }
+  int a = n;
+  for (int step = 0; step < nq && a >= 0; ++step) {
+    const size_t kr = (((size_t)b * nq + a) * heads + h) * D;
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = lane + c * kWave;
+      if (d < D) dot = fmaf(qv[c], to_f32(dk[kr + d]), dot);
+    }
+    const float sc = wave_sum(dot) * qk_scale;
+    const float mn = fmaxf(M, sc);
+    const float alpha = fast_exp2(M - mn), pr = fast_exp2(sc - mn);
+    L = L * alpha + pr;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = lane + c * kWave;
+      const float v = d < D ? to_f32(dv[kr + d]) : 0.f;
+      acc[c] = fmaf(pr, v, acc[c] * alpha);
+    }
+    M = mn;
+    const int64_t pa = parents[(size_t)b * nq + a];
+    a = (pa >= 0 && pa < a) ? (int)pa : -1;
+  }
+  QT* o = out + (size_t)row * D;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int d = lane + c * kWave;
+    if (d < D) o[d] = from_f32<QT>(L > 0.f ? acc[c] / L : 0.f);
   }
 }
 
@@ -827,7 +910,7 @@ static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, 
   if ((int64_t)p.rows * p.max_splits > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "decode grid too large");
   if (!p.q || !p.kv[0] || !p.kv[1] || !p.sc[0] || !p.sc[1] || !p.zp[0] || !p.zp[1] || !p.out)
     return set_error(FS_ERR_INVALID, "null tensor pointer");
-  if (p.max_splits > 1) {
+  if (p.max_splits > 1 || p.force_partials) {
     const int64_t need = fs_decode_workspace_bytes(p.rows, p.max_splits, p.head_dim);
     if (workspace_bytes < need || p.part_acc == nullptr)
       return set_error(FS_ERR_INVALID, "split-K workspace too small (" + std::to_string(workspace_bytes) +
@@ -877,14 +960,15 @@ extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_va
   return launch_decode<false>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }
 
-extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
-                                  const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
-                                  const int16_t* v_zero, const void* block_table, int table_index_bytes,
-                                  int64_t table_cols, const int64_t* lengths, void* out, void* workspace,
-                                  int64_t workspace_bytes, int batch, int heads, int head_dim, int64_t num_pages,
-                                  int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
-                                  int max_splits, int waves_per_block, void* stream) {
-  DecodeParams p{};
+// Parameters and checks shared by the paged decode and the tree verification entry points;
+// `rows_per_request` = query rows per request (heads * nodes).
+static int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_values, const float* k_scale,
+                        const int16_t* k_zero, const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                        const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
+                        void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads,
+                        int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
+                        float sm_scale, int split_tiles, int max_splits, int waves_per_block) {
+  p = DecodeParams{};
   p.q = q;
   p.kv[0] = k_values; p.kv[1] = v_values;
   p.sc[0] = k_scale; p.sc[1] = v_scale;
@@ -892,14 +976,16 @@ extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_va
   p.table = block_table; p.table_cols = table_cols; p.table_bytes = table_index_bytes;
   p.lengths = lengths;
   p.out = out;
-  p.rows = batch * heads; p.heads = heads; p.head_dim = head_dim;
+  p.rows = batch * nq * heads; p.heads = heads; p.head_dim = head_dim;
+  p.nq = nq;
   p.seq_len = max_seq_len;
   p.num_pages = num_pages; p.page_size = page_size; p.quant_block = quant_block;
   p.split_tiles = split_tiles; p.max_splits = max_splits;
   p.qk_scale = sm_scale * kLog2e;
-  if (batch <= 0) return set_error(FS_ERR_INVALID, "batch must be positive");
+  if (batch <= 0 || nq <= 0) return set_error(FS_ERR_INVALID, "batch and nodes must be positive");
+  if ((int64_t)batch * nq * heads > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "too many query rows");
   bind_workspace(p, workspace);
-  const bool tiled = tiled_path(head_dim, page_size, quant_block);
+  tiled = tiled_path(head_dim, page_size, quant_block);
   if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes)) return rc;
   if (!block_table || !lengths) return set_error(FS_ERR_INVALID, "block_table and lengths are required");
   if (table_index_bytes != 4 && table_index_bytes != 8) return set_error(FS_ERR_INVALID, "table_index_bytes must be 4 or 8");
@@ -909,6 +995,23 @@ extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_va
     return set_error(FS_ERR_INVALID, "page_size must be a positive multiple of the quant block");
   if (tiled && num_pages * heads * (quant_block == 1 ? page_size : page_size / kTile) > 0x7fffffffLL)
     return set_error(FS_ERR_INVALID, "page store too large for 32-bit tile ids");
+  return FS_OK;
+}
+
+extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                  const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                  const int16_t* v_zero, const void* block_table, int table_index_bytes,
+                                  int64_t table_cols, const int64_t* lengths, void* out, void* workspace,
+                                  int64_t workspace_bytes, int batch, int heads, int head_dim, int64_t num_pages,
+                                  int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
+                                  int max_splits, int waves_per_block, void* stream) {
+  DecodeParams p;
+  bool tiled = false;
+  if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
+                            table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, 1, heads,
+                            head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
+                            max_splits, waves_per_block))
+    return rc;
   return launch_decode<true>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }
 
@@ -939,4 +1042,58 @@ extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, 
     default: return set_error(FS_ERR_INVALID, "out dtype code must be 0, 1 or 2");
   }
   return check_launch("combine_splits_kernel");
+}
+
+template <typename QT, typename DT>
+static void launch_tree_tail(const DecodeParams& p, const void* dk, const void* dv, const int64_t* parents, int nq,
+                             hipStream_t st) {
+  const dim3 grid((unsigned)(((int64_t)p.rows + 3) / 4)), block(256);
+  hipLaunchKernelGGL((tree_tail_kernel<QT, DT>), grid, block, 0, st, p.part_ml, p.part_acc, p.lengths,
+                     (const QT*)p.q, (const DT*)dk, (const DT*)dv, parents, (QT*)p.out, p.rows, p.heads, nq,
+                     p.head_dim, p.seq_len, p.split_tiles, p.max_splits, p.qk_scale);
+}
+
+template <typename QT>
+static int launch_tree_tail_q(const DecodeParams& p, const void* dk, const void* dv, int draft_dtype,
+                              const int64_t* parents, int nq, hipStream_t st) {
+  switch (draft_dtype) {
+    case FS_F32: launch_tree_tail<QT, float>(p, dk, dv, parents, nq, st); break;
+    case FS_F16: launch_tree_tail<QT, __half>(p, dk, dv, parents, nq, st); break;
+    case FS_BF16: launch_tree_tail<QT, __hip_bfloat16>(p, dk, dv, parents, nq, st); break;
+    default: return set_error(FS_ERR_INVALID, "draft dtype code must be 0, 1 or 2");
+  }
+  return check_launch("tree_verify_tail");
+}
+
+extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                 const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                 const int16_t* v_zero, const void* block_table, int table_index_bytes,
+                                 int64_t table_cols, const int64_t* lengths, const void* draft_k, const void* draft_v,
+                                 int draft_dtype, const int64_t* parents, void* out, void* workspace,
+                                 int64_t workspace_bytes, int batch, int nodes, int heads, int head_dim,
+                                 int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
+                                 int split_tiles, int max_splits, int waves_per_block, void* stream) {
+  DecodeParams p;
+  bool tiled = false;
+  if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
+                            table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, nodes,
+                            heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
+                            max_splits, waves_per_block))
+    return rc;
+  if (!draft_k || !draft_v || !parents) return set_error(FS_ERR_INVALID, "tree verify: null draft or parents pointer");
+  if (draft_dtype != FS_F32 && draft_dtype != FS_F16 && draft_dtype != FS_BF16)
+    return set_error(FS_ERR_INVALID, "draft dtype code must be 0, 1 or 2");
+  p.force_partials = 1;
+  const int64_t need = fs_decode_workspace_bytes(p.rows, p.max_splits, p.head_dim);
+  if (workspace_bytes < need || p.part_acc == nullptr)
+    return set_error(FS_ERR_INVALID, "tree verify workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                                         std::to_string(need) + " bytes)");
+  hipStream_t st = (hipStream_t)stream;
+  if (int rc = launch_decode<true>(p, q_dtype, tiled, waves_per_block, st)) return rc;
+  switch (q_dtype) {
+    case FS_F32: return launch_tree_tail_q<float>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
+    case FS_F16: return launch_tree_tail_q<__half>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
+    case FS_BF16: return launch_tree_tail_q<__hip_bfloat16>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
+    default: return set_error(FS_ERR_INVALID, "q dtype code must be 0 (f32), 1 (f16) or 2 (bf16)");
+  }
 }

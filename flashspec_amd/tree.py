@@ -1,0 +1,159 @@
+"""Speculative-decoding tree verification over a paged INT8 prefix.
+
+The reference plans this kernel (doc/TODO.MD:186-237) without implementing it.  Semantics:
+request b carries N draft nodes in topological order with ``parents[b, n]`` in [-1, n)
+(-1: the node hangs off the last committed token).  Node n attends to the committed prefix
+(tokens [0, lengths[b]) of a ``PagedKVCache``) and to the draft tokens on its own root path
+(n and its ancestors), never to siblings or other branches.  Draft K/V are unquantized.
+
+On GPU, ``fs_tree_verify_i8`` runs the paged decode kernel with one query row per node
+(the N rows of one request and head are scheduled together on one XCD, so the prefix pages
+they share are read from HBM once) and a tail kernel that merges the prefix partial states
+with the path tokens.  On CPU the dense tree-mask formulation runs in torch.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from . import _lib
+from .paged import PagedKVCache
+from .quant import build_compression_stats
+from .triton_utils import launch_plan
+
+__all__ = ["tree_verify_attention", "validate_parents", "path_mask"]
+
+
+def validate_parents(parents: torch.Tensor, batch: int, nodes: int) -> torch.Tensor:
+    """Host copy of ``parents`` after checking it is a forest in topological order."""
+
+    if parents.ndim != 2 or tuple(parents.shape) != (batch, nodes):
+        raise ValueError(f"parents must be [batch, nodes] = [{batch}, {nodes}]")
+    if parents.dtype not in (torch.int32, torch.int64):
+        raise ValueError("parents must be an int32/int64 tensor")
+    host = parents.detach().to("cpu", torch.int64)
+    idx = torch.arange(nodes, dtype=torch.int64)[None, :]
+    if bool((host < -1).any()) or bool((host >= idx).any()):
+        raise ValueError("parents[b, n] must lie in [-1, n): cycles, forward edges and orphans are invalid")
+    return host
+
+
+def path_mask(parents: torch.Tensor) -> torch.Tensor:
+    """``mask[b, n, j]`` = draft node j lies on node n's root path (``parents`` validated)."""
+
+    batch, nodes = parents.shape
+    mask = torch.zeros((batch, nodes, nodes), dtype=torch.bool)
+    for n in range(nodes):
+        mask[:, n, n] = True
+        par = parents[:, n]
+        has = par >= 0
+        if bool(has.any()):
+            mask[has, n] |= mask[has, par[has]]
+    return mask
+
+
+def _validate(q, cache, draft_k, draft_v):
+    if not isinstance(cache, PagedKVCache):
+        raise ValueError("cache must be a PagedKVCache")
+    if q.ndim != 4:
+        raise ValueError("q must be [batch, nodes, heads, head_dim]")
+    if draft_k.shape != q.shape or draft_v.shape != q.shape:
+        raise ValueError("draft_k and draft_v must match q's [batch, nodes, heads, head_dim]")
+    batch, nodes, heads, head_dim = (int(s) for s in q.shape)
+    if batch != cache.batch_size or heads != cache.num_heads or head_dim != cache.head_dim:
+        raise ValueError("q does not match the cache's batch, heads or head_dim")
+    if nodes <= 0:
+        raise ValueError("need at least one draft node")
+    if head_dim > 256:
+        raise ValueError("head_dim must be <= 256")
+    return batch, nodes, heads, head_dim
+
+
+def _portable(q, cache, draft_k, draft_v, parents_host):
+    batch, nodes, heads, head_dim = q.shape
+    kp, vp = cache.to_dense()  # [B, H, S, D] float32
+    S = kp.shape[2]
+    dev = kp.device
+    keys = torch.cat([kp, draft_k.to(dev, torch.float32).permute(0, 2, 1, 3)], dim=2)
+    vals = torch.cat([vp, draft_v.to(dev, torch.float32).permute(0, 2, 1, 3)], dim=2)
+    allowed = torch.zeros((batch, nodes, S + nodes), dtype=torch.bool, device=dev)
+    allowed[:, :, :S] = torch.arange(S, device=dev)[None, None, :] < cache.lengths.to(dev)[:, None, None]
+    allowed[:, :, S:] = path_mask(parents_host).to(dev)
+    scores = torch.einsum("bnhd,bhkd->bhnk", q.to(dev, torch.float32), keys) / math.sqrt(head_dim)
+    scores = scores.masked_fill(~allowed[:, None], torch.finfo(torch.float32).min)
+    out = torch.einsum("bhnk,bhkd->bnhd", torch.softmax(scores, dim=-1), vals)
+    return out.to(q.dtype)
+
+
+def _hip(q, cache, draft_k, draft_v, parents_host, dims):
+    batch, nodes, heads, head_dim = dims
+    lib = _lib.require()
+    dev = q.device
+    kq, vq = cache.k_quant, cache.v_quant
+    if draft_k.device != dev or draft_v.device != dev or cache.block_table.device != dev:
+        raise RuntimeError("q, draft K/V and the cache must be on the same GPU")
+    if q.dtype not in _lib.DTYPE_CODE or draft_k.dtype not in _lib.DTYPE_CODE or draft_v.dtype != draft_k.dtype:
+        raise ValueError("q and draft K/V must be float32, float16 or bfloat16 (draft_k and draft_v alike)")
+    q_c, dk_c, dv_c = q.contiguous(), draft_k.contiguous(), draft_v.contiguous()
+    table = cache.block_table.contiguous()
+    lengths = cache.lengths.to(torch.int64).contiguous()
+    parents_dev = parents_host.to(dev).contiguous()
+    rows = batch * nodes * heads
+    max_seq_len = int(cache.max_seq_len)
+    tiled, waves, split_tiles, max_splits, block_n = launch_plan(max_seq_len, rows, head_dim, int(cache.block_size),
+                                                                 int(kq.block_size), dev)
+    ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q_c)
+    _lib.check(lib.fs_tree_verify_i8(
+        q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kq.values.data_ptr(), kq.scale.data_ptr(),
+        kq.zero_point.data_ptr(), vq.values.data_ptr(), vq.scale.data_ptr(), vq.zero_point.data_ptr(),
+        table.data_ptr(), table.element_size(), int(table.shape[1]), lengths.data_ptr(), dk_c.data_ptr(),
+        dv_c.data_ptr(), _lib.dtype_code(dk_c.dtype), parents_dev.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+        ws_bytes, batch, nodes, heads, head_dim, int(kq.values.shape[0]), int(cache.block_size), int(kq.block_size),
+        max_seq_len, 1.0 / math.sqrt(head_dim), split_tiles, max_splits, waves, _lib.stream_ptr(dev)))
+    plan = {"num_splits": float(max_splits), "split_tiles": float(split_tiles), "num_warps": float(waves),
+            "block_n": float(block_n), "tiled_path": float(tiled)}
+    return out, plan
+
+
+def tree_verify_attention(q: torch.Tensor, cache: PagedKVCache, draft_k: torch.Tensor, draft_v: torch.Tensor,
+                          parents: torch.Tensor, return_stats: bool = False) -> Any:
+    """Attention of every draft node over the prefix and its root path.
+
+    ``q``, ``draft_k``, ``draft_v``: ``[batch, nodes, heads, head_dim]``; ``parents``:
+    ``[batch, nodes]`` int with ``parents[b, n]`` in [-1, n).  Returns ``[batch, nodes, heads,
+    head_dim]`` in q's dtype (and a stats dict with ``return_stats``).  ``ValueError`` for a
+    malformed tree or shapes, ``RuntimeError`` for device mismatches or a GPU tensor without
+    the HIP library.
+    """
+
+    dims = _validate(q, cache, draft_k, draft_v)
+    parents_host = validate_parents(parents, dims[0], dims[1])
+    if q.device.type == "cuda":
+        out, plan = _hip(q, cache, draft_k, draft_v, parents_host, dims)
+        materializes = False
+    else:
+        out, plan = _portable(q, cache, draft_k, draft_v, parents_host), {}
+        materializes = True
+    if not return_stats:
+        return out
+    batch, nodes, heads, head_dim = dims
+    dense_bytes = 2 * batch * heads * int(cache.max_seq_len) * head_dim * q.element_size()
+    stats = build_compression_stats(dense_bytes, cache.estimated_bytes(), materializes_dense_kv=materializes,
+                                    tree_nodes=float(nodes), tree_depth=float(_depth(parents_host)), **plan)
+    return out, stats
+
+
+def _depth(parents_host: torch.Tensor) -> int:
+    batch, nodes = parents_host.shape
+    depth = torch.ones((batch, nodes), dtype=torch.int64)
+    for n in range(nodes):
+        par = parents_host[:, n]
+        has = par >= 0
+        if bool(has.any()):
+            depth[has, n] = depth[has, par[has]] + 1
+    return int(depth.max().item()) if nodes else 0

@@ -110,6 +110,32 @@ int fs_paged_decode_i8(const void* q, int q_dtype,
                        int split_tiles, int max_splits, int waves_per_block, void* stream);
 
 /*
+ * Speculative-decoding tree verification over a paged INT8 prefix.  Request b has `nodes`
+ * draft nodes in topological order; node n attends to the prefix tokens [0, lengths[b]) of
+ * the paged cache and to the draft tokens on its path to the root (n, parents[b, n],
+ * parents[b, parents[b, n]], ... until -1).  The prefix part runs as the paged decode with one
+ * query row per node, rows ordered (b, n, h), leaving split partials in `workspace`; a tail
+ * kernel merges them with the path tokens (fp32 online softmax) and writes `out`.
+ *   q, out          [batch, nodes, heads, head_dim]  q_dtype
+ *   draft_k/draft_v [batch, nodes, heads, head_dim]  draft_dtype (unquantized)
+ *   parents         [batch, nodes] int64, parents[b, n] in [-1, n) (the caller validates;
+ *                   the kernel ends a path at any entry outside that range)
+ *   workspace       >= fs_decode_workspace_bytes(batch*nodes*heads, max_splits, head_dim)
+ *   other arguments as for fs_paged_decode_i8 (split plan for batch*nodes*heads rows).
+ * No counterpart in the reference, which plans this kernel (doc/TODO.MD:186-237) without
+ * implementing it; a chain of nodes reduces to paged decode over prefix + path.
+ */
+int fs_tree_verify_i8(const void* q, int q_dtype,
+                      const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                      const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                      const void* block_table, int table_index_bytes, int64_t table_cols,
+                      const int64_t* lengths, const void* draft_k, const void* draft_v, int draft_dtype,
+                      const int64_t* parents, void* out, void* workspace, int64_t workspace_bytes,
+                      int batch, int nodes, int heads, int head_dim, int64_t num_pages,
+                      int page_size, int quant_block, int max_seq_len, float sm_scale,
+                      int split_tiles, int max_splits, int waves_per_block, void* stream);
+
+/*
  * Merge the per-split partial states a decode call with max_splits > 1 left in
  * `workspace`, for the rows that needed more than one split.  Replaces _combine_splits_kernel
  * (reference src/flashspec/triton_fused.py:445-503).  `lengths` may be NULL;

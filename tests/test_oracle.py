@@ -17,6 +17,7 @@ import pytest
 from oracle import attention as oa
 from oracle import paged as op
 from oracle import quant as oq
+from oracle import tree as ot
 from tests._helpers import assert_quant_equal, golden_cache, golden_quant, load_npz
 
 F32 = np.float32
@@ -263,3 +264,54 @@ def test_allocator_reuses_lowest_released_page():
     alloc.release_request(20)
     alloc.add_request(30, np.zeros((1, 2, 1, 8), F32), np.zeros((1, 2, 1, 8), F32))
     assert alloc.requests[30]["blocks"][0] == released == 2
+
+
+# ---- tree verification -------------------------------------------------------------------------
+
+def _tree_case(B, H, S, D, N, seed, lengths):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((B, H, S, D)).astype(F32)
+    v = rng.standard_normal((B, H, S, D)).astype(F32)
+    cache = op.from_dense(k, v, 4, lengths=np.asarray(lengths, dtype=np.int64))
+    q = rng.standard_normal((B, N, H, D)).astype(F32)
+    dk = rng.standard_normal((B, N, H, D)).astype(F32)
+    dv = rng.standard_normal((B, N, H, D)).astype(F32)
+    return q, cache, dk, dv
+
+
+def test_tree_mask_formulation_matches_f64_parent_walk():
+    q, cache, dk, dv = _tree_case(2, 2, 13, 8, 6, 1, [13, 5])
+    parents = np.array([[-1, 0, 0, 1, 3, -1], [-1, -1, 1, 2, 0, 4]])
+    got = ot.tree_verify_attention(q, cache, dk, dv, parents)
+    ref = ot.tree_verify_f64_loops(q, cache, dk, dv, parents)
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-6)
+
+
+def test_tree_chain_and_star_equal_attention_on_concatenated_kv():
+    """Chain: node n sees prefix + draft[0..n]; star: prefix + draft[n] only.  Both against
+    reference_attention on explicitly concatenated K/V (a formulation without any mask)."""
+
+    B, H, S, D, N = 2, 3, 11, 8, 4
+    q, cache, dk, dv = _tree_case(B, H, S, D, N, 2, [11, 7])
+    kp, vp = op.to_dense(cache)
+    chain = np.array([[-1, 0, 1, 2]] * B)
+    star = np.array([[-1, -1, -1, -1]] * B)
+    got_chain = ot.tree_verify_attention(q, cache, dk, dv, chain)
+    got_star = ot.tree_verify_attention(q, cache, dk, dv, star)
+    for b in range(B):
+        L = int(cache.lengths[b])
+        for n in range(N):
+            for sel, got in (([*range(n + 1)], got_chain), ([n], got_star)):
+                keys = np.concatenate([kp[b:b + 1, :, :L], dk[b:b + 1, sel].transpose(0, 2, 1, 3)], axis=2)
+                vals = np.concatenate([vp[b:b + 1, :, :L], dv[b:b + 1, sel].transpose(0, 2, 1, 3)], axis=2)
+                ref = oa.reference_attention(q[b:b + 1, n], keys, vals)
+                np.testing.assert_allclose(got[b:b + 1, n], ref, rtol=2e-5, atol=2e-6)
+
+
+def test_tree_rejects_malformed_parents():
+    for bad in ([[0, -1]], [[-1, 1]], [[-1, 2, 0]], [[-2, -1]]):
+        with pytest.raises(ValueError):
+            ot.validate_parents(np.array(bad))
+    assert ot.path_mask(np.array([[-1, 0, 0, 2]]))[0].tolist() == [
+        [True, False, False, False], [True, True, False, False], [True, False, True, False],
+        [True, False, True, True]]
