@@ -51,10 +51,11 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--layout", default="contiguous", choices=["contiguous", "shuffled", "interleaved"])
-    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "serving", "shapes"],
+    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "serving", "shapes", "tree"],
                     help="full: the JSON line; paged: only the timed paged steps (for rocprofv3); "
                          "copy: a plain 256 MiB device copy, to calibrate rocprofv3 byte counters; "
-                         "serving: only the 64-request serving decode step; shapes: the SHAPES table")
+                         "serving: only the 64-request serving decode step; shapes: the SHAPES table; "
+                         "tree: tree verification for 1-16 draft nodes")
     return ap.parse_args()
 
 
@@ -305,6 +306,57 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
     return out
 
 
+TREE_CASES = ((4, (1, 4, 8, 16, 64)), (8, (16,)))  # (requests, draft-node counts)
+
+
+def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
+    """tree_verify_attention over B4 and B8 H32 S4096 D128 paged prefixes (16-token pages, fp16
+    q and drafts) for random draft trees of 1-64 nodes, 3 rotated input sets.  Algorithmic
+    bytes read the shared prefix once per (request, head) plus the drafts, q, output and parents;
+    ``vs_decode`` = time / the time of one single-query paged decode over the same prefix.  The
+    tree topology is a host tensor, as a drafter produces it (checked, then copied through
+    pinned memory inside the timed call)."""
+
+    out = []
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    gp = torch.Generator().manual_seed(17)
+    for nb, node_counts in TREE_CASES:
+        caches = []
+        for _ in range(ROTATE):
+            k = torch.randn((nb, H, S, D), generator=g, device=dev, dtype=torch.float16)
+            v = torch.randn((nb, H, S, D), generator=g, device=dev, dtype=torch.float16)
+            caches.append(fa.PagedKVCache.from_dense(k, v, block_size=PAGE))
+            del k, v
+        q1 = [torch.randn((nb, H, D), generator=g, device=dev, dtype=torch.float16) for _ in range(ROTATE)]
+        dec_ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(q1[i % ROTATE], caches[i % ROTATE]),
+                           steps, warmup)
+        prefix = algorithmic_bytes([S] * nb, H, D, PAGE) - 2 * nb * H * D * 2
+        for n in node_counts:
+            par = torch.full((nb, n), -1, dtype=torch.int64)
+            for j in range(1, n):
+                par[:, j] = torch.randint(-1, j, (nb,), generator=gp)
+            ins = [tuple(torch.randn((nb, n, H, D), generator=g, device=dev, dtype=torch.float16) for _ in range(3))
+                   for _ in range(ROTATE)]
+            ms = time_loop(torch, lambda i: fa.tree_verify_attention(ins[i % ROTATE][0], caches[i % ROTATE],
+                                                                     ins[i % ROTATE][1], ins[i % ROTATE][2], par),
+                           steps, warmup)
+            _, st = fa.tree_verify_attention(ins[0][0], caches[0], ins[0][1], ins[0][2], par, return_stats=True)
+            nbytes = prefix + 4 * nb * n * H * D * 2 + nb * n * 8
+            row = {"workload": f"tree verify B{nb} H{H} S{S} D{D}, {n} draft nodes", "nodes": n,
+                   "depth": st["tree_depth"], "us_per_call": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                   "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                   "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
+                   "single_query_decode_us": round(dec_ms * 1e3, 2), "vs_decode": round(ms / dec_ms, 3),
+                   "num_splits": st["num_splits"], "waves": st["num_warps"], "mfma_prefix": st["mfma_prefix"]}
+            out.append(row)
+            print(json.dumps({"mode": "tree", **row}), flush=True)
+            del ins
+        del caches
+        torch.cuda.empty_cache()
+    return out
+
+
 def load_traffic(config_key: str):
     if not PMC_SUMMARY.exists():
         return None
@@ -338,6 +390,9 @@ def main() -> int:
         return copy_calibration(torch, args.steps)
     if args.mode == "shapes":
         shapes_bench(torch, fa, dev, min(args.steps, 100), min(args.warmup, 10))
+        return 0
+    if args.mode == "tree":
+        tree_bench(torch, fa, dev, min(args.steps, 100), min(args.warmup, 10))
         return 0
     if args.mode == "serving":
         print(json.dumps({"mode": "serving", **serving_step_bench(torch, fa, dev, args.steps, args.warmup)}),

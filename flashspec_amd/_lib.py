@@ -41,8 +41,9 @@ _SIGNATURES = {
         c_int,
         [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
          c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int,
-         c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+         c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_void_p],
     ),
+    "fs_tree_mfma_path": (c_int, [c_int, c_int, c_int]),
     "fs_combine_splits": (
         c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p]
     ),

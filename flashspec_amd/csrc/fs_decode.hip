@@ -20,104 +20,10 @@
 // src/flashspec/triton_paged.py:119-299 (masking of tokens past the row length and
 // of unallocated pages; a row with no valid token writes zeros, triton_utils.py:181-186).
 
-#include "fs_common.h"
+#include "fs_paged.h"
 
 namespace fs {
 
-constexpr int kMaxWaves = 16;       // waves per workgroup on the tiled path
-constexpr int kMaxTilesPerWave = 64;  // per split and wave: one metadata lane per tile
-constexpr float kRescaleSlack = 8.0f;  // running max may lag the true max by 2^8
-constexpr int kXcds = 8;  // MI355X: accelerator complex dies, each with its own L2
-
-// How a tile finds its quantization parameters (scale / zero point).
-enum QuantMode : int {
-  kQmBlock = 0,  // quant block a multiple of 16 tokens: one entry per tile
-  kQmSub = 1,    // quant block an odd multiple of 8 tokens (or 8-token pages): one per 8-token half
-  kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
-};
-
-struct DecodeParams {
-  const void* q;
-  const int8_t* kv[2];
-  const float* sc[2];
-  const int16_t* zp[2];
-  const void* table;
-  int64_t table_cols;
-  int table_bytes;
-  const int64_t* lengths;
-  void* out;
-  float* part_ml;   // [rows, max_splits, 2] (max in log2 units, denominator)
-  float* part_acc;  // [rows, max_splits, D]
-  int rows, heads, head_dim;
-  int seq_len;
-  int64_t num_pages;
-  int n_blocks;
-  int quant_block;
-  int page_size;
-  int split_tiles, max_splits;
-  float qk_scale;  // sm_scale * log2(e)
-  // Tree verification: nq query rows per (request, head), rows ordered (b, n, h); the decode
-  // writes split partials for every row (force_partials) for the tree-tail merge.
-  int nq;
-  int force_partials;
-};
-
-__device__ __forceinline__ int queries_per_head(const DecodeParams& p) { return p.nq > 1 ? p.nq : 1; }
-
-// The dispatcher hands workgroups to the XCDs round-robin (workgroup i to XCD i % 8).
-// decode_unit renumbers them so that XCD x owns heads [x*H/8, (x+1)*H/8) of every batch
-// (all their splits): an XCD then streams an H/8-head slab of each page instead of one
-// 2 KiB head slice of every page, while every XCD still gets the same share of each
-// request, so ragged lengths stay balanced across XCDs.  Measured on one MI355X against the
-// plain order: B8 H32 S4096 paged 46.1 vs 46.9 us, 64 ragged requests 616 vs 624 us.
-// Giving each XCD whole batches instead is as fast on uniform lengths but 1.35x slower
-// when lengths descend across the batch.  Heads not divisible by 8 keep the plain order.
-__device__ __forceinline__ int xcd_chunked_unit(int bid, int units) {
-  const int per = units / kXcds, rem = units - per * kXcds;
-  const int x = bid % kXcds, k = bid / kXcds;
-  return x * per + min(x, rem) + k;
-}
-
-struct Unit {
-  int row, split;
-};
-
-__device__ __forceinline__ Unit decode_unit(const DecodeParams& p, int bid, int units) {
-  // pos = (((x * batch + b) * hg + hh) * nq + n) * max_splits + split with head h = x * hg + hh
-  // and row = (b * nq + n) * heads + h; with hg = heads (heads not divisible by 8) the same
-  // formula is the plain order, x = 0.  The nq query rows of one (request, head) are adjacent
-  // on one XCD, so they read the same pages at the same time (L2 hits after the first).
-  const bool grouped = p.heads % kXcds == 0;
-  const int hg = grouped ? p.heads / kXcds : p.heads;
-  const int nq = queries_per_head(p);
-  const int pos = grouped ? xcd_chunked_unit(bid, units) : bid;
-  const int batch = p.rows / (p.heads * nq);
-  const int split = pos % p.max_splits;
-  int t = pos / p.max_splits;
-  const int n = t % nq;
-  t /= nq;
-  const int hh = t % hg;
-  t /= hg;
-  const int b = t % batch, x = t / batch;
-  return {(b * nq + n) * p.heads + x * hg + hh, split};
-}
-
-__device__ __forceinline__ int row_length(const int64_t* lengths, int b, int seq_len) {
-  if (lengths == nullptr) return seq_len;
-  const int64_t l = lengths[b];
-  return (int)(l < 0 ? 0 : (l < (int64_t)seq_len ? l : (int64_t)seq_len));
-}
-
-__device__ __forceinline__ int row_splits(int len, int split_tiles) {
-  const int tiles = (len + kTile - 1) / kTile;
-  const int n = (tiles + split_tiles - 1) / split_tiles;
-  return n < 1 ? 1 : n;
-}
-
-__device__ __forceinline__ int64_t table_entry(const DecodeParams& p, int b, int64_t col) {
-  if (p.table_bytes == 4) return (int64_t)((const int32_t*)p.table)[(int64_t)b * p.table_cols + col];
-  return ((const int64_t*)p.table)[(int64_t)b * p.table_cols + col];
-}
 
 // ---- tiled path -------------------------------------------------------------------------------
 
@@ -218,66 +124,6 @@ __device__ __forceinline__ void axpy16_u8(float* acc, float wgt, uint4 raw) {
   }
 }
 
-// Sequence tile `tile` (16 tokens) of (b, h): `data` indexes 16*D-byte tiles of the value
-// store, `meta` the scale / zero entries (one per quant block; a quant block is a multiple
-// of 16 tokens on this path, so a tile never straddles two).  data = -1 when the tile is
-// not backed by an allocated page.
-struct TileIndex {
-  int data, meta;
-};
-
-template <bool PAGED>
-__device__ __forceinline__ TileIndex tile_index(const DecodeParams& p, int b, int h, int row, int tile) {
-  const int tpq = p.quant_block / kTile;  // tiles per quant block
-  if constexpr (PAGED) {
-    const int tpp = p.page_size / kTile;
-    const int lp = tile / tpp;
-    const int sub = tile - lp * tpp;
-    if (lp >= p.table_cols) return {-1, 0};
-    const int64_t pg = table_entry(p, b, lp);
-    if (pg < 0 || pg >= p.num_pages) return {-1, 0};
-    const int64_t ph = pg * p.heads + h;
-    return {(int)(ph * tpp + sub), (int)(ph * (tpp / tpq) + sub / tpq)};
-  } else {
-    return {row * p.n_blocks * tpq + tile, row * p.n_blocks + tile / tpq};
-  }
-}
-
-// 8-token sub-tile `u` of (b, h) for stores whose quant block or page is 8 tokens (an odd
-// multiple of 8): `data` in units of 8*D value bytes, `meta` the scale / zero entry of the
-// quant block holding it; data = -1 when not backed by an allocated page.
-template <bool PAGED>
-__device__ __forceinline__ TileIndex sub_index(const DecodeParams& p, int b, int h, int row, int u) {
-  const int token0 = 8 * u;
-  if constexpr (PAGED) {
-    const int lp = token0 / p.page_size;
-    const int within = token0 - lp * p.page_size;
-    if (lp >= p.table_cols) return {-1, 0};
-    const int64_t pg = table_entry(p, b, lp);
-    if (pg < 0 || pg >= p.num_pages) return {-1, 0};
-    const int64_t ph = pg * p.heads + h;
-    return {(int)(ph * (p.page_size / 8) + within / 8), (int)(ph * (p.page_size / p.quant_block) + within / p.quant_block)};
-  } else {
-    return {row * p.n_blocks * (p.quant_block / 8) + u, row * p.n_blocks + token0 / p.quant_block};
-  }
-}
-
-// Token mode: first token of tile `tile` of (b, h) in the value store (units of D bytes, the
-// same index as its per-token scale / zero), -1 when not backed by an allocated page.
-template <bool PAGED>
-__device__ __forceinline__ int token_index(const DecodeParams& p, int b, int h, int row, int tile) {
-  if constexpr (PAGED) {
-    const int tpp = p.page_size / kTile;
-    const int lp = tile / tpp;
-    const int sub = tile - lp * tpp;
-    if (lp >= p.table_cols) return -1;
-    const int64_t pg = table_entry(p, b, lp);
-    if (pg < 0 || pg >= p.num_pages) return -1;
-    return (int)((pg * p.heads + h) * p.page_size + sub * kTile);
-  } else {
-    return row * p.n_blocks + tile * kTile;
-  }
-}
 
 // Register layout for head dims up to DP (64, 128 or 256): DP/16 lanes share a token row,
 // each holding 16 of its dims; a head_dim D < DP (a multiple of 16) leaves the lanes with
@@ -292,14 +138,6 @@ struct TileRegs {
   float ks[LPTILE], kz[LPTILE], vs[LPTILE], vz[LPTILE];  // per-row parameters (token mode only)
 };
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-// K/V bytes are read exactly once: non-temporal loads keep them from displacing the
-// cache lines the rest of the GPU is using (measured: ~7% faster than plain loads).
-__device__ __forceinline__ uint4 stream_load(const uint4* p) {
-  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 // Loads one tile.  An unbacked or out-of-range tile (base < 0) loads tile 0 of the store
 // instead and its tokens are masked by the caller: a branch around the loads would make
@@ -767,9 +605,11 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
 // ---- tree verification tail -------------------------------------------------------------------
 
 // Row = (b * nq + n) * heads + h of a tree verification: merges the prefix partial states the
-// decode kernel left for the row (one per split the row's length needs), then walks node n's
-// path to the root over the draft K/V (parents[b, a]; a well-formed parent precedes its child,
-// -1 ends the path, at most nq steps) with the same online softmax, and writes the output.
+// prefix kernel left for the row (one per split the row's length needs), then attends to the
+// draft tokens on node n's path to the root (parents[b, a]; a parent outside [0, a) ends the
+// path, at most nq steps) with the same online softmax, and writes the output.  With nq <= 64
+// the request's parents are loaded once, one per lane, and the path is walked in registers;
+// its tokens are then taken four at a time, so their K/V rows load together.
 template <typename QT, typename DT>
 __global__ void __launch_bounds__(256)
 tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* lengths, const QT* q, const DT* dk,
@@ -782,6 +622,11 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
   const int bn = row / heads;
   const int b = bn / nq;
   const int n = bn - b * nq;
+  int pl = -1;  // this lane's node's parent, sanitized (nq <= 64)
+  if (nq <= kWave && lane < nq) {
+    const int64_t pa = parents[(size_t)b * nq + lane];
+    pl = (pa >= 0 && pa < lane) ? (int)pa : -1;
+  }
   const int nsplit = row_splits(row_length(lengths, b, seq_len), split_tiles);
   const float* ml = part_ml + (size_t)row * max_splits * 2;
   const float* pacc = part_acc + (size_t)row * max_splits * D;
@@ -790,6 +635,7 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
   M = wave_max(M);
   float L = 0.f;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
   for (int sp = 0; sp < nsplit; ++sp) {
     const float wgt = fast_exp2(ml[2 * sp] - M);
     L = fmaf(ml[2 * sp + 1], wgt, L);
@@ -805,28 +651,78 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
     const int d = lane + c * kWave;
     qv[c] = d < D ? to_f32(q[(size_t)row * D + d]) : 0.f;
   }
-  int a = n;
-  for (int step = 0; step < nq && a >= 0; ++step) {
-    const size_t kr = (((size_t)b * nq + a) * heads + h) * D;
-    float dot = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = lane + c * kWave;
-      if (d < D) dot = fmaf(qv[c], to_f32(dk[kr + d]), dot);
+  if (nq <= kWave) {
+    uint64_t path = 0;
+    for (int a = n, step = 0; step < nq && a >= 0; ++step) {
+      path |= 1ull << a;
+      a = __builtin_amdgcn_readlane(pl, a);
     }
-    const float sc = wave_sum(dot) * qk_scale;
-    const float mn = fmaxf(M, sc);
-    const float alpha = fast_exp2(M - mn), pr = fast_exp2(sc - mn);
-    L = L * alpha + pr;
+    while (path) {
+      int idx[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = lane + c * kWave;
-      const float v = d < D ? to_f32(dv[kr + d]) : 0.f;
-      acc[c] = fmaf(pr, v, acc[c] * alpha);
+      for (int i = 0; i < 4; ++i) {
+        idx[i] = path ? __builtin_ctzll(path) : -1;
+        path &= path - 1;  // no-op once empty
+      }
+      float kx[4][4], vx[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const size_t kr = (((size_t)b * nq + (idx[i] < 0 ? 0 : idx[i])) * heads + h) * D;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int d = lane + c * kWave;
+          const bool ok = idx[i] >= 0 && d < D;
+          kx[i][c] = ok ? to_f32(dk[kr + d]) : 0.f;
+          vx[i][c] = ok ? to_f32(dv[kr + d]) : 0.f;
+        }
+      }
+      float sc[4];
+      float mn = M;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float dot = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dot = fmaf(qv[c], kx[i][c], dot);
+        sc[i] = wave_sum(dot) * qk_scale;
+        if (idx[i] >= 0) mn = fmaxf(mn, sc[i]);
+      }
+      const float alpha = fast_exp2(M - mn);
+      L *= alpha;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pr = idx[i] >= 0 ? fast_exp2(sc[i] - mn) : 0.f;
+        L += pr;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = fmaf(pr, vx[i][c], acc[c]);
+      }
+      M = mn;
     }
-    M = mn;
-    const int64_t pa = parents[(size_t)b * nq + a];
-    a = (pa >= 0 && pa < a) ? (int)pa : -1;
+  } else {
+    int a = n;
+    for (int step = 0; step < nq && a >= 0; ++step) {
+      const size_t kr = (((size_t)b * nq + a) * heads + h) * D;
+      float dot = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = lane + c * kWave;
+        if (d < D) dot = fmaf(qv[c], to_f32(dk[kr + d]), dot);
+      }
+      const float sc = wave_sum(dot) * qk_scale;
+      const float mn = fmaxf(M, sc);
+      const float alpha = fast_exp2(M - mn), pr = fast_exp2(sc - mn);
+      L = L * alpha + pr;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = lane + c * kWave;
+        const float v = d < D ? to_f32(dv[kr + d]) : 0.f;
+        acc[c] = fmaf(pr, v, acc[c] * alpha);
+      }
+      M = mn;
+      const int64_t pa = parents[(size_t)b * nq + a];
+      a = (pa >= 0 && pa < a) ? (int)pa : -1;
+    }
   }
   QT* o = out + (size_t)row * D;
 #pragma unroll
@@ -891,7 +787,8 @@ static void bind_workspace(DecodeParams& p, void* workspace) {
   p.part_ml = workspace ? (float*)workspace + (size_t)p.rows * p.max_splits * p.head_dim : nullptr;
 }
 
-static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, int64_t workspace_bytes) {
+static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, int64_t workspace_bytes,
+                        bool row_kernel = true) {
   if (p.rows <= 0 || p.heads <= 0) return set_error(FS_ERR_INVALID, "batch and heads must be positive");
   if (p.head_dim <= 0 || p.head_dim > 256) return set_error(FS_ERR_INVALID, "head_dim must be in [1, 256]");
   if (p.seq_len < 0) return set_error(FS_ERR_INVALID, "seq_len must be >= 0");
@@ -900,13 +797,17 @@ static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, 
   const int64_t tiles = ((int64_t)p.seq_len + kTile - 1) / kTile;
   if ((int64_t)p.max_splits * p.split_tiles < tiles)
     return set_error(FS_ERR_INVALID, "max_splits * split_tiles must cover ceil(seq_len / 16) tiles");
-  if (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4 && waves_per_block != 8 &&
-      waves_per_block != 16)
-    return set_error(FS_ERR_INVALID, "waves_per_block must be 1, 2, 4, 8 or 16");
-  if (tiled && waves_per_block > max_tiled_waves(padded_head_dim(p.head_dim)))
-    return set_error(FS_ERR_INVALID, "waves_per_block must be <= 8 for head_dim > 128 on the tiled path");
-  if (tiled && p.split_tiles > kMaxTilesPerWave * waves_per_block)
-    return set_error(FS_ERR_INVALID, "split_tiles must be <= 64 * waves_per_block on the tiled path");
+  // row_kernel = false: the launch goes to the multi-query tree kernel, which checks its own
+  // workgroup size
+  if (row_kernel) {
+    if (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4 && waves_per_block != 8 &&
+        waves_per_block != 16)
+      return set_error(FS_ERR_INVALID, "waves_per_block must be 1, 2, 4, 8 or 16");
+    if (tiled && waves_per_block > max_tiled_waves(padded_head_dim(p.head_dim)))
+      return set_error(FS_ERR_INVALID, "waves_per_block must be <= 8 for head_dim > 128 on the tiled path");
+    if (tiled && p.split_tiles > kMaxTilesPerWave * waves_per_block)
+      return set_error(FS_ERR_INVALID, "split_tiles must be <= 64 * waves_per_block on the tiled path");
+  }
   if ((int64_t)p.rows * p.max_splits > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "decode grid too large");
   if (!p.q || !p.kv[0] || !p.kv[1] || !p.sc[0] || !p.sc[1] || !p.zp[0] || !p.zp[1] || !p.out)
     return set_error(FS_ERR_INVALID, "null tensor pointer");
@@ -929,6 +830,10 @@ extern "C" int64_t fs_decode_workspace_bytes(int64_t rows, int64_t max_splits, i
 
 extern "C" int fs_decode_tiled_path(int head_dim, int page_size, int quant_block) {
   return tiled_path(head_dim, page_size, quant_block) ? 1 : 0;
+}
+
+extern "C" int fs_tree_mfma_path(int head_dim, int page_size, int quant_block) {
+  return tree_mfma_path(head_dim, page_size, quant_block) ? 1 : 0;
 }
 
 extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
@@ -967,7 +872,8 @@ static int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_
                         const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
                         void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads,
                         int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
-                        float sm_scale, int split_tiles, int max_splits, int waves_per_block) {
+                        float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                        bool row_kernel = true) {
   p = DecodeParams{};
   p.q = q;
   p.kv[0] = k_values; p.kv[1] = v_values;
@@ -986,7 +892,7 @@ static int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_
   if ((int64_t)batch * nq * heads > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "too many query rows");
   bind_workspace(p, workspace);
   tiled = tiled_path(head_dim, page_size, quant_block);
-  if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes)) return rc;
+  if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes, row_kernel)) return rc;
   if (!block_table || !lengths) return set_error(FS_ERR_INVALID, "block_table and lengths are required");
   if (table_index_bytes != 4 && table_index_bytes != 8) return set_error(FS_ERR_INVALID, "table_index_bytes must be 4 or 8");
   if (table_cols <= 0) return set_error(FS_ERR_INVALID, "block_table needs at least one column");
@@ -1072,13 +978,21 @@ extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_val
                                  int draft_dtype, const int64_t* parents, void* out, void* workspace,
                                  int64_t workspace_bytes, int batch, int nodes, int heads, int head_dim,
                                  int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
-                                 int split_tiles, int max_splits, int waves_per_block, void* stream) {
+                                 int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
+                                 void* stream) {
+  if (prefix_kernel < 0 || prefix_kernel > 2)
+    return set_error(FS_ERR_INVALID, "prefix_kernel must be 0 (auto), 1 (row kernel) or 2 (multi-query kernel)");
+  const bool mq_ok = tree_mfma_path(head_dim, page_size, quant_block);
+  if (prefix_kernel == 2 && !mq_ok)
+    return set_error(FS_ERR_INVALID, "the multi-query tree kernel needs head_dim 64/128/256, pages of 16k tokens "
+                                     "and quant blocks of 16k tokens (or 1)");
+  const bool mq = mq_ok && prefix_kernel != 1;
   DecodeParams p;
   bool tiled = false;
   if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
                             table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, nodes,
                             heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
-                            max_splits, waves_per_block))
+                            max_splits, waves_per_block, !mq))
     return rc;
   if (!draft_k || !draft_v || !parents) return set_error(FS_ERR_INVALID, "tree verify: null draft or parents pointer");
   if (draft_dtype != FS_F32 && draft_dtype != FS_F16 && draft_dtype != FS_BF16)
@@ -1089,7 +1003,11 @@ extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_val
     return set_error(FS_ERR_INVALID, "tree verify workspace too small (" + std::to_string(workspace_bytes) + " < " +
                                          std::to_string(need) + " bytes)");
   hipStream_t st = (hipStream_t)stream;
-  if (int rc = launch_decode<true>(p, q_dtype, tiled, waves_per_block, st)) return rc;
+  if (mq) {
+    if (int rc = launch_tree_prefix_mfma(p, q_dtype, waves_per_block, st)) return rc;
+  } else if (int rc = launch_decode<true>(p, q_dtype, tiled, waves_per_block, st)) {
+    return rc;
+  }
   switch (q_dtype) {
     case FS_F32: return launch_tree_tail_q<float>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
     case FS_F16: return launch_tree_tail_q<__half>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);

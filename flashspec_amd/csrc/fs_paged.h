@@ -1,0 +1,180 @@
+// Paged / contiguous INT8 K/V store addressing and the decode launch parameters shared by the
+// decode kernels (fs_decode.hip) and the multi-query tree-verification kernel (fs_tree.hip).
+#pragma once
+
+#include "fs_common.h"
+
+namespace fs {
+
+constexpr int kMaxWaves = 16;       // waves per workgroup on the tiled path
+constexpr int kMaxTilesPerWave = 64;  // per split and wave: one metadata lane per tile
+constexpr float kRescaleSlack = 8.0f;  // running max may lag the true max by 2^8
+constexpr int kXcds = 8;  // MI355X: accelerator complex dies, each with its own L2
+
+// How a tile finds its quantization parameters (scale / zero point).
+enum QuantMode : int {
+  kQmBlock = 0,  // quant block a multiple of 16 tokens: one entry per tile
+  kQmSub = 1,    // quant block an odd multiple of 8 tokens (or 8-token pages): one per 8-token half
+  kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
+};
+
+struct DecodeParams {
+  const void* q;
+  const int8_t* kv[2];
+  const float* sc[2];
+  const int16_t* zp[2];
+  const void* table;
+  int64_t table_cols;
+  int table_bytes;
+  const int64_t* lengths;
+  void* out;
+  float* part_ml;   // [rows, max_splits, 2] (max in log2 units, denominator)
+  float* part_acc;  // [rows, max_splits, D]
+  int rows, heads, head_dim;
+  int seq_len;
+  int64_t num_pages;
+  int n_blocks;
+  int quant_block;
+  int page_size;
+  int split_tiles, max_splits;
+  float qk_scale;  // sm_scale * log2(e)
+  // Tree verification: nq query rows per (request, head), rows ordered (b, n, h); the decode
+  // writes split partials for every row (force_partials) for the tree-tail merge.
+  int nq;
+  int force_partials;
+};
+
+__device__ __forceinline__ int queries_per_head(const DecodeParams& p) { return p.nq > 1 ? p.nq : 1; }
+
+// The dispatcher hands workgroups to the XCDs round-robin (workgroup i to XCD i % 8).
+// decode_unit renumbers them so that XCD x owns heads [x*H/8, (x+1)*H/8) of every batch
+// (all their splits): an XCD then streams an H/8-head slab of each page instead of one
+// 2 KiB head slice of every page, while every XCD still gets the same share of each
+// request, so ragged lengths stay balanced across XCDs.  Measured on one MI355X against the
+// plain order: B8 H32 S4096 paged 46.1 vs 46.9 us, 64 ragged requests 616 vs 624 us.
+// Giving each XCD whole batches instead is as fast on uniform lengths but 1.35x slower
+// when lengths descend across the batch.  Heads not divisible by 8 keep the plain order.
+__device__ __forceinline__ int xcd_chunked_unit(int bid, int units) {
+  const int per = units / kXcds, rem = units - per * kXcds;
+  const int x = bid % kXcds, k = bid / kXcds;
+  return x * per + min(x, rem) + k;
+}
+
+struct Unit {
+  int row, split;
+};
+
+__device__ __forceinline__ Unit decode_unit(const DecodeParams& p, int bid, int units) {
+  // pos = (((x * batch + b) * hg + hh) * nq + n) * max_splits + split with head h = x * hg + hh
+  // and row = (b * nq + n) * heads + h; with hg = heads (heads not divisible by 8) the same
+  // formula is the plain order, x = 0.  The nq query rows of one (request, head) are adjacent
+  // on one XCD, so they read the same pages at the same time (L2 hits after the first).
+  const bool grouped = p.heads % kXcds == 0;
+  const int hg = grouped ? p.heads / kXcds : p.heads;
+  const int nq = queries_per_head(p);
+  const int pos = grouped ? xcd_chunked_unit(bid, units) : bid;
+  const int batch = p.rows / (p.heads * nq);
+  const int split = pos % p.max_splits;
+  int t = pos / p.max_splits;
+  const int n = t % nq;
+  t /= nq;
+  const int hh = t % hg;
+  t /= hg;
+  const int b = t % batch, x = t / batch;
+  return {(b * nq + n) * p.heads + x * hg + hh, split};
+}
+
+__device__ __forceinline__ int row_length(const int64_t* lengths, int b, int seq_len) {
+  if (lengths == nullptr) return seq_len;
+  const int64_t l = lengths[b];
+  return (int)(l < 0 ? 0 : (l < (int64_t)seq_len ? l : (int64_t)seq_len));
+}
+
+__device__ __forceinline__ int row_splits(int len, int split_tiles) {
+  const int tiles = (len + kTile - 1) / kTile;
+  const int n = (tiles + split_tiles - 1) / split_tiles;
+  return n < 1 ? 1 : n;
+}
+
+__device__ __forceinline__ int64_t table_entry(const DecodeParams& p, int b, int64_t col) {
+  if (p.table_bytes == 4) return (int64_t)((const int32_t*)p.table)[(int64_t)b * p.table_cols + col];
+  return ((const int64_t*)p.table)[(int64_t)b * p.table_cols + col];
+}
+
+// Sequence tile `tile` (16 tokens) of (b, h): `data` indexes 16*D-byte tiles of the value
+// store, `meta` the scale / zero entries (one per quant block; a quant block is a multiple
+// of 16 tokens on this path, so a tile never straddles two).  data = -1 when the tile is
+// not backed by an allocated page.
+struct TileIndex {
+  int data, meta;
+};
+
+template <bool PAGED>
+__device__ __forceinline__ TileIndex tile_index(const DecodeParams& p, int b, int h, int row, int tile) {
+  const int tpq = p.quant_block / kTile;  // tiles per quant block
+  if constexpr (PAGED) {
+    const int tpp = p.page_size / kTile;
+    const int lp = tile / tpp;
+    const int sub = tile - lp * tpp;
+    if (lp >= p.table_cols) return {-1, 0};
+    const int64_t pg = table_entry(p, b, lp);
+    if (pg < 0 || pg >= p.num_pages) return {-1, 0};
+    const int64_t ph = pg * p.heads + h;
+    return {(int)(ph * tpp + sub), (int)(ph * (tpp / tpq) + sub / tpq)};
+  } else {
+    return {row * p.n_blocks * tpq + tile, row * p.n_blocks + tile / tpq};
+  }
+}
+
+// 8-token sub-tile `u` of (b, h) for stores whose quant block or page is 8 tokens (an odd
+// multiple of 8): `data` in units of 8*D value bytes, `meta` the scale / zero entry of the
+// quant block holding it; data = -1 when not backed by an allocated page.
+template <bool PAGED>
+__device__ __forceinline__ TileIndex sub_index(const DecodeParams& p, int b, int h, int row, int u) {
+  const int token0 = 8 * u;
+  if constexpr (PAGED) {
+    const int lp = token0 / p.page_size;
+    const int within = token0 - lp * p.page_size;
+    if (lp >= p.table_cols) return {-1, 0};
+    const int64_t pg = table_entry(p, b, lp);
+    if (pg < 0 || pg >= p.num_pages) return {-1, 0};
+    const int64_t ph = pg * p.heads + h;
+    return {(int)(ph * (p.page_size / 8) + within / 8), (int)(ph * (p.page_size / p.quant_block) + within / p.quant_block)};
+  } else {
+    return {row * p.n_blocks * (p.quant_block / 8) + u, row * p.n_blocks + token0 / p.quant_block};
+  }
+}
+
+// Token mode: first token of tile `tile` of (b, h) in the value store (units of D bytes, the
+// same index as its per-token scale / zero), -1 when not backed by an allocated page.
+template <bool PAGED>
+__device__ __forceinline__ int token_index(const DecodeParams& p, int b, int h, int row, int tile) {
+  if constexpr (PAGED) {
+    const int tpp = p.page_size / kTile;
+    const int lp = tile / tpp;
+    const int sub = tile - lp * tpp;
+    if (lp >= p.table_cols) return -1;
+    const int64_t pg = table_entry(p, b, lp);
+    if (pg < 0 || pg >= p.num_pages) return -1;
+    return (int)((pg * p.heads + h) * p.page_size + sub * kTile);
+  } else {
+    return row * p.n_blocks + tile * kTile;
+  }
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// K/V bytes are read exactly once: non-temporal loads keep them from displacing the
+// cache lines the rest of the GPU is using (measured: ~7% faster than plain loads).
+__device__ __forceinline__ uint4 stream_load(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Multi-query (tree verification) prefix kernel of fs_tree.hip: whether it serves a store
+// shape, and its launch (split partials for every (request, node, head) row).
+bool tree_mfma_path(int head_dim, int page_size, int quant_block);
+int tree_mfma_max_waves(int head_dim);
+int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves_per_block, hipStream_t st);
+
+}  // namespace fs

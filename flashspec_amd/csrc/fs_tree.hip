@@ -1,0 +1,499 @@
+// Multi-query prefix attention for tree verification on gfx950 matrix cores.
+//
+// Tree verification (flashspec_amd/tree.py; planned by the reference in doc/TODO.MD:186-237)
+// asks, for every request b and head h, N draft-node queries over the same paged INT8
+// prefix.  Here one wave reads each 16-token K/V tile of (b, h) once and serves 16 nodes:
+//
+//   S[t, n]  = sum_d (u[t, d] - zk[t]) * q[n, d]        v_mfma_f32_16x16x32_f16, A = K tile, B = Q
+//   O[d, n] += sum_t (u[t, d] - zv[t]) * P'[n, t]       v_mfma_f32_16x16x32_f16, A = V^T,    B = P'
+//
+// (u = stored int8 + 128; the P.V product takes two tiles, 32 tokens, at once).  K
+// bytes enter the product as fp16 1024 + u (one byte permute and
+// one XOR per pair), and the zero point is removed on the fp32 scores as (1024 + zk) * sum(q)
+// per node, as in the row kernel; V bytes become u - zv exactly in fp16 (integers in
+// [-255, 255]) with one more packed fp16 add per pair.  The key scale multiplies the fp32
+// scores; the value scale is folded into the weights as
+// P' = P * vs / vref, with vref the largest value scale among the wave's tiles, so that
+// P' <= 2^8 fits fp16 (the wave's output is multiplied by vref at the end).  P' enters the
+// P.V product as fp16 hi + lo (two products), which keeps about 22 significant bits: one
+// fp16 rounding (2^-11) would put errors of ~1e-4 on the outputs.  The lane
+// layouts chain without data movement: lane l holds the scores of node l % 16 for tokens
+// 4*(l/16) + r (r < 4) -- the result layout of the Q.K product is the B-operand layout of
+// the P.V product -- and its P.V accumulator holds node l % 16 for dims [D/4 * (l/16),
+// D/4 * (l/16 + 1)).  Softmax runs online per node in the log2 domain with the lazily
+// refreshed running max of the row kernel.
+//
+// Queries: fp16 directly; bf16 and fp32 queries are scaled per node by a power of two
+// (largest |q| into [2^13, 2^14)) and held as fp16 (bf16: exactly; fp32: as hi + lo, two
+// Q.K products), the power of two is undone on the scores.
+//
+// Workgroup = W waves over one (request, head, 16-node group, split); wave w takes tiles
+// w, w+W, ... of the split (metadata resolved by one lane per tile), and the W wave states
+// merge through LDS into one split partial (max, denominator, unnormalized accumulator) per
+// (request, node, head) row, in the layout the tree tail kernel merges with the path tokens.
+
+#include <type_traits>
+
+#include "fs_paged.h"
+
+namespace fs {
+
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kNodeGroup = 16;  // draft nodes per wave: the N dimension of the MFMA tiles
+
+// Waves per workgroup: 8 (4 for head_dim 256, whose ~250 registers per lane leave one wave
+// per SIMD).  Measured: 12-wave workgroups (the register file holds 3 waves per SIMD at
+// head_dim 128) run 6-12% slower than 8-wave ones.
+__host__ __device__ constexpr int tree_waves_cap_dp(int DP) { return DP == 256 ? 4 : 8; }
+
+// Byte pair -> fp16 pair (1024 + u_a, 1024 + u_b): the permute puts the two raw bytes in the
+// low bytes of the halves (high bytes zero), XOR 0x6480 flips the int8 sign bit (u = raw ^
+// 0x80) and sets the fp16 exponent of 1024.
+constexpr uint32_t kHalfBias = 0x64806480u;
+
+__device__ __forceinline__ f16x8_t k_step_f16(uint32_t w0, uint32_t w1) {
+  const uint32_t a = __builtin_amdgcn_perm(0u, w0, 0x0c010c00u) ^ kHalfBias;
+  const uint32_t b = __builtin_amdgcn_perm(0u, w0, 0x0c030c02u) ^ kHalfBias;
+  const uint32_t c = __builtin_amdgcn_perm(0u, w1, 0x0c010c00u) ^ kHalfBias;
+  const uint32_t d = __builtin_amdgcn_perm(0u, w1, 0x0c030c02u) ^ kHalfBias;
+  const u32x4_t v = {a, b, c, d};
+  return __builtin_bit_cast(f16x8_t, v);
+}
+
+// Byte `bp` of four tokens' dwords -> fp16 (1024 + u) of tokens 0..3.
+template <int BP>
+__device__ __forceinline__ f16x4_t v_block_f16(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3, f16x4_t nz) {
+  constexpr uint32_t sel = (uint32_t)BP | (0x0cu << 8) | ((uint32_t)(4 + BP) << 16) | (0x0cu << 24);
+  const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel) ^ kHalfBias;
+  const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel) ^ kHalfBias;
+  const u32x2_t v = {lo, hi};
+  return __builtin_bit_cast(f16x4_t, v) + nz;
+}
+
+// J bytes of one token row (J = D / 16: 4, 8 or 16).  Plain (cached) loads, unlike the row
+// kernel's non-temporal ones: the node groups of one (request, head) read the same tiles, and
+// measured at 16 and 64 nodes cached loads are 1-4% faster.
+template <int J>
+struct VBytes {
+  uint32_t w[J / 4];
+  __device__ __forceinline__ void load(const int8_t* p) {
+    if constexpr (J == 16) {
+      const uint4 v = *(const uint4*)p;
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (J == 8) {
+      const u32x2_t v = *(const u32x2_t*)p;
+      w[0] = v.x; w[1] = v.y;
+    } else {
+      w[0] = *(const uint32_t*)p;
+    }
+  }
+};
+
+// One tile in flight: the lane's K slice (token l%16, C 16-byte chunks), its V bytes (tokens
+// 4g..4g+3, J bytes each) and, in token mode, those tokens' quantization parameters.
+template <int DP, bool TOK>
+struct MqTile {
+  static constexpr int C = DP / 64, J = DP / 16;
+  uint4 k[C];
+  VBytes<J> v[4];
+  float ks[TOK ? 4 : 1], vs[TOK ? 4 : 1];
+  int kz[TOK ? 4 : 1], vz[TOK ? 4 : 1];
+};
+
+// Per-node query in fp16 MFMA operands (hi, and lo for fp32 queries) and the power of two
+// the scores are multiplied by.
+template <typename QT, int DP>
+struct MqQuery {
+  static constexpr int KS = DP / 32;  // x32 Q.K steps
+  static constexpr bool kLo = std::is_same<QT, float>::value;
+  f16x8_t hi[KS];
+  f16x8_t lo[kLo ? KS : 1];
+  float mul;
+  float sum;  // sum over the node's dims of the operand values (hi + lo), for the zero point
+
+  // Lane (node n = l % 16, group g = l / 16) holds dims 16*(4c + g) + i, c < DP/64, i < 16,
+  // as elements 16c + i; step s of the product uses elements [8s, 8s + 8).
+  __device__ __forceinline__ void load(const QT* qrow, bool present, int g) {
+    float x[DP / 4];
+#pragma unroll
+    for (int c = 0; c < DP / 64; ++c) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[16 * c + i] = present ? to_f32(qrow[16 * (4 * c + g) + i]) : 0.f;
+    }
+    float scale = 1.f;
+    mul = 1.f;
+    if constexpr (!std::is_same<QT, __half>::value) {
+      float mx = 0.f;
+#pragma unroll
+      for (int e = 0; e < DP / 4; ++e) mx = fmaxf(mx, fabsf(x[e]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      if (mx > 0.f) {
+        int ex;
+        (void)frexpf(mx, &ex);            // mx in [2^(ex-1), 2^ex)
+        scale = ldexpf(1.f, 14 - ex);     // largest |q| into [2^13, 2^14)
+        mul = ldexpf(1.f, ex - 14);
+      }
+    }
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = x[8 * s + e] * scale;
+        const _Float16 h = (_Float16)v;
+        hi[s][e] = h;
+        part += (float)h;
+        if constexpr (kLo) {
+          const _Float16 lw = (_Float16)(v - (float)h);
+          lo[s][e] = lw;
+          part += (float)lw;
+        }
+      }
+    }
+    part += __shfl_xor(part, 16, kWave);
+    sum = part + __shfl_xor(part, 32, kWave);
+  }
+};
+
+struct TreeUnit {
+  int b, h, grp, split;
+};
+
+// pos = ((((x * batch + b) * hg + hh) * groups + grp) * max_splits + split, head h = x * hg + hh:
+// XCD x owns heads [x*H/8, (x+1)*H/8) of every request (plain order when H % 8 != 0), as in
+// the row kernel's decode_unit.
+__device__ __forceinline__ TreeUnit tree_unit(const DecodeParams& p, int groups, int bid, int units) {
+  const bool grouped = p.heads % kXcds == 0;
+  const int hg = grouped ? p.heads / kXcds : p.heads;
+  const int pos = grouped ? xcd_chunked_unit(bid, units) : bid;
+  const int batch = p.rows / (p.heads * p.nq);
+  TreeUnit u;
+  u.split = pos % p.max_splits;
+  int t = pos / p.max_splits;
+  u.grp = t % groups;
+  t /= groups;
+  const int hh = t % hg;
+  t /= hg;
+  u.b = t % batch;
+  u.h = (t / batch) * hg + hh;
+  return u;
+}
+
+template <int DP, typename QT, int QM>
+__global__ void __launch_bounds__(kWave * tree_waves_cap_dp(DP))
+tree_prefix_mfma_kernel(const DecodeParams p) {
+  constexpr bool TOK = QM == kQmToken;
+  constexpr int C = DP / 64, J = DP / 16, KS = DP / 32;
+  constexpr int ROW = DP + 4;  // padded LDS row (floats)
+  __shared__ float s_acc[tree_waves_cap_dp(DP) * kNodeGroup * ROW];
+  __shared__ float s_ml[tree_waves_cap_dp(DP) * kNodeGroup * 2];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int W = blockDim.x / kWave;
+  const int nq = p.nq;
+  const int groups = (nq + kNodeGroup - 1) / kNodeGroup;
+  const TreeUnit u = tree_unit(p, groups, blockIdx.x, gridDim.x);
+  const int b = u.b, h = u.h, split = u.split;
+  const int nl = lane & 15;  // node within the group (and token row of the K slice)
+  const int g = lane >> 4;   // lane group: tokens 4g..4g+3, dims of K slice 16(4c+g)+i
+  const int node = u.grp * kNodeGroup + nl;
+
+  const int len = row_length(p.lengths, b, p.seq_len);
+  const int nsplit = row_splits(len, p.split_tiles);
+  if (split >= nsplit) return;  // whole workgroup, before any barrier
+  const int first = split * p.split_tiles + w;
+  const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
+  const int nk = first < tile_end ? (tile_end - first + W - 1) / W : 0;  // <= kMaxTilesPerWave
+
+  // lane k resolves the wave's k-th tile: byte offset of its 16 K/V rows (-1: unbacked) and,
+  // in block mode, its quantization parameters; vmax = largest value scale it holds
+  int64_t my_off = -1;
+  float my_ks = 0.f, my_vs = 0.f, vmax = 0.f;
+  int my_kz = 0, my_vz = 0;
+  const int D = DP;
+  if (lane < nk) {
+    const int tile = first + W * lane;
+    if constexpr (TOK) {
+      const int base = token_index<true>(p, b, h, 0, tile);
+      if (base >= 0) {
+        my_off = (int64_t)base * D;
+#pragma unroll
+        for (int r = 0; r < kTile; ++r) vmax = fmaxf(vmax, p.sc[1][base + r]);
+      }
+    } else {
+      const TileIndex ti = tile_index<true>(p, b, h, 0, tile);
+      if (ti.data >= 0) {
+        my_off = (int64_t)ti.data * (kTile * D);
+        my_ks = p.sc[0][ti.meta] * p.qk_scale;
+        my_kz = p.zp[0][ti.meta];
+        my_vs = p.sc[1][ti.meta];
+        my_vz = p.zp[1][ti.meta];
+        vmax = my_vs;
+      }
+    }
+  }
+  vmax = wave_max(vmax);
+  const float vref = vmax > 0.f ? vmax : 1.f;
+  const float inv_vref = 1.f / vref;
+
+  MqQuery<QT, DP> q;
+  const size_t qrow = (((size_t)b * nq + node) * p.heads + h) * D;
+  q.load((const QT*)p.q + (node < nq ? qrow : 0), node < nq, g);
+  const float qmul = q.mul * (TOK ? p.qk_scale : 1.f);
+
+  const int8_t* kbase = p.kv[0];
+  const int8_t* vbase = p.kv[1];
+  auto off_of = [&](int k) -> int64_t {
+    const int lo = __builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)my_off, k);
+    const int hi = __builtin_amdgcn_readlane((int)((uint64_t)my_off >> 32), k);
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+  };
+  // An unbacked tile loads tile 0 of the store (L2 hits) and is masked: a branch around the
+  // loads would make the compiler keep the registers in scratch memory.
+  auto load = [&](MqTile<DP, TOK>& t, int k) {
+    const int64_t o = k < nk ? off_of(k) : -1;
+    const size_t to = o < 0 ? 0 : (size_t)o;
+    const int8_t* kp = kbase + to + (size_t)nl * D;
+#pragma unroll
+    for (int c = 0; c < C; ++c) t.k[c] = *(const uint4*)(kp + 16 * (4 * c + g));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t.v[e].load(vbase + to + (size_t)(4 * g + e) * D + J * nl);
+    if constexpr (TOK) {
+      const size_t tok0 = to / D;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        t.ks[r] = p.sc[0][tok0 + 4 * g + r];
+        t.kz[r] = p.zp[0][tok0 + 4 * g + r];
+        t.vs[r] = p.sc[1][tok0 + 4 * g + r];
+        t.vz[r] = p.zp[1][tok0 + 4 * g + r];
+      }
+    }
+  };
+
+  float m = kNegBig, l = 0.f;
+  f32x4_t acc[J];
+#pragma unroll
+  for (int jb = 0; jb < J; ++jb) acc[jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Scores of tile k (4 tokens 4g + r of node l % 16, masked to kNegBig), the tile's value
+  // factors vs / vref and fp16 -(1024 + zv) for those tokens.
+  auto scores = [&](const MqTile<DP, TOK>& t, int k, float (&sc)[4], float (&vfac)[4], f16x4_t& nzv) {
+    const bool backed = k < nk && off_of(k) >= 0;
+    const int token0 = (first + W * k) * kTile + 4 * g;
+    float kmul[4], kzo[4];
+    int vz[4];
+    if constexpr (TOK) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        kmul[r] = t.ks[r] * qmul;
+        kzo[r] = (float)(1024 + t.kz[r]);
+        vfac[r] = t.vs[r] * inv_vref;
+        vz[r] = t.vz[r];
+      }
+    } else {
+      const int kk = k < nk ? k : 0;
+      const float ks = readlane_f32(my_ks, kk) * qmul, vf = readlane_f32(my_vs, kk) * inv_vref;
+      const int vzz = readlane_i32(my_vz, kk);
+      const float kz = (float)(1024 + readlane_i32(my_kz, kk));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        kmul[r] = ks;
+        kzo[r] = kz;
+        vfac[r] = vf;
+        vz[r] = vzz;
+      }
+    }
+    // S[t = 4g + r][n = l % 16] = sum_d q (1024 + u) - (1024 + zk) * sum_d q
+    f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint4 raw = t.k[s >> 1];
+      const f16x8_t kf = (s & 1) ? k_step_f16(raw.z, raw.w) : k_step_f16(raw.x, raw.y);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.hi[s], sacc, 0, 0, 0);
+      if constexpr (MqQuery<QT, DP>::kLo) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.lo[s], sacc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = backed && token0 + r < len;
+      sc[r] = ok ? fmaf(-kzo[r], q.sum, sacc[r]) * kmul[r] : kNegBig;
+    }
+    // -(1024 + z) straight from the integer (exact in fp16 for zero points in [0, 255]); no
+    // fp32 step, which the vectorizer would pair into fp32 vector ops
+    nzv = f16x4_t{(_Float16)(-1024 - vz[0]), (_Float16)(-1024 - vz[1]), (_Float16)(-1024 - vz[2]),
+                  (_Float16)(-1024 - vz[3])};
+  };
+
+  // Tiles k and k + 1 (k + 1 may lie past the wave's tiles: masked): the P.V product runs on
+  // the pair as 16x16x32 MFMAs whose 32-token dimension takes tokens 4g..4g+3 of both tiles
+  // from lane group g -- where the Q.K products left their weights.
+  auto consume_pair = [&](const MqTile<DP, TOK>& ta, const MqTile<DP, TOK>& tb, int k) {
+    float sa[4], sb[4], fa[4], fb[4];
+    f16x4_t za, zb;
+    scores(ta, k, sa, fa, za);
+    scores(tb, k + 1, sb, fb, zb);
+    float mt = kNegBig;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mt = fmaxf(mt, fmaxf(sa[r], sb[r]));
+    // The four lanes of a node share its running max m.  Each lane tests its own tokens; only
+    // when one of them exceeds m by the slack does the wave take the max over the node's four
+    // lanes and rescale (all lanes of a node then agree on the new m again).
+    if (__any(mt > m + kRescaleSlack)) {
+      mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+      const float mnew = fmaxf(m, mt);
+      const float alpha = fast_exp2(m - mnew);
+      m = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int jb = 0; jb < J; ++jb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[jb][r] *= alpha;
+      }
+    }
+    // weights as fp16 hi + lo (about 22 significant bits, like the fp32 weights of the row
+    // kernel): two P.V products per block
+    f16x8_t pw, pl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sv = e < 4 ? sa[e] : sb[e - 4];
+      const float pr = sv > kNegBig ? fast_exp2(sv - m) : 0.f;
+      l += pr;
+      const float pv = pr * (e < 4 ? fa[e] : fb[e - 4]);
+      const _Float16 ph = (_Float16)pv;
+      pw[e] = ph;
+      pl[e] = (_Float16)(pv - (float)ph);
+    }
+#pragma unroll
+    for (int jb = 0; jb < J; ++jb) {
+      const int dw = jb >> 2;
+      f16x4_t va, vb;
+      switch (jb & 3) {
+        case 0:
+          va = v_block_f16<0>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+          vb = v_block_f16<0>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+          break;
+        case 1:
+          va = v_block_f16<1>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+          vb = v_block_f16<1>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+          break;
+        case 2:
+          va = v_block_f16<2>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+          vb = v_block_f16<2>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+          break;
+        default:
+          va = v_block_f16<3>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+          vb = v_block_f16<3>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+          break;
+      }
+      const f16x8_t vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pw, acc[jb], 0, 0, 0);
+      acc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, acc[jb], 0, 0, 0);
+    }
+  };
+
+  // two pairs of register buffers: tiles k+2, k+3 are in flight while k, k+1 are consumed
+  MqTile<DP, TOK> ta, tb, tc, td;
+  load(ta, 0);
+  load(tb, 1);
+  for (int k = 0; k < nk; k += 4) {
+    load(tc, k + 2);
+    load(td, k + 3);
+    consume_pair(ta, tb, k);
+    if (k + 2 >= nk) break;
+    load(ta, k + 4);
+    load(tb, k + 5);
+    consume_pair(tc, td, k + 2);
+  }
+
+  // node totals over the four lane groups; accumulator to value units
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  float* my_acc = s_acc + (size_t)(w * kNodeGroup + nl) * ROW;
+#pragma unroll
+  for (int jb = 0; jb < J; ++jb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) my_acc[J * (4 * g + r) + jb] = acc[jb][r] * vref;
+  }
+  if (g == 0) {
+    s_ml[2 * (w * kNodeGroup + nl)] = m;
+    s_ml[2 * (w * kNodeGroup + nl) + 1] = l;
+  }
+  __syncthreads();
+  const int nodes_here = min(kNodeGroup, nq - u.grp * kNodeGroup);
+  for (int e = threadIdx.x; e < nodes_here * D; e += blockDim.x) {
+    const int n = e / D, d = e - n * D;
+    float M = kNegBig;
+    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, s_ml[2 * (ww * kNodeGroup + n)]);
+    float L = 0.f, a = 0.f;
+    for (int ww = 0; ww < W; ++ww) {
+      const float f = fast_exp2(s_ml[2 * (ww * kNodeGroup + n)] - M);
+      L = fmaf(s_ml[2 * (ww * kNodeGroup + n) + 1], f, L);
+      a = fmaf(s_acc[(size_t)(ww * kNodeGroup + n) * ROW + d], f, a);
+    }
+    const int row = (b * nq + u.grp * kNodeGroup + n) * p.heads + h;
+    const size_t ws = (size_t)row * p.max_splits + split;
+    p.part_acc[ws * D + d] = a;
+    if (d == 0) {
+      p.part_ml[2 * ws] = M;
+      p.part_ml[2 * ws + 1] = L;
+    }
+  }
+}
+
+// ---- host side ---------------------------------------------------------------------------
+
+bool tree_mfma_path(int head_dim, int page_size, int quant_block) {
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return false;
+  if (page_size <= 0 || page_size % kTile != 0) return false;
+  if (quant_block == 1) return true;
+  return quant_block > 0 && quant_block % kTile == 0 && page_size % quant_block == 0;
+}
+
+int tree_mfma_max_waves(int head_dim) { return tree_waves_cap_dp(head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256)); }
+
+template <int DP, typename QT>
+static void launch_mq(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
+  if (tok)
+    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock>), grid, block, 0, st, p);
+}
+
+template <typename QT>
+static void launch_mq_q(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
+  switch (p.head_dim) {
+    case 64: launch_mq<64, QT>(p, tok, grid, block, st); break;
+    case 128: launch_mq<128, QT>(p, tok, grid, block, st); break;
+    default: launch_mq<256, QT>(p, tok, grid, block, st); break;
+  }
+}
+
+// Preconditions checked by the caller: paged store, valid pointers, workspace for rows x
+// max_splits partials, tree_mfma_path() true.
+int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves, hipStream_t st) {
+  if (waves < 1 || waves > tree_mfma_max_waves(p.head_dim))
+    return set_error(FS_ERR_INVALID, "tree verify: waves_per_block must be in [1, 8] ([1, 4] for head_dim 256)");
+  if (p.split_tiles > kMaxTilesPerWave * waves)
+    return set_error(FS_ERR_INVALID, "tree verify: split_tiles must be <= 64 * waves_per_block");
+  const int groups = (p.nq + kNodeGroup - 1) / kNodeGroup;
+  const int batch = p.rows / (p.heads * p.nq);
+  const int64_t units = (int64_t)batch * p.heads * groups * p.max_splits;
+  if (units > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "tree verify grid too large");
+  const dim3 grid((unsigned)units), block(kWave * waves);
+  const bool tok = p.quant_block == 1;
+  switch (q_dtype) {
+    case FS_F32: launch_mq_q<float>(p, tok, grid, block, st); break;
+    case FS_F16: launch_mq_q<__half>(p, tok, grid, block, st); break;
+    case FS_BF16: launch_mq_q<__hip_bfloat16>(p, tok, grid, block, st); break;
+    default: return set_error(FS_ERR_INVALID, "q dtype code must be 0 (f32), 1 (f16) or 2 (bf16)");
+  }
+  return check_launch("tree_prefix_mfma");
+}
+
+}  // namespace fs

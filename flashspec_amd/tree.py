@@ -17,12 +17,13 @@ from __future__ import annotations
 import math
 from typing import Any
 
+import numpy as np
 import torch
 
 from . import _lib
 from .paged import PagedKVCache
 from .quant import build_compression_stats
-from .triton_utils import launch_plan
+from .triton_utils import TREE_NODE_GROUP, device_cu_count, launch_plan, plan_tree_splits
 
 __all__ = ["tree_verify_attention", "validate_parents", "path_mask"]
 
@@ -34,9 +35,9 @@ def validate_parents(parents: torch.Tensor, batch: int, nodes: int) -> torch.Ten
         raise ValueError(f"parents must be [batch, nodes] = [{batch}, {nodes}]")
     if parents.dtype not in (torch.int32, torch.int64):
         raise ValueError("parents must be an int32/int64 tensor")
-    host = parents.detach().to("cpu", torch.int64)
-    idx = torch.arange(nodes, dtype=torch.int64)[None, :]
-    if bool((host < -1).any()) or bool((host >= idx).any()):
+    host = parents.detach().to("cpu", torch.int64).contiguous()
+    a = host.numpy()
+    if bool(((a < -1) | (a >= np.arange(nodes, dtype=np.int64))).any()):
         raise ValueError("parents[b, n] must lie in [-1, n): cycles, forward edges and orphans are invalid")
     return host
 
@@ -88,7 +89,10 @@ def _portable(q, cache, draft_k, draft_v, parents_host):
     return out.to(q.dtype)
 
 
-def _hip(q, cache, draft_k, draft_v, parents_host, dims):
+_KERNELS = {"auto": 0, "rows": 1, "mfma": 2}
+
+
+def _hip(q, cache, draft_k, draft_v, parents_host, dims, kernel):
     batch, nodes, heads, head_dim = dims
     lib = _lib.require()
     dev = q.device
@@ -100,11 +104,24 @@ def _hip(q, cache, draft_k, draft_v, parents_host, dims):
     q_c, dk_c, dv_c = q.contiguous(), draft_k.contiguous(), draft_v.contiguous()
     table = cache.block_table.contiguous()
     lengths = cache.lengths.to(torch.int64).contiguous()
-    parents_dev = parents_host.to(dev).contiguous()
+    if parents_host.device.type == "cpu":
+        parents_dev = parents_host.pin_memory().to(dev, non_blocking=True)
+    else:
+        parents_dev = parents_host.to(torch.int64).contiguous()
     rows = batch * nodes * heads
     max_seq_len = int(cache.max_seq_len)
-    tiled, waves, split_tiles, max_splits, block_n = launch_plan(max_seq_len, rows, head_dim, int(cache.block_size),
-                                                                 int(kq.block_size), dev)
+    mfma_ok = bool(lib.fs_tree_mfma_path(head_dim, int(cache.block_size), int(kq.block_size)))
+    if kernel == "mfma" and not mfma_ok:
+        raise ValueError("kernel='mfma' needs head_dim 64/128/256, pages of a multiple of 16 tokens and "
+                         "quant blocks of 1 or a multiple of 16 tokens")
+    use_mfma = mfma_ok and kernel != "rows"
+    if use_mfma:
+        units = batch * heads * math.ceil(nodes / TREE_NODE_GROUP)
+        split_tiles, max_splits, waves = plan_tree_splits(max_seq_len, units, head_dim, device_cu_count(dev))
+        tiled, block_n = True, 16
+    else:
+        tiled, waves, split_tiles, max_splits, block_n = launch_plan(max_seq_len, rows, head_dim,
+                                                                     int(cache.block_size), int(kq.block_size), dev)
     ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty_like(q_c)
@@ -114,14 +131,16 @@ def _hip(q, cache, draft_k, draft_v, parents_host, dims):
         table.data_ptr(), table.element_size(), int(table.shape[1]), lengths.data_ptr(), dk_c.data_ptr(),
         dv_c.data_ptr(), _lib.dtype_code(dk_c.dtype), parents_dev.data_ptr(), out.data_ptr(), workspace.data_ptr(),
         ws_bytes, batch, nodes, heads, head_dim, int(kq.values.shape[0]), int(cache.block_size), int(kq.block_size),
-        max_seq_len, 1.0 / math.sqrt(head_dim), split_tiles, max_splits, waves, _lib.stream_ptr(dev)))
+        max_seq_len, 1.0 / math.sqrt(head_dim), split_tiles, max_splits, waves, _KERNELS[kernel] if kernel != "auto"
+        else (2 if use_mfma else 1), _lib.stream_ptr(dev)))
     plan = {"num_splits": float(max_splits), "split_tiles": float(split_tiles), "num_warps": float(waves),
-            "block_n": float(block_n), "tiled_path": float(tiled)}
+            "block_n": float(block_n), "tiled_path": float(tiled), "mfma_prefix": float(use_mfma)}
     return out, plan
 
 
 def tree_verify_attention(q: torch.Tensor, cache: PagedKVCache, draft_k: torch.Tensor, draft_v: torch.Tensor,
-                          parents: torch.Tensor, return_stats: bool = False) -> Any:
+                          parents: torch.Tensor, return_stats: bool = False, validate: bool = True,
+                          kernel: str = "auto") -> Any:
     """Attention of every draft node over the prefix and its root path.
 
     ``q``, ``draft_k``, ``draft_v``: ``[batch, nodes, heads, head_dim]``; ``parents``:
@@ -129,12 +148,30 @@ def tree_verify_attention(q: torch.Tensor, cache: PagedKVCache, draft_k: torch.T
     head_dim]`` in q's dtype (and a stats dict with ``return_stats``).  ``ValueError`` for a
     malformed tree or shapes, ``RuntimeError`` for device mismatches or a GPU tensor without
     the HIP library.
+
+    ``parents`` on the CPU (the usual case: the drafter builds the tree on the host) is
+    checked there and copied to the GPU through pinned memory without waiting for the
+    device.  ``parents`` already on the GPU is copied back to check it, which waits for
+    the device; ``validate=False`` skips that check, and the kernel then ends a node's path
+    at the first parent outside [-1, own index) (never reading out of bounds).
+
+    ``kernel`` picks the GPU prefix kernel: ``"mfma"`` reads each prefix tile once for 16
+    nodes with matrix-core products (head_dim 64/128/256, pages of 16k tokens, quant blocks
+    of 1 or 16k tokens), ``"rows"`` runs the paged decode with one query row per node (any
+    store), ``"auto"`` the first where it applies.
     """
 
+    if kernel not in _KERNELS:
+        raise ValueError(f"kernel must be one of {sorted(_KERNELS)}")
     dims = _validate(q, cache, draft_k, draft_v)
-    parents_host = validate_parents(parents, dims[0], dims[1])
+    if validate or parents.device.type != "cuda" or q.device.type != "cuda":
+        parents_host = validate_parents(parents, dims[0], dims[1])
+    else:
+        if parents.ndim != 2 or tuple(parents.shape) != dims[:2] or parents.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"parents must be an int32/int64 [batch, nodes] = [{dims[0]}, {dims[1]}] tensor")
+        parents_host = parents
     if q.device.type == "cuda":
-        out, plan = _hip(q, cache, draft_k, draft_v, parents_host, dims)
+        out, plan = _hip(q, cache, draft_k, draft_v, parents_host, dims, kernel)
         materializes = False
     else:
         out, plan = _portable(q, cache, draft_k, draft_v, parents_host), {}
@@ -143,8 +180,9 @@ def tree_verify_attention(q: torch.Tensor, cache: PagedKVCache, draft_k: torch.T
         return out
     batch, nodes, heads, head_dim = dims
     dense_bytes = 2 * batch * heads * int(cache.max_seq_len) * head_dim * q.element_size()
+    depth = float(_depth(parents_host)) if parents_host.device.type == "cpu" else float("nan")
     stats = build_compression_stats(dense_bytes, cache.estimated_bytes(), materializes_dense_kv=materializes,
-                                    tree_nodes=float(nodes), tree_depth=float(_depth(parents_host)), **plan)
+                                    tree_nodes=float(nodes), tree_depth=depth, **plan)
     return out, stats
 
 

@@ -178,6 +178,46 @@ def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: 
     return split_tiles, math.ceil(tiles / split_tiles), waves
 
 
+TREE_NODE_GROUP = 16  # draft nodes served by one wave of the multi-query tree kernel
+# One 8-wave workgroup of the multi-query kernel holds a CU (its ~140 registers per lane leave
+# room for 3 waves per SIMD): the plan splits only while the grid fits one workgroup per CU.
+# Measured on MI355X, B4 H32 S4096 D128, 16 nodes: 2 splits (256 workgroups) 33.5 us,
+# 4 splits (two rounds) 45.6 us; 4 nodes: 27.6 vs 35.0 us.
+TREE_WG_PER_CU = 1
+
+
+def tree_max_waves(head_dim: int) -> int:
+    """Waves per workgroup of the multi-query tree kernel: 8 (4 for head_dim 256)."""
+
+    return 4 if head_dim > 128 else 8
+
+
+def plan_tree_splits(seq_len: int, units: int, head_dim: int, cu_count: int) -> tuple[int, int, int]:
+    """``(split_tiles, max_splits, waves_per_block)`` of the multi-query tree kernel.
+
+    ``units`` = batch * heads * ceil(nodes / 16) workgroups per split.  Workgroups of 8 waves
+    (4 for head_dim 256, whose register layout is twice as wide); as many splits as keep the
+    grid within one workgroup per CU, at least two tiles per wave; ``FLASHSPEC_NUM_SPLITS`` /
+    ``FLASHSPEC_NUM_WARPS`` override as for the decode plan.
+    """
+
+    tiles = max(1, math.ceil(seq_len / TILE_TOKENS))
+    cap = tree_max_waves(head_dim)
+    forced_waves = forced_tiled_waves()
+    waves = min(forced_waves, cap) if forced_waves is not None else cap
+    forced = forced_num_splits(seq_len, resolve_block_n())
+    if forced is not None:
+        n = forced
+    else:
+        n = max(1, (TREE_WG_PER_CU * cu_count) // max(1, units))
+        n = min(n, max(1, tiles // (2 * waves)))
+    split_tiles = math.ceil(tiles / n)
+    limit = MAX_TILES_PER_WAVE * waves
+    if split_tiles > limit:
+        split_tiles = math.ceil(tiles / math.ceil(tiles / limit))
+    return split_tiles, math.ceil(tiles / split_tiles), waves
+
+
 def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, device):
     """(tiled, waves_per_block, split_tiles, max_splits, block_n) for one decode launch."""
 

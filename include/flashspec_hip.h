@@ -113,9 +113,14 @@ int fs_paged_decode_i8(const void* q, int q_dtype,
  * Speculative-decoding tree verification over a paged INT8 prefix.  Request b has `nodes`
  * draft nodes in topological order; node n attends to the prefix tokens [0, lengths[b]) of
  * the paged cache and to the draft tokens on its path to the root (n, parents[b, n],
- * parents[b, parents[b, n]], ... until -1).  The prefix part runs as the paged decode with one
- * query row per node, rows ordered (b, n, h), leaving split partials in `workspace`; a tail
- * kernel merges them with the path tokens (fp32 online softmax) and writes `out`.
+ * parents[b, parents[b, n]], ... until -1).  The prefix part leaves split partials per
+ * (b, n, h) row in `workspace`; a tail kernel merges them with the path tokens (fp32 online
+ * softmax) and writes `out`.  Prefix kernels (`prefix_kernel`):
+ *   1 = the paged decode with one query row per node (any store the decode serves);
+ *   2 = the multi-query kernel: one wave reads each 16-token tile once for 16 nodes with
+ *       MFMA products (fs_tree_mfma_path() stores; waves_per_block 1/2/4/8, <= 4 for
+ *       head_dim 256; split plan over batch*heads*ceil(nodes/16) workgroups per split);
+ *   0 = 2 where fs_tree_mfma_path() holds, else 1.
  *   q, out          [batch, nodes, heads, head_dim]  q_dtype
  *   draft_k/draft_v [batch, nodes, heads, head_dim]  draft_dtype (unquantized)
  *   parents         [batch, nodes] int64, parents[b, n] in [-1, n) (the caller validates;
@@ -133,7 +138,15 @@ int fs_tree_verify_i8(const void* q, int q_dtype,
                       const int64_t* parents, void* out, void* workspace, int64_t workspace_bytes,
                       int batch, int nodes, int heads, int head_dim, int64_t num_pages,
                       int page_size, int quant_block, int max_seq_len, float sm_scale,
-                      int split_tiles, int max_splits, int waves_per_block, void* stream);
+                      int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
+                      void* stream);
+
+/*
+ * 1 when fs_tree_verify_i8 can run its multi-query prefix kernel on this store: head_dim 64,
+ * 128 or 256, page_size a multiple of 16, quant_block 1 or a multiple of 16 dividing the
+ * page.  No counterpart in the reference (tree verification is not implemented there).
+ */
+int fs_tree_mfma_path(int head_dim, int page_size, int quant_block);
 
 /*
  * Merge the per-split partial states a decode call with max_splits > 1 left in

@@ -48,8 +48,8 @@ def _random_parents(B, N, seed):
 
 
 def _run(B, H, S, D, N, parents, lengths, page=16, layout="shuffled", q_dtype=torch.float16, kv_format="affine_block",
-         seed=0):
-    q = randn((B, N, H, D), seed + 1, q_dtype)
+         seed=0, kernel="auto", q_scale=1.0):
+    q = (randn((B, N, H, D), seed + 1, torch.float32) * q_scale).to(q_dtype)
     k = randn((B, H, S, D), seed + 2)
     v = randn((B, H, S, D), seed + 3)
     dk = randn((B, N, H, D), seed + 4)
@@ -57,7 +57,7 @@ def _run(B, H, S, D, N, parents, lengths, page=16, layout="shuffled", q_dtype=to
     cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), page, lengths=torch.tensor(lengths).to(DEV),
                                        block_table_pattern=layout, layout_seed=seed, kv_format=kv_format)
     got, stats = fa.tree_verify_attention(q.to(DEV), cache, dk.to(DEV), dv.to(DEV),
-                                          torch.tensor(parents).to(DEV), return_stats=True)
+                                          torch.tensor(parents).to(DEV), return_stats=True, kernel=kernel)
     torch.cuda.synchronize(DEV)
     ref = ot.tree_verify_attention(np_of(q.float()), from_cache(cache), np_of(dk.float()), np_of(dv.float()),
                                    np.asarray(parents))
@@ -72,16 +72,18 @@ def _run(B, H, S, D, N, parents, lengths, page=16, layout="shuffled", q_dtype=to
     (1, 4, 700, 256, 4, "random", [700]),
     (2, 3, 90, 96, 7, "random", [90, 45]),
 ])
-def test_tree_verify_matches_oracle(B, H, S, D, N, kind, lengths):
-    announce(f"tree verify B{B} H{H} S{S} D{D} N{N} {kind} lengths={lengths}")
+@pytest.mark.parametrize("kernel", ["auto", "rows"])
+def test_tree_verify_matches_oracle(B, H, S, D, N, kind, lengths, kernel):
+    announce(f"tree verify B{B} H{H} S{S} D{D} N{N} {kind} lengths={lengths} kernel={kernel}")
     if kind == "chain":
         parents = np.tile(np.arange(-1, N - 1), (B, 1))
     elif kind == "star":
         parents = np.full((B, N), -1)
     else:
         parents = _random_parents(B, N, S + N)
-    got, ref, stats = _run(B, H, S, D, N, parents, lengths, seed=B + S)
+    got, ref, stats = _run(B, H, S, D, N, parents, lengths, seed=B + S, kernel=kernel)
     assert stats["materializes_dense_kv"] == 0.0
+    assert stats["mfma_prefix"] == float(kernel == "auto" and D in (64, 128, 256))
     assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, f"tree {kind}")
 
 
@@ -116,3 +118,117 @@ def test_tree_single_node_matches_paged_decode_plus_token():
     B, H, S, D = 2, 4, 200, 128
     got, ref, _ = _run(B, H, S, D, 1, np.full((B, 1), -1), [200, 64], seed=21)
     assert_attention_close(got.reshape(B, H, D), ref.reshape(B, H, D), torch.float16, "single node")
+
+
+def test_tree_device_parents_without_validation():
+    """validate=False with parents on the GPU: a valid tree gives the validated result; a parent
+    outside [-1, n) ends that node's path there (the oracle sees the tree with it set to -1)."""
+
+    announce("tree verify device parents, validate=False")
+    B, H, S, D, N = 2, 4, 160, 128, 6
+    q = randn((B, N, H, D), 31).to(DEV)
+    k, v = randn((B, H, S, D), 32).to(DEV), randn((B, H, S, D), 33).to(DEV)
+    dk, dv = randn((B, N, H, D), 34).to(DEV), randn((B, N, H, D), 35).to(DEV)
+    cache = fa.PagedKVCache.from_dense(k, v, 16, block_table_pattern="shuffled", layout_seed=3)
+    good = np.array([[-1, 0, 1, 1, -1, 4], [-1, -1, 0, 2, 3, 0]])
+    a = fa.tree_verify_attention(q, cache, dk, dv, torch.tensor(good, dtype=torch.int32))
+    b = fa.tree_verify_attention(q, cache, dk, dv, torch.tensor(good).to(DEV), validate=False)
+    torch.cuda.synchronize(DEV)
+    assert torch.equal(a, b)
+    bad = good.copy()
+    bad[0, 3], bad[1, 5] = 7, -5  # a forward edge and an out-of-range parent
+    got = fa.tree_verify_attention(q, cache, dk, dv, torch.tensor(bad).to(DEV), validate=False)
+    torch.cuda.synchronize(DEV)
+    cut = good.copy()
+    cut[0, 3], cut[1, 5] = -1, -1
+    ref = ot.tree_verify_attention(np_of(q.cpu().float()), from_cache(cache), np_of(dk.cpu().float()),
+                                   np_of(dv.cpu().float()), cut)
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, "cut tree")
+
+
+# Multi-query MFMA prefix kernel: (B, H, S, D, N, page, kv_format, q dtype, lengths)
+MFMA_CASES = [
+    (2, 8, 1000, 128, 16, 16, "affine_block", torch.float16, [1000, 333]),
+    (1, 4, 700, 128, 17, 32, "affine_block", torch.float16, [700]),          # two node groups, 32-token pages
+    (2, 2, 257, 64, 40, 16, "symmetric_token", torch.bfloat16, [257, 16]),  # three groups, per-token scales
+    (1, 4, 530, 256, 9, 16, "affine_block", torch.float32, [530]),
+    (2, 4, 100, 128, 5, 64, "affine_block", torch.bfloat16, [100, 0]),      # 64-token pages, an empty prefix
+    (3, 8, 2100, 128, 12, 16, "symmetric_token", torch.float16, [2100, 5, 1500]),
+    (2, 4, 333, 256, 3, 32, "symmetric_token", torch.float16, [333, 200]),
+    (1, 16, 4096, 64, 16, 16, "affine_block", torch.float32, [4096]),
+    (1, 2, 200, 64, 70, 16, "affine_block", torch.float16, [200]),          # > 64 nodes: tail walks memory
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,N,page,fmt,q_dtype,lengths", MFMA_CASES)
+def test_tree_mfma_prefix_matches_oracle(B, H, S, D, N, page, fmt, q_dtype, lengths):
+    announce(f"tree mfma B{B} H{H} S{S} D{D} N{N} page{page} {fmt} {q_dtype} lengths={lengths}")
+    parents = _random_parents(B, N, S + 7 * N)
+    got, ref, stats = _run(B, H, S, D, N, parents, lengths, page=page, kv_format=fmt, q_dtype=q_dtype,
+                           seed=S + N, kernel="mfma")
+    assert stats["mfma_prefix"] == 1.0
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), q_dtype, f"mfma {fmt}")
+
+
+@pytest.mark.parametrize("q_dtype,q_scale", [(torch.bfloat16, 3000.0), (torch.bfloat16, 1e-3), (torch.float32, 40.0),
+                                             (torch.float32, 1e-4), (torch.float16, 20.0)])
+def test_tree_mfma_query_magnitudes(q_dtype, q_scale):
+    """Queries far from unit scale: the per-node power-of-two scaling keeps bf16 / fp32 queries
+    exact (bf16) or hi+lo exact to ~22 bits (fp32) in the fp16 operands; a large-magnitude fp16
+    query makes the softmax nearly one-hot."""
+
+    announce(f"tree mfma q magnitude {q_dtype} x{q_scale}")
+    B, H, S, D, N = 2, 4, 300, 128, 6
+    parents = _random_parents(B, N, 5)
+    got, ref, _ = _run(B, H, S, D, N, parents, [300, 150], q_dtype=q_dtype, seed=41, kernel="mfma", q_scale=q_scale)
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), q_dtype, "q magnitude")
+
+
+@pytest.mark.parametrize("splits,warps", [("3", "2"), ("1", "1"), ("7", "8")])
+def test_tree_mfma_forced_plans(monkeypatch, splits, warps):
+    """Split counts and workgroup sizes away from the default plan (the LDS merge of 1..8 waves,
+    split partials merged by the tail kernel)."""
+
+    announce(f"tree mfma forced splits={splits} warps={warps}")
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", splits)
+    monkeypatch.setenv("FLASHSPEC_NUM_WARPS", warps)
+    monkeypatch.setenv("FLASHSPEC_BLOCK_N", "16")
+    B, H, S, D, N = 2, 4, 1500, 128, 10
+    parents = _random_parents(B, N, 8)
+    got, ref, stats = _run(B, H, S, D, N, parents, [1500, 700], seed=43, kernel="mfma")
+    assert stats["num_warps"] == float(warps)
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, "forced plan")
+
+
+def test_tree_mfma_agrees_with_row_kernel():
+    """Both prefix kernels on one input: within the attention tolerance of each other."""
+
+    announce("tree mfma vs rows")
+    B, H, S, D, N = 4, 8, 2048, 128, 16
+    parents = _random_parents(B, N, 9)
+    q = randn((B, N, H, D), 51).to(DEV)
+    k, v = randn((B, H, S, D), 52).to(DEV), randn((B, H, S, D), 53).to(DEV)
+    dk, dv = randn((B, N, H, D), 54).to(DEV), randn((B, N, H, D), 55).to(DEV)
+    cache = fa.PagedKVCache.from_dense(k, v, 16, lengths=torch.tensor([2048, 1000, 17, 1600]).to(DEV),
+                                       block_table_pattern="shuffled", layout_seed=4)
+    par = torch.tensor(parents)
+    a = fa.tree_verify_attention(q, cache, dk, dv, par, kernel="mfma")
+    b = fa.tree_verify_attention(q, cache, dk, dv, par, kernel="rows")
+    torch.cuda.synchronize(DEV)
+    ref = ot.tree_verify_attention(np_of(q.cpu().float()), from_cache(cache), np_of(dk.cpu().float()),
+                                   np_of(dv.cpu().float()), parents)
+    assert_attention_close(a.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, "mfma")
+    assert_attention_close(b.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, "rows")
+    assert float((a.float() - b.float()).abs().max()) <= 2e-3
+
+
+def test_tree_deep_chain_64_nodes():
+    """A 64-node chain: the tail's register walk sets every bit of the path mask (node 63 sees
+    all 64 drafts); with the prefix it is plain attention over prefix + chain."""
+
+    announce("tree 64-node chain")
+    B, H, S, D, N = 2, 2, 150, 128, 64
+    parents = np.tile(np.arange(-1, N - 1), (B, 1))
+    for kernel in ("mfma", "rows"):
+        got, ref, _ = _run(B, H, S, D, N, parents, [150, 40], seed=61, kernel=kernel)
+        assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, f"chain {kernel}")

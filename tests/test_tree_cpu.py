@@ -48,3 +48,6 @@ def test_tree_validation():
         fa.tree_verify_attention(q, cache, dk, dv, torch.tensor([[-1.0, 0.0, 0.0]]))
     assert validate_parents(torch.tensor([[-1, 0, 1]], dtype=torch.int32), 1, 3).dtype == torch.int64
     assert path_mask(torch.tensor([[-1, 0, 0, 2]]))[0].tolist() == ot.path_mask(np.array([[-1, 0, 0, 2]]))[0].tolist()
+    # validate=False only skips the check for parents already on the GPU: CPU calls still check
+    with pytest.raises(ValueError):
+        fa.tree_verify_attention(q, cache, dk, dv, torch.tensor([[-1, 0, 5]]), validate=False)
