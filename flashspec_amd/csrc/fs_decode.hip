@@ -602,136 +602,6 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
   }
 }
 
-// ---- tree verification tail -------------------------------------------------------------------
-
-// Row = (b * nq + n) * heads + h of a tree verification: merges the prefix partial states the
-// prefix kernel left for the row (one per split the row's length needs), then attends to the
-// draft tokens on node n's path to the root (parents[b, a]; a parent outside [0, a) ends the
-// path, at most nq steps) with the same online softmax, and writes the output.  With nq <= 64
-// the request's parents are loaded once, one per lane, and the path is walked in registers;
-// its tokens are then taken four at a time, so their K/V rows load together.
-template <typename QT, typename DT>
-__global__ void __launch_bounds__(256)
-tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* lengths, const QT* q, const DT* dk,
-                 const DT* dv, const int64_t* parents, QT* out, int rows, int heads, int nq, int D, int seq_len,
-                 int split_tiles, int max_splits, float qk_scale) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
-  if (row >= rows) return;
-  const int h = row % heads;
-  const int bn = row / heads;
-  const int b = bn / nq;
-  const int n = bn - b * nq;
-  int pl = -1;  // this lane's node's parent, sanitized (nq <= 64)
-  if (nq <= kWave && lane < nq) {
-    const int64_t pa = parents[(size_t)b * nq + lane];
-    pl = (pa >= 0 && pa < lane) ? (int)pa : -1;
-  }
-  const int nsplit = row_splits(row_length(lengths, b, seq_len), split_tiles);
-  const float* ml = part_ml + (size_t)row * max_splits * 2;
-  const float* pacc = part_acc + (size_t)row * max_splits * D;
-  float M = kNegBig;
-  for (int sp = lane; sp < nsplit; sp += kWave) M = fmaxf(M, ml[2 * sp]);
-  M = wave_max(M);
-  float L = 0.f;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int sp = 0; sp < nsplit; ++sp) {
-    const float wgt = fast_exp2(ml[2 * sp] - M);
-    L = fmaf(ml[2 * sp + 1], wgt, L);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = lane + c * kWave;
-      if (d < D) acc[c] = fmaf(pacc[(size_t)sp * D + d], wgt, acc[c]);
-    }
-  }
-  float qv[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int d = lane + c * kWave;
-    qv[c] = d < D ? to_f32(q[(size_t)row * D + d]) : 0.f;
-  }
-  if (nq <= kWave) {
-    uint64_t path = 0;
-    for (int a = n, step = 0; step < nq && a >= 0; ++step) {
-      path |= 1ull << a;
-      a = __builtin_amdgcn_readlane(pl, a);
-    }
-    while (path) {
-      int idx[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        idx[i] = path ? __builtin_ctzll(path) : -1;
-        path &= path - 1;  // no-op once empty
-      }
-      float kx[4][4], vx[4][4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const size_t kr = (((size_t)b * nq + (idx[i] < 0 ? 0 : idx[i])) * heads + h) * D;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int d = lane + c * kWave;
-          const bool ok = idx[i] >= 0 && d < D;
-          kx[i][c] = ok ? to_f32(dk[kr + d]) : 0.f;
-          vx[i][c] = ok ? to_f32(dv[kr + d]) : 0.f;
-        }
-      }
-      float sc[4];
-      float mn = M;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float dot = 0.f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) dot = fmaf(qv[c], kx[i][c], dot);
-        sc[i] = wave_sum(dot) * qk_scale;
-        if (idx[i] >= 0) mn = fmaxf(mn, sc[i]);
-      }
-      const float alpha = fast_exp2(M - mn);
-      L *= alpha;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] *= alpha;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pr = idx[i] >= 0 ? fast_exp2(sc[i] - mn) : 0.f;
-        L += pr;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] = fmaf(pr, vx[i][c], acc[c]);
-      }
-      M = mn;
-    }
-  } else {
-    int a = n;
-    for (int step = 0; step < nq && a >= 0; ++step) {
-      const size_t kr = (((size_t)b * nq + a) * heads + h) * D;
-      float dot = 0.f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d = lane + c * kWave;
-        if (d < D) dot = fmaf(qv[c], to_f32(dk[kr + d]), dot);
-      }
-      const float sc = wave_sum(dot) * qk_scale;
-      const float mn = fmaxf(M, sc);
-      const float alpha = fast_exp2(M - mn), pr = fast_exp2(sc - mn);
-      L = L * alpha + pr;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d = lane + c * kWave;
-        const float v = d < D ? to_f32(dv[kr + d]) : 0.f;
-        acc[c] = fmaf(pr, v, acc[c] * alpha);
-      }
-      M = mn;
-      const int64_t pa = parents[(size_t)b * nq + a];
-      a = (pa >= 0 && pa < a) ? (int)pa : -1;
-    }
-  }
-  QT* o = out + (size_t)row * D;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int d = lane + c * kWave;
-    if (d < D) o[d] = from_f32<QT>(L > 0.f ? acc[c] / L : 0.f);
-  }
-}
-
 // ---- host launchers --------------------------------------------------------------------------
 
 // Tiled path: head_dim a multiple of 16 up to 256 (served by the 64-, 128- or 256-dim
@@ -779,6 +649,10 @@ static int launch_decode(const DecodeParams& p, int q_dtype, bool tiled, int wav
     case FS_BF16: return launch_typed<__hip_bfloat16, PAGED>(p, tiled, waves_per_block, st);
     default: return set_error(FS_ERR_INVALID, "q dtype code must be 0 (f32), 1 (f16) or 2 (bf16)");
   }
+}
+
+int launch_paged_rows(const DecodeParams& p, int q_dtype, bool tiled, int waves_per_block, hipStream_t st) {
+  return launch_decode<true>(p, q_dtype, tiled, waves_per_block, st);
 }
 
 // Workspace layout: part_acc [rows, max_splits, D] first, then part_ml [rows, max_splits, 2].
@@ -832,10 +706,6 @@ extern "C" int fs_decode_tiled_path(int head_dim, int page_size, int quant_block
   return tiled_path(head_dim, page_size, quant_block) ? 1 : 0;
 }
 
-extern "C" int fs_tree_mfma_path(int head_dim, int page_size, int quant_block) {
-  return tree_mfma_path(head_dim, page_size, quant_block) ? 1 : 0;
-}
-
 extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
                                   const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
                                   const int16_t* v_zero, const int64_t* lengths, void* out, void* workspace,
@@ -865,15 +735,15 @@ extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_va
   return launch_decode<false>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }
 
-// Parameters and checks shared by the paged decode and the tree verification entry points;
-// `rows_per_request` = query rows per request (heads * nodes).
-static int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_values, const float* k_scale,
+// Parameters and checks shared by the paged decode and the tree verification entry points
+// (`nq` query rows per request and head).
+int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_values, const float* k_scale,
                         const int16_t* k_zero, const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
                         const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
                         void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads,
                         int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
                         float sm_scale, int split_tiles, int max_splits, int waves_per_block,
-                        bool row_kernel = true) {
+                        bool row_kernel) {
   p = DecodeParams{};
   p.q = q;
   p.kv[0] = k_values; p.kv[1] = v_values;
@@ -950,68 +820,3 @@ extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, 
   return check_launch("combine_splits_kernel");
 }
 
-template <typename QT, typename DT>
-static void launch_tree_tail(const DecodeParams& p, const void* dk, const void* dv, const int64_t* parents, int nq,
-                             hipStream_t st) {
-  const dim3 grid((unsigned)(((int64_t)p.rows + 3) / 4)), block(256);
-  hipLaunchKernelGGL((tree_tail_kernel<QT, DT>), grid, block, 0, st, p.part_ml, p.part_acc, p.lengths,
-                     (const QT*)p.q, (const DT*)dk, (const DT*)dv, parents, (QT*)p.out, p.rows, p.heads, nq,
-                     p.head_dim, p.seq_len, p.split_tiles, p.max_splits, p.qk_scale);
-}
-
-template <typename QT>
-static int launch_tree_tail_q(const DecodeParams& p, const void* dk, const void* dv, int draft_dtype,
-                              const int64_t* parents, int nq, hipStream_t st) {
-  switch (draft_dtype) {
-    case FS_F32: launch_tree_tail<QT, float>(p, dk, dv, parents, nq, st); break;
-    case FS_F16: launch_tree_tail<QT, __half>(p, dk, dv, parents, nq, st); break;
-    case FS_BF16: launch_tree_tail<QT, __hip_bfloat16>(p, dk, dv, parents, nq, st); break;
-    default: return set_error(FS_ERR_INVALID, "draft dtype code must be 0, 1 or 2");
-  }
-  return check_launch("tree_verify_tail");
-}
-
-extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
-                                 const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
-                                 const int16_t* v_zero, const void* block_table, int table_index_bytes,
-                                 int64_t table_cols, const int64_t* lengths, const void* draft_k, const void* draft_v,
-                                 int draft_dtype, const int64_t* parents, void* out, void* workspace,
-                                 int64_t workspace_bytes, int batch, int nodes, int heads, int head_dim,
-                                 int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
-                                 int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
-                                 void* stream) {
-  if (prefix_kernel < 0 || prefix_kernel > 2)
-    return set_error(FS_ERR_INVALID, "prefix_kernel must be 0 (auto), 1 (row kernel) or 2 (multi-query kernel)");
-  const bool mq_ok = tree_mfma_path(head_dim, page_size, quant_block);
-  if (prefix_kernel == 2 && !mq_ok)
-    return set_error(FS_ERR_INVALID, "the multi-query tree kernel needs head_dim 64/128/256, pages of 16k tokens "
-                                     "and quant blocks of 16k tokens (or 1)");
-  const bool mq = mq_ok && prefix_kernel != 1;
-  DecodeParams p;
-  bool tiled = false;
-  if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
-                            table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, nodes,
-                            heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
-                            max_splits, waves_per_block, !mq))
-    return rc;
-  if (!draft_k || !draft_v || !parents) return set_error(FS_ERR_INVALID, "tree verify: null draft or parents pointer");
-  if (draft_dtype != FS_F32 && draft_dtype != FS_F16 && draft_dtype != FS_BF16)
-    return set_error(FS_ERR_INVALID, "draft dtype code must be 0, 1 or 2");
-  p.force_partials = 1;
-  const int64_t need = fs_decode_workspace_bytes(p.rows, p.max_splits, p.head_dim);
-  if (workspace_bytes < need || p.part_acc == nullptr)
-    return set_error(FS_ERR_INVALID, "tree verify workspace too small (" + std::to_string(workspace_bytes) + " < " +
-                                         std::to_string(need) + " bytes)");
-  hipStream_t st = (hipStream_t)stream;
-  if (mq) {
-    if (int rc = launch_tree_prefix_mfma(p, q_dtype, waves_per_block, st)) return rc;
-  } else if (int rc = launch_decode<true>(p, q_dtype, tiled, waves_per_block, st)) {
-    return rc;
-  }
-  switch (q_dtype) {
-    case FS_F32: return launch_tree_tail_q<float>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
-    case FS_F16: return launch_tree_tail_q<__half>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
-    case FS_BF16: return launch_tree_tail_q<__hip_bfloat16>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
-    default: return set_error(FS_ERR_INVALID, "q dtype code must be 0 (f32), 1 (f16) or 2 (bf16)");
-  }
-}

@@ -42,6 +42,12 @@ struct DecodeParams {
   // writes split partials for every row (force_partials) for the tree-tail merge.
   int nq;
   int force_partials;
+  // Multi-query tree kernel with one split: it finishes the rows itself (path tokens from
+  // draft_k / draft_v, which then have q's dtype, and parents) instead of leaving partials.
+  int fuse_tail;
+  const void* draft_k;
+  const void* draft_v;
+  const int64_t* parents;
 };
 
 __device__ __forceinline__ int queries_per_head(const DecodeParams& p) { return p.nq > 1 ? p.nq : 1; }
@@ -171,10 +177,16 @@ __device__ __forceinline__ uint4 stream_load(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Multi-query (tree verification) prefix kernel of fs_tree.hip: whether it serves a store
-// shape, and its launch (split partials for every (request, node, head) row).
-bool tree_mfma_path(int head_dim, int page_size, int quant_block);
-int tree_mfma_max_waves(int head_dim);
-int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves_per_block, hipStream_t st);
+// Paged-store parameters and checks (fs_decode.hip), shared with the tree verification entry
+// point; row_kernel = false leaves the workgroup-size checks to the multi-query tree kernel.
+int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_values, const float* k_scale,
+                 const int16_t* k_zero, const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                 const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
+                 void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads, int head_dim,
+                 int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
+                 int max_splits, int waves_per_block, bool row_kernel = true);
+
+// The paged decode row kernel on `p` (fs_decode.hip).
+int launch_paged_rows(const DecodeParams& p, int q_dtype, bool tiled, int waves_per_block, hipStream_t st);
 
 }  // namespace fs

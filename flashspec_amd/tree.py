@@ -6,15 +6,17 @@ request b carries N draft nodes in topological order with ``parents[b, n]`` in [
 (tokens [0, lengths[b]) of a ``PagedKVCache``) and to the draft tokens on its own root path
 (n and its ancestors), never to siblings or other branches.  Draft K/V are unquantized.
 
-On GPU, ``fs_tree_verify_i8`` runs the paged decode kernel with one query row per node
-(the N rows of one request and head are scheduled together on one XCD, so the prefix pages
-they share are read from HBM once) and a tail kernel that merges the prefix partial states
-with the path tokens.  On CPU the dense tree-mask formulation runs in torch.
+On GPU, ``fs_tree_verify_i8`` runs a multi-query prefix kernel (one wave reads each prefix
+tile once for 16 nodes, matrix-core products; head_dim 64/128/256, pages of 16k tokens) or,
+for other stores, the paged decode kernel with one query row per node; a tail merges the
+prefix state with the path tokens (inside the prefix kernel when it runs one split).  On CPU
+the dense tree-mask formulation runs in torch.
 """
 
 from __future__ import annotations
 
 import math
+from collections import OrderedDict
 from typing import Any
 
 import numpy as np
@@ -25,7 +27,7 @@ from .paged import PagedKVCache
 from .quant import build_compression_stats
 from .triton_utils import TREE_NODE_GROUP, device_cu_count, launch_plan, plan_tree_splits
 
-__all__ = ["tree_verify_attention", "validate_parents", "path_mask"]
+__all__ = ["tree_verify_attention", "validate_parents", "path_mask", "tree_shape"]
 
 
 def validate_parents(parents: torch.Tensor, batch: int, nodes: int) -> torch.Tensor:
@@ -92,7 +94,7 @@ def _portable(q, cache, draft_k, draft_v, parents_host):
 _KERNELS = {"auto": 0, "rows": 1, "mfma": 2}
 
 
-def _hip(q, cache, draft_k, draft_v, parents_host, dims, kernel):
+def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
     batch, nodes, heads, head_dim = dims
     lib = _lib.require()
     dev = q.device
@@ -104,10 +106,6 @@ def _hip(q, cache, draft_k, draft_v, parents_host, dims, kernel):
     q_c, dk_c, dv_c = q.contiguous(), draft_k.contiguous(), draft_v.contiguous()
     table = cache.block_table.contiguous()
     lengths = cache.lengths.to(torch.int64).contiguous()
-    if parents_host.device.type == "cpu":
-        parents_dev = parents_host.pin_memory().to(dev, non_blocking=True)
-    else:
-        parents_dev = parents_host.to(torch.int64).contiguous()
     rows = batch * nodes * heads
     max_seq_len = int(cache.max_seq_len)
     mfma_ok = bool(lib.fs_tree_mfma_path(head_dim, int(cache.block_size), int(kq.block_size)))
@@ -151,7 +149,8 @@ def tree_verify_attention(q: torch.Tensor, cache: PagedKVCache, draft_k: torch.T
 
     ``parents`` on the CPU (the usual case: the drafter builds the tree on the host) is
     checked there and copied to the GPU through pinned memory without waiting for the
-    device.  ``parents`` already on the GPU is copied back to check it, which waits for
+    device; the validated device copy is kept (by content) for later calls with the same
+    topology.  ``parents`` already on the GPU is copied back to check it, which waits for
     the device; ``validate=False`` skips that check, and the kernel then ends a node's path
     at the first parent outside [-1, own index) (never reading out of bounds).
 
@@ -164,34 +163,82 @@ def tree_verify_attention(q: torch.Tensor, cache: PagedKVCache, draft_k: torch.T
     if kernel not in _KERNELS:
         raise ValueError(f"kernel must be one of {sorted(_KERNELS)}")
     dims = _validate(q, cache, draft_k, draft_v)
-    if validate or parents.device.type != "cuda" or q.device.type != "cuda":
-        parents_host = validate_parents(parents, dims[0], dims[1])
-    else:
-        if parents.ndim != 2 or tuple(parents.shape) != dims[:2] or parents.dtype not in (torch.int32, torch.int64):
-            raise ValueError(f"parents must be an int32/int64 [batch, nodes] = [{dims[0]}, {dims[1]}] tensor")
-        parents_host = parents
+    batch, nodes, heads, head_dim = dims
+    parents_host = None
     if q.device.type == "cuda":
-        out, plan = _hip(q, cache, draft_k, draft_v, parents_host, dims, kernel)
+        if parents.device.type == "cpu":
+            parents_dev = _device_parents(parents, batch, nodes, q.device)
+            parents_host = parents
+        elif validate:
+            parents_host = validate_parents(parents, batch, nodes)
+            parents_dev = parents.to(torch.int64).contiguous()
+        else:
+            if parents.ndim != 2 or tuple(parents.shape) != (batch, nodes) or \
+                    parents.dtype not in (torch.int32, torch.int64):
+                raise ValueError(f"parents must be an int32/int64 [batch, nodes] = [{batch}, {nodes}] tensor")
+            parents_dev = parents.to(torch.int64).contiguous()
+        out, plan = _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel)
         materializes = False
     else:
+        parents_host = validate_parents(parents, batch, nodes)
         out, plan = _portable(q, cache, draft_k, draft_v, parents_host), {}
         materializes = True
     if not return_stats:
         return out
-    batch, nodes, heads, head_dim = dims
     dense_bytes = 2 * batch * heads * int(cache.max_seq_len) * head_dim * q.element_size()
-    depth = float(_depth(parents_host)) if parents_host.device.type == "cpu" else float("nan")
+    shape = tree_shape(parents_host) if parents_host is not None else {}
     stats = build_compression_stats(dense_bytes, cache.estimated_bytes(), materializes_dense_kv=materializes,
-                                    tree_nodes=float(nodes), tree_depth=depth, **plan)
+                                    tree_nodes=float(nodes), tree_depth=float(shape.get("depth", float("nan"))),
+                                    tree_leaves=float(shape.get("leaves", float("nan"))),
+                                    tree_max_branch=float(shape.get("max_branch", float("nan"))), **plan)
     return out, stats
 
 
-def _depth(parents_host: torch.Tensor) -> int:
-    batch, nodes = parents_host.shape
-    depth = torch.ones((batch, nodes), dtype=torch.int64)
+# Validated device copies of host parents tensors, keyed by content: a drafter with a static
+# tree topology (one parents tensor reused every step) pays neither the check nor the copy
+# after the first call.  A copy made on another stream is waited for through its event.
+_PARENTS_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+_PARENTS_CACHE_ENTRIES = 16
+
+
+def _device_parents(parents: torch.Tensor, batch: int, nodes: int, dev: torch.device) -> torch.Tensor:
+    host = parents.detach().to(torch.int64).contiguous()
+    if tuple(host.shape) != (batch, nodes):
+        raise ValueError(f"parents must be [batch, nodes] = [{batch}, {nodes}]")
+    key = (dev.index, batch, nodes, host.numpy().tobytes())
+    stream = torch.cuda.current_stream(dev)
+    hit = _PARENTS_CACHE.get(key)
+    if hit is not None:
+        _PARENTS_CACHE.move_to_end(key)
+        tensor, made_on, ready = hit
+        if made_on != stream:
+            stream.wait_event(ready)
+        return tensor
+    validate_parents(parents, batch, nodes)
+    tensor = host.pin_memory().to(dev, non_blocking=True)
+    ready = torch.cuda.Event()
+    ready.record(stream)
+    _PARENTS_CACHE[key] = (tensor, stream, ready)
+    if len(_PARENTS_CACHE) > _PARENTS_CACHE_ENTRIES:
+        _PARENTS_CACHE.popitem(last=False)
+    return tensor
+
+
+def tree_shape(parents: torch.Tensor) -> dict:
+    """Largest depth (nodes on a root path), leaf count and branching factor over the batch of
+    a validated ``parents`` (host or device tensor; [batch, nodes])."""
+
+    a = parents.detach().to("cpu", torch.int64).numpy()
+    batch, nodes = a.shape
+    if nodes == 0:
+        return {"depth": 0, "leaves": 0, "max_branch": 0}
+    depth = np.ones((batch, nodes), dtype=np.int64)
     for n in range(nodes):
-        par = parents_host[:, n]
+        par = a[:, n]
         has = par >= 0
-        if bool(has.any()):
-            depth[has, n] = depth[has, par[has]] + 1
-    return int(depth.max().item()) if nodes else 0
+        depth[has, n] = depth[has, par[has]] + 1
+    children = np.zeros((batch, nodes + 1), dtype=np.int64)  # column nodes: children of the root
+    for b in range(batch):
+        np.add.at(children[b], np.where(a[b] >= 0, a[b], nodes), 1)
+    leaves = int((children[:, :nodes] == 0).sum(axis=1).max())
+    return {"depth": int(depth.max()), "leaves": leaves, "max_branch": int(children.max())}

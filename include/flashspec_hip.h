@@ -121,6 +121,8 @@ int fs_paged_decode_i8(const void* q, int q_dtype,
  *       MFMA products (fs_tree_mfma_path() stores; waves_per_block 1/2/4/8, <= 4 for
  *       head_dim 256; split plan over batch*heads*ceil(nodes/16) workgroups per split);
  *   0 = 2 where fs_tree_mfma_path() holds, else 1.
+ * With the multi-query kernel, one split (max_splits == 1) and drafts in q's dtype, the prefix
+ * kernel finishes the rows itself (path tokens and output; no tail launch, workspace unused).
  *   q, out          [batch, nodes, heads, head_dim]  q_dtype
  *   draft_k/draft_v [batch, nodes, heads, head_dim]  draft_dtype (unquantized)
  *   parents         [batch, nodes] int64, parents[b, n] in [-1, n) (the caller validates;

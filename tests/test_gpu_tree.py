@@ -48,12 +48,12 @@ def _random_parents(B, N, seed):
 
 
 def _run(B, H, S, D, N, parents, lengths, page=16, layout="shuffled", q_dtype=torch.float16, kv_format="affine_block",
-         seed=0, kernel="auto", q_scale=1.0):
+         seed=0, kernel="auto", q_scale=1.0, draft_dtype=torch.float16):
     q = (randn((B, N, H, D), seed + 1, torch.float32) * q_scale).to(q_dtype)
     k = randn((B, H, S, D), seed + 2)
     v = randn((B, H, S, D), seed + 3)
-    dk = randn((B, N, H, D), seed + 4)
-    dv = randn((B, N, H, D), seed + 5)
+    dk = randn((B, N, H, D), seed + 4, torch.float32).to(draft_dtype)
+    dv = randn((B, N, H, D), seed + 5, torch.float32).to(draft_dtype)
     cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), page, lengths=torch.tensor(lengths).to(DEV),
                                        block_table_pattern=layout, layout_seed=seed, kv_format=kv_format)
     got, stats = fa.tree_verify_attention(q.to(DEV), cache, dk.to(DEV), dv.to(DEV),
@@ -232,3 +232,46 @@ def test_tree_deep_chain_64_nodes():
     for kernel in ("mfma", "rows"):
         got, ref, _ = _run(B, H, S, D, N, parents, [150, 40], seed=61, kernel=kernel)
         assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, f"chain {kernel}")
+
+
+@pytest.mark.parametrize("D,fmt,dtype,N", [(128, "affine_block", torch.float16, 16), (64, "symmetric_token", torch.bfloat16, 40),
+                                          (256, "affine_block", torch.float32, 9), (128, "symmetric_token", torch.float16, 70)])
+def test_tree_mfma_fused_tail(monkeypatch, D, fmt, dtype, N):
+    """One split and drafts in q's dtype: the multi-query kernel finishes the rows itself (its
+    LDS-merged prefix state plus the path tokens; > 64 nodes walk parents in memory)."""
+
+    announce(f"tree mfma fused tail D{D} {fmt} {dtype} N{N}")
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", "1")
+    B, H, S = 2, 4, 700
+    parents = _random_parents(B, N, D + N)
+    got, ref, stats = _run(B, H, S, D, N, parents, [700, 333], kv_format=fmt, q_dtype=dtype, draft_dtype=dtype,
+                           seed=D + N, kernel="mfma")
+    assert stats["num_splits"] == 1.0
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), dtype, "fused tail")
+
+
+def test_tree_parents_cache_reuse_and_change():
+    """A host parents tensor reused across calls is served from the device cache; changing its
+    contents (in place) gives a different, correct tree."""
+
+    announce("tree parents cache")
+    B, H, S, D, N = 2, 4, 300, 128, 8
+    q = randn((B, N, H, D), 71).to(DEV)
+    k, v = randn((B, H, S, D), 72).to(DEV), randn((B, H, S, D), 73).to(DEV)
+    dk, dv = randn((B, N, H, D), 74).to(DEV), randn((B, N, H, D), 75).to(DEV)
+    cache = fa.PagedKVCache.from_dense(k, v, 16, block_table_pattern="shuffled", layout_seed=5)
+    par = torch.tensor(_random_parents(B, N, 3))
+    outs = []
+    for _ in range(2):
+        outs.append(fa.tree_verify_attention(q, cache, dk, dv, par))
+    par.numpy()[0, 5] = -1  # in place, behind torch's version counter
+    outs.append(fa.tree_verify_attention(q, cache, dk, dv, par))
+    torch.cuda.synchronize(DEV)
+    assert torch.equal(outs[0], outs[1])
+    ref = ot.tree_verify_attention(np_of(q.cpu().float()), from_cache(cache), np_of(dk.cpu().float()),
+                                   np_of(dv.cpu().float()), par.numpy())
+    assert_attention_close(outs[2].reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, "changed tree")
+    with pytest.raises(ValueError):
+        bad = par.clone()
+        bad[1, 2] = 5
+        fa.tree_verify_attention(q, cache, dk, dv, bad)

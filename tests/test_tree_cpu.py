@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import flashspec_amd as fa
-from flashspec_amd.tree import path_mask, validate_parents
+from flashspec_amd.tree import path_mask, tree_shape, validate_parents
 from oracle import tree as ot
 from tests._helpers import from_cache
 
@@ -51,3 +51,12 @@ def test_tree_validation():
     # validate=False only skips the check for parents already on the GPU: CPU calls still check
     with pytest.raises(ValueError):
         fa.tree_verify_attention(q, cache, dk, dv, torch.tensor([[-1, 0, 5]]), validate=False)
+
+
+
+def test_tree_shape_counts():
+    # request 0: root children {0, 4}, node 0 -> {1, 2}, 1 -> {3}, 4 -> {5}: leaves 2, 3, 5
+    # request 1: a chain of 6
+    shape = tree_shape(torch.tensor([[-1, 0, 0, 1, -1, 4], [-1, 0, 1, 2, 3, 4]]))
+    assert shape == {"depth": 6, "leaves": 3, "max_branch": 2}
+    assert tree_shape(torch.tensor([[-1, -1, -1]])) == {"depth": 1, "leaves": 3, "max_branch": 3}
