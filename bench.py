@@ -35,11 +35,13 @@ PMC_SUMMARY = ROOT / "profiles" / "paged_decode_b8h32s4096d128_pmc.json"
 
 
 def algorithmic_bytes(lengths, heads: int, head_dim: int, page: int, q_bytes: int = 2, idx_bytes: int = 8,
-                      quant_block: int | None = None) -> int:
+                      quant_block: int | None = None, param_bytes: int = 6) -> int:
+    """param_bytes per quant block and tensor: fp32 scale + int16 zero (INT8), fp32 scale (FP8)."""
+
     pages = sum(math.ceil(L / page) for L in lengths)
     blocks = sum(math.ceil(L / (quant_block or page)) for L in lengths)
     kv = 2 * sum(lengths) * heads * head_dim
-    params = 2 * blocks * heads * (4 + 2)
+    params = 2 * blocks * heads * param_bytes
     table = pages * idx_bytes
     return kv + params + table + 8 * len(lengths) + 2 * len(lengths) * heads * head_dim * q_bytes
 
@@ -214,8 +216,9 @@ def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
             "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1)}
 
 
-# Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths);
-# quant block 1 = symmetric absmax INT8 with one scale per token (quantize_int8_symmetric_per_token).
+# Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths
+# [, format]); quant block 1 = symmetric absmax INT8 with one scale per token
+# (quantize_int8_symmetric_per_token), or one FP8 scale per token with format "fp8".
 SHAPES = [
     ("metric", 8, 32, 4096, 128, 16, 16, "float16", None),
     ("c3_s2048", 8, 32, 2048, 128, 16, 16, "float16", None),
@@ -235,6 +238,10 @@ SHAPES = [
     ("batch_1_splitk", 1, 32, 16384, 128, 16, 16, "float16", None),
     ("c1_symmetric_per_token", 4, 32, 2048, 128, 16, 1, "float16", None),
     ("c2_symmetric_per_token", 8, 32, 4096, 128, 16, 1, "float16", None),
+    ("metric_fp8", 8, 32, 4096, 128, 16, 16, "float16", None, "fp8"),
+    ("head_dim_64_fp8", 8, 32, 4096, 64, 16, 16, "float16", None, "fp8"),
+    ("q_bfloat16_fp8", 8, 32, 4096, 128, 16, 16, "bfloat16", None, "fp8"),
+    ("fp8_per_token", 8, 32, 4096, 128, 16, 1, "float16", None, "fp8"),
 ]
 
 
@@ -264,7 +271,8 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
     JSON object per shape."""
 
     out = []
-    for name, b, h, s, d, page, qb, qdt, lens in SHAPES:
+    for name, b, h, s, d, page, qb, qdt, lens, *rest in SHAPES:
+        fmt = rest[0] if rest else "int8"
         g = torch.Generator(device=dev)
         g.manual_seed(11)
         qdtype = getattr(torch, qdt)
@@ -274,7 +282,21 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
             k = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
             v = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
             lt = None if lens is None else torch.tensor(lens, dtype=torch.int64, device=dev)
-            if qb == 1:
+            if fmt == "fp8":
+                if qb == 1:
+                    pk = fa.PagedKVCache._physical_pages(k, page, None)
+                    pv = fa.PagedKVCache._physical_pages(v, page, None)
+                    nbps = (s + page - 1) // page
+                    cache = fa.PagedKVCache(
+                        k_quant=fa.quantize_fp8_per_block(pk, 1), v_quant=fa.quantize_fp8_per_block(pv, 1),
+                        block_table=torch.arange(b * nbps, dtype=torch.int64, device=dev).reshape(b, nbps),
+                        lengths=lt if lt is not None else torch.full((b,), s, dtype=torch.int64, device=dev),
+                        block_size=page, max_seq_len=s)
+                    del pk, pv
+                else:
+                    cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt, kv_format="fp8_block")
+                kq, vq = fa.quantize_fp8_per_block(k, qb), fa.quantize_fp8_per_block(v, qb)
+            elif qb == 1:
                 cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt, kv_format="symmetric_token")
                 kq, vq = fa.quantize_int8_symmetric_per_token(k), fa.quantize_int8_symmetric_per_token(v)
             else:
@@ -287,12 +309,13 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
             del k, v
             sets.append((q, cache, kq, vq, lt))
         lengths = lens or [s] * b
-        nbytes = algorithmic_bytes(lengths, h, d, page, q_bytes=torch.finfo(qdtype).bits // 8, quant_block=qb)
+        nbytes = algorithmic_bytes(lengths, h, d, page, q_bytes=torch.finfo(qdtype).bits // 8, quant_block=qb,
+                                   param_bytes=4 if fmt == "fp8" else 6)
         ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(sets[i % ROTATE][0], sets[i % ROTATE][1]),
                        steps, warmup)
         _, st = fa.paged_quant_attention_triton(sets[0][0], sets[0][1], return_stats=True)
-        row = {"shape": name, "batch": b, "heads": h, "seq_len": s, "head_dim": d, "page": page, "quant_block": qb,
-               "q_dtype": qdt, "paged_us": round(ms * 1e3, 2), "paged_pct_of_peak": round(
+        row = {"shape": name, "format": fmt, "batch": b, "heads": h, "seq_len": s, "head_dim": d, "page": page,
+               "quant_block": qb, "q_dtype": qdt, "paged_us": round(ms * 1e3, 2), "paged_pct_of_peak": round(
                    100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
                "tiled_path": bool(st["tiled_path"]), "num_splits": st["num_splits"], "waves": st["num_warps"]}
         fms = time_loop(torch, lambda i: fa.fused_dequant_attention_triton(

@@ -44,6 +44,22 @@ _SIGNATURES = {
          c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_void_p],
     ),
     "fs_tree_mfma_path": (c_int, [c_int, c_int, c_int]),
+    "fs_quantize_fp8": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "fs_quantize_pages_fp8": (
+        c_int,
+        [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "fs_dequantize_fp8": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p]),
+    "fs_fused_decode_fp8": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int,
+         c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+    ),
+    "fs_paged_decode_fp8": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p,
+         c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+    ),
     "fs_combine_splits": (
         c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p]
     ),

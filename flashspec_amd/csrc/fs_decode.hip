@@ -20,6 +20,8 @@
 // src/flashspec/triton_paged.py:119-299 (masking of tokens past the row length and
 // of unallocated pages; a row with no valid token writes zeros, triton_utils.py:181-186).
 
+#include <type_traits>
+
 #include "fs_paged.h"
 
 namespace fs {
@@ -66,9 +68,44 @@ __device__ __forceinline__ float dot16_u8_f16(const uint32_t* qp, uint4 raw) {
   return a0 + a1;
 }
 
-// Query slice of one lane (16 dims) in the form its K dot product wants.
+// FP8 E4M3 bytes (value format kVfFp8): v_cvt_pk_f32_fp8 decodes two codes per instruction,
+// exactly; the products and sums are fp32.
+
+__device__ __forceinline__ float dot16_fp8(const float* q, uint4 raw) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], true);
+    a0 = fmaf(q[4 * k + 0], lo[0], a0);
+    a1 = fmaf(q[4 * k + 1], lo[1], a1);
+    a0 = fmaf(q[4 * k + 2], hi[0], a0);
+    a1 = fmaf(q[4 * k + 3], hi[1], a1);
+  }
+  return a0 + a1;
+}
+
+__device__ __forceinline__ void axpy16_fp8(float* acc, float wgt, uint4 raw) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], true);
+    acc[4 * k + 0] = fmaf(wgt, lo[0], acc[4 * k + 0]);
+    acc[4 * k + 1] = fmaf(wgt, lo[1], acc[4 * k + 1]);
+    acc[4 * k + 2] = fmaf(wgt, hi[0], acc[4 * k + 2]);
+    acc[4 * k + 3] = fmaf(wgt, hi[1], acc[4 * k + 3]);
+  }
+}
+
+__device__ __forceinline__ float fp8_value(int8_t code) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)(uint8_t)code, false)[0];
+}
+
+// Query slice of one lane (16 dims) as fp32, for both value formats.
 template <typename QT>
-struct QSlice {
+struct QSliceF {
   static constexpr float kOffset = 0.f;  // dot16 returns sum q*u
   float q[16];
   __device__ __forceinline__ void load(const QT* qp) {
@@ -86,7 +123,13 @@ struct QSlice {
     return s;
   }
   __device__ __forceinline__ float dot(uint4 raw) const { return dot16_u8(q, raw); }
+  __device__ __forceinline__ float dot_fp8(uint4 raw) const { return dot16_fp8(q, raw); }
 };
+
+// Query slice in the form the INT8 K dot product wants: fp32 in general, fp16 pairs for fp16
+// queries (below).
+template <typename QT>
+struct QSlice : QSliceF<QT> {};
 
 template <>
 struct QSlice<__half> {
@@ -178,7 +221,7 @@ __device__ __forceinline__ void load_tile_sub(TileRegs<DP>& t, const int8_t* kba
 // Token mode: `base` is the tile's first token in the store (units of D bytes), which also
 // indexes the per-token scale / zero arrays; rows at or past `avail` (stored tokens left from
 // `base`, short only at the end of a contiguous row) read row 0 and are masked by the caller.
-template <int DP>
+template <int DP, bool ZP>
 __device__ __forceinline__ void load_tile_tok(TileRegs<DP>& t, const DecodeParams& p, const int8_t* kbase,
                                               const int8_t* vbase, int base, int avail, int D, int g, int col) {
   constexpr int LPTILE = TileRegs<DP>::LPTILE, RPL = TileRegs<DP>::RPL;
@@ -192,9 +235,9 @@ __device__ __forceinline__ void load_tile_tok(TileRegs<DP>& t, const DecodeParam
     t.v[r] = stream_load((const uint4*)(vbase + off));
     const int idx = b0 + rowt;
     t.ks[r] = p.sc[0][idx] * p.qk_scale;
-    t.kz[r] = (float)p.zp[0][idx];
+    t.kz[r] = ZP ? (float)p.zp[0][idx] : 0.f;
     t.vs[r] = p.sc[1][idx];
-    t.vz[r] = (float)p.zp[1][idx];
+    t.vz[r] = ZP ? (float)p.zp[1][idx] : 0.f;
   }
 }
 
@@ -211,8 +254,8 @@ struct LaneState {
   float acc[16];
 };
 
-template <int DP, typename QT>
-__device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& t, const QSlice<QT>& q, float qsum,
+template <int DP, int VF, typename QS>
+__device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& t, const QS& q, float qsum,
                                              const RowMeta<TileRegs<DP>::LPTILE>& rm, int token0, int len, int g) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
   float s[LPTILE];
@@ -220,9 +263,13 @@ __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& 
   float mnew = st.m;
 #pragma unroll
   for (int r = 0; r < LPTILE; ++r) {
-    const float dot = group_sum<LPT>(q.dot(t.k[r]));
     ok[r] = rm.valid[r] && (token0 + r * RPL + g) < len;
-    s[r] = (dot - (QSlice<QT>::kOffset + rm.kz[r]) * qsum) * rm.ks[r];
+    if constexpr (VF == kVfFp8) {
+      s[r] = group_sum<LPT>(q.dot_fp8(t.k[r])) * rm.ks[r];
+    } else {
+      const float dot = group_sum<LPT>(q.dot(t.k[r]));
+      s[r] = (dot - (QS::kOffset + rm.kz[r]) * qsum) * rm.ks[r];
+    }
     if (ok[r]) mnew = fmaxf(mnew, s[r]);
   }
   // Refresh the running max only when some lane's max grew by more than the slack;
@@ -240,8 +287,12 @@ __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& 
     const float pr = ok[r] ? fast_exp2(s[r] - st.m) : 0.f;
     st.l += pr;
     const float w = pr * rm.vs[r];
-    st.zacc = fmaf(w, rm.vz[r], st.zacc);
-    axpy16_u8(st.acc, w, t.v[r]);
+    if constexpr (VF == kVfFp8) {
+      axpy16_fp8(st.acc, w, t.v[r]);
+    } else {
+      st.zacc = fmaf(w, rm.vz[r], st.zacc);
+      axpy16_u8(st.acc, w, t.v[r]);
+    }
   }
 }
 
@@ -252,7 +303,7 @@ constexpr int max_tiled_waves(int DP) { return DP == 256 ? 8 : kMaxWaves; }
 // Register layout (64, 128 or 256 dims) that serves a head_dim on the tiled path.
 __host__ __device__ constexpr int padded_head_dim(int D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
 
-template <int DP, typename QT, bool PAGED, int QM>
+template <int DP, typename QT, bool PAGED, int QM, int VF>
 __global__ void __launch_bounds__(kWave * max_tiled_waves(DP))
 decode_rows_kernel(const DecodeParams p) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
@@ -311,17 +362,17 @@ decode_rows_kernel(const DecodeParams p) {
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
   if (!TOK && my_base >= 0) {
     my_ks = p.sc[0][my_meta] * p.qk_scale;
-    my_kz = (float)p.zp[0][my_meta];
+    my_kz = VF == kVfInt8 ? (float)p.zp[0][my_meta] : 0.f;
     my_vs = p.sc[1][my_meta];
-    my_vz = (float)p.zp[1][my_meta];
+    my_vz = VF == kVfInt8 ? (float)p.zp[1][my_meta] : 0.f;
   }
   float my_ks1 = 0.f, my_kz1 = 0.f, my_vs1 = 0.f, my_vz1 = 0.f;
   if constexpr (SUB) {
     if (my_base1 >= 0) {
       my_ks1 = p.sc[0][my_meta1] * p.qk_scale;
-      my_kz1 = (float)p.zp[0][my_meta1];
+      my_kz1 = VF == kVfInt8 ? (float)p.zp[0][my_meta1] : 0.f;
       my_vs1 = p.sc[1][my_meta1];
-      my_vz1 = (float)p.zp[1][my_meta1];
+      my_vz1 = VF == kVfInt8 ? (float)p.zp[1][my_meta1] : 0.f;
     }
   }
 
@@ -331,7 +382,8 @@ decode_rows_kernel(const DecodeParams p) {
   const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
   const int lane_off = g * D + (active ? 16 * j : 0);
   const int rstride = RPL * D;
-  QSlice<QT> q;
+  using QS = typename std::conditional<VF == kVfFp8, QSliceF<QT>, QSlice<QT>>::type;
+  QS q;
   if (active)
     q.load((const QT*)p.q + (size_t)row * D + 16 * j);
   else
@@ -358,7 +410,7 @@ decode_rows_kernel(const DecodeParams p) {
     if constexpr (SUB)
       load_tile_sub<DP>(t, kbase, vbase, base_of(k), base1_of(k), D, g, active ? 16 * j : 0);
     else if constexpr (TOK)
-      load_tile_tok<DP>(t, p, kbase, vbase, base_of(k), avail_of(k), D, g, active ? 16 * j : 0);
+      load_tile_tok<DP, VF == kVfInt8>(t, p, kbase, vbase, base_of(k), avail_of(k), D, g, active ? 16 * j : 0);
     else
       load_tile<DP>(t, kbase, vbase, base_of(k), D, lane_off, rstride);
   };
@@ -396,7 +448,7 @@ decode_rows_kernel(const DecodeParams p) {
         rm.valid[r] = hi ? v1 : v0;
       }
     }
-    consume_tile<DP, QT>(st, t, q, qsum, rm, (first + W * k) * kTile, len, g);
+    consume_tile<DP, VF>(st, t, q, qsum, rm, (first + W * k) * kTile, len, g);
   };
   // two register buffers: tile k+1 is in flight while tile k is consumed
   TileRegs<DP> ta, tb2;
@@ -471,7 +523,7 @@ decode_rows_kernel(const DecodeParams p) {
 
 // ---- generic path: any head_dim <= 256, any page / quant block --------------------------------
 
-template <typename QT, bool PAGED>
+template <typename QT, bool PAGED, int VF>
 __global__ void __launch_bounds__(1024)
 decode_generic_kernel(const DecodeParams p) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -515,13 +567,16 @@ decode_generic_kernel(const DecodeParams p) {
       sidx = (int64_t)row * p.n_blocks + blk;
       voff = (sidx * p.quant_block + o) * D;
     }
-    const float ks = p.sc[0][sidx], kz = (float)p.zp[0][sidx];
-    const float vs = p.sc[1][sidx], vz = (float)p.zp[1][sidx];
+    const float ks = p.sc[0][sidx], kz = VF == kVfInt8 ? (float)p.zp[0][sidx] : 0.f;
+    const float vs = p.sc[1][sidx], vz = VF == kVfInt8 ? (float)p.zp[1][sidx] : 0.f;
     float dot = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int d = lane + c * kWave;
-      if (d < D) dot = fmaf(q[c], ((float)((int)p.kv[0][voff + d] + 128) - kz) * ks, dot);
+      if (d < D) {
+        const int8_t b = p.kv[0][voff + d];
+        dot = fmaf(q[c], (VF == kVfFp8 ? fp8_value(b) : (float)((int)b + 128) - kz) * ks, dot);
+      }
     }
     const float s = wave_sum(dot) * p.qk_scale;
     const float mn = fmaxf(m, s);
@@ -530,7 +585,8 @@ decode_generic_kernel(const DecodeParams p) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int d = lane + c * kWave;
-      const float v = d < D ? ((float)((int)p.kv[1][voff + d] + 128) - vz) * vs : 0.f;
+      const int8_t b = d < D ? p.kv[1][voff + d] : (int8_t)0;
+      const float v = d < D ? (VF == kVfFp8 ? fp8_value(b) : (float)((int)b + 128) - vz) * vs : 0.f;
       acc[c] = fmaf(pr, v, acc[c] * alpha);
     }
     m = mn;
@@ -613,13 +669,21 @@ static bool tiled_path(int head_dim, int page_size, int quant_block) {
   return quant_block % 8 == 0 && page_size % quant_block == 0;
 }
 
+template <typename QT, bool PAGED, int QM, int VF>
+static void launch_tiled_vf(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
+  switch (padded_head_dim(p.head_dim)) {
+    case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
+    case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
+    default: hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
+  }
+}
+
 template <typename QT, bool PAGED, int QM>
 static void launch_tiled(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
-  switch (padded_head_dim(p.head_dim)) {
-    case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, QM>), grid, block, 0, st, p); break;
-    case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, QM>), grid, block, 0, st, p); break;
-    default: hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, QM>), grid, block, 0, st, p); break;
-  }
+  if (p.vfmt == kVfFp8)
+    launch_tiled_vf<QT, PAGED, QM, kVfFp8>(p, grid, block, st);
+  else
+    launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);
 }
 
 template <typename QT, bool PAGED>
@@ -636,7 +700,10 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
   } else {
     const int64_t waves = (int64_t)p.rows * p.max_splits;
     const dim3 grid((unsigned)((waves + waves_per_block - 1) / waves_per_block));
-    hipLaunchKernelGGL((decode_generic_kernel<QT, PAGED>), grid, block, 0, st, p);
+    if (p.vfmt == kVfFp8)
+      hipLaunchKernelGGL((decode_generic_kernel<QT, PAGED, kVfFp8>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((decode_generic_kernel<QT, PAGED, kVfInt8>), grid, block, 0, st, p);
   }
   return check_launch(PAGED ? "paged_quant_attention_kernel" : "fused_dequant_attention_kernel");
 }
@@ -683,7 +750,8 @@ static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, 
       return set_error(FS_ERR_INVALID, "split_tiles must be <= 64 * waves_per_block on the tiled path");
   }
   if ((int64_t)p.rows * p.max_splits > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "decode grid too large");
-  if (!p.q || !p.kv[0] || !p.kv[1] || !p.sc[0] || !p.sc[1] || !p.zp[0] || !p.zp[1] || !p.out)
+  if (!p.q || !p.kv[0] || !p.kv[1] || !p.sc[0] || !p.sc[1] || !p.out ||
+      (p.vfmt == kVfInt8 && (!p.zp[0] || !p.zp[1])))
     return set_error(FS_ERR_INVALID, "null tensor pointer");
   if (p.max_splits > 1 || p.force_partials) {
     const int64_t need = fs_decode_workspace_bytes(p.rows, p.max_splits, p.head_dim);
@@ -706,13 +774,13 @@ extern "C" int fs_decode_tiled_path(int head_dim, int page_size, int quant_block
   return tiled_path(head_dim, page_size, quant_block) ? 1 : 0;
 }
 
-extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
-                                  const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
-                                  const int16_t* v_zero, const int64_t* lengths, void* out, void* workspace,
-                                  int64_t workspace_bytes, int batch, int heads, int head_dim, int seq_len,
-                                  int n_blocks, int block_size, float sm_scale, int split_tiles, int max_splits,
-                                  int waves_per_block, void* stream) {
+static int fused_decode(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                        const int16_t* k_zero, const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                        const int64_t* lengths, void* out, void* workspace, int64_t workspace_bytes, int batch,
+                        int heads, int head_dim, int seq_len, int n_blocks, int block_size, float sm_scale,
+                        int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream) {
   DecodeParams p{};
+  p.vfmt = vfmt;
   p.q = q;
   p.kv[0] = k_values; p.kv[1] = v_values;
   p.sc[0] = k_scale; p.sc[1] = v_scale;
@@ -735,6 +803,27 @@ extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_va
   return launch_decode<false>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }
 
+extern "C" int fs_fused_decode_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                  const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                  const int16_t* v_zero, const int64_t* lengths, void* out, void* workspace,
+                                  int64_t workspace_bytes, int batch, int heads, int head_dim, int seq_len,
+                                  int n_blocks, int block_size, float sm_scale, int split_tiles, int max_splits,
+                                  int waves_per_block, void* stream) {
+  return fused_decode(q, q_dtype, k_values, k_scale, k_zero, v_values, v_scale, v_zero, lengths, out, workspace,
+                      workspace_bytes, batch, heads, head_dim, seq_len, n_blocks, block_size, sm_scale, split_tiles,
+                      max_splits, waves_per_block, kVfInt8, stream);
+}
+
+extern "C" int fs_fused_decode_fp8(const void* q, int q_dtype, const uint8_t* k_values, const float* k_scale,
+                                   const uint8_t* v_values, const float* v_scale, const int64_t* lengths, void* out,
+                                   void* workspace, int64_t workspace_bytes, int batch, int heads, int head_dim,
+                                   int seq_len, int n_blocks, int block_size, float sm_scale, int split_tiles,
+                                   int max_splits, int waves_per_block, void* stream) {
+  return fused_decode(q, q_dtype, (const int8_t*)k_values, k_scale, nullptr, (const int8_t*)v_values, v_scale,
+                      nullptr, lengths, out, workspace, workspace_bytes, batch, heads, head_dim, seq_len, n_blocks,
+                      block_size, sm_scale, split_tiles, max_splits, waves_per_block, kVfFp8, stream);
+}
+
 // Parameters and checks shared by the paged decode and the tree verification entry points
 // (`nq` query rows per request and head).
 int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_values, const float* k_scale,
@@ -743,8 +832,9 @@ int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* 
                         void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads,
                         int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
                         float sm_scale, int split_tiles, int max_splits, int waves_per_block,
-                        bool row_kernel) {
+                        bool row_kernel, int vfmt) {
   p = DecodeParams{};
+  p.vfmt = vfmt;
   p.q = q;
   p.kv[0] = k_values; p.kv[1] = v_values;
   p.sc[0] = k_scale; p.sc[1] = v_scale;
@@ -774,6 +864,22 @@ int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* 
   return FS_OK;
 }
 
+static int paged_decode(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                        const int16_t* k_zero, const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                        const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
+                        void* out, void* workspace, int64_t workspace_bytes, int batch, int heads, int head_dim,
+                        int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
+                        int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream) {
+  DecodeParams p;
+  bool tiled = false;
+  if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
+                            table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, 1, heads,
+                            head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
+                            max_splits, waves_per_block, true, vfmt))
+    return rc;
+  return launch_decode<true>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
+}
+
 extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
                                   const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
                                   const int16_t* v_zero, const void* block_table, int table_index_bytes,
@@ -781,14 +887,22 @@ extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_va
                                   int64_t workspace_bytes, int batch, int heads, int head_dim, int64_t num_pages,
                                   int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
                                   int max_splits, int waves_per_block, void* stream) {
-  DecodeParams p;
-  bool tiled = false;
-  if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
-                            table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, 1, heads,
-                            head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
-                            max_splits, waves_per_block))
-    return rc;
-  return launch_decode<true>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
+  return paged_decode(q, q_dtype, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
+                      table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, heads, head_dim,
+                      num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles, max_splits,
+                      waves_per_block, kVfInt8, stream);
+}
+
+extern "C" int fs_paged_decode_fp8(const void* q, int q_dtype, const uint8_t* k_values, const float* k_scale,
+                                   const uint8_t* v_values, const float* v_scale, const void* block_table,
+                                   int table_index_bytes, int64_t table_cols, const int64_t* lengths, void* out,
+                                   void* workspace, int64_t workspace_bytes, int batch, int heads, int head_dim,
+                                   int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
+                                   int split_tiles, int max_splits, int waves_per_block, void* stream) {
+  return paged_decode(q, q_dtype, (const int8_t*)k_values, k_scale, nullptr, (const int8_t*)v_values, v_scale,
+                      nullptr, block_table, table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes,
+                      batch, heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
+                      max_splits, waves_per_block, kVfFp8, stream);
 }
 
 extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype,

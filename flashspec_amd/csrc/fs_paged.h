@@ -18,6 +18,13 @@ enum QuantMode : int {
   kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
 };
 
+// Value format of the K/V store: affine INT8 (values int8 = u - 128, scale, zero point) or FP8
+// E4M3 codes with a scale and no zero point (the zero arrays are all 0 and unused).
+enum ValueFormat : int {
+  kVfInt8 = 0,
+  kVfFp8 = 1,
+};
+
 struct DecodeParams {
   const void* q;
   const int8_t* kv[2];
@@ -42,6 +49,7 @@ struct DecodeParams {
   // writes split partials for every row (force_partials) for the tree-tail merge.
   int nq;
   int force_partials;
+  int vfmt;  // ValueFormat
   // Multi-query tree kernel with one split: it finishes the rows itself (path tokens from
   // draft_k / draft_v, which then have q's dtype, and parents) instead of leaving partials.
   int fuse_tail;
@@ -184,7 +192,7 @@ int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_va
                  const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
                  void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads, int head_dim,
                  int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
-                 int max_splits, int waves_per_block, bool row_kernel = true);
+                 int max_splits, int waves_per_block, bool row_kernel = true, int vfmt = kVfInt8);
 
 // The paged decode row kernel on `p` (fs_decode.hip).
 int launch_paged_rows(const DecodeParams& p, int q_dtype, bool tiled, int waves_per_block, hipStream_t st);

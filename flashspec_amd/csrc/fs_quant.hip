@@ -42,6 +42,33 @@ __device__ __forceinline__ void quantize_group(const Get& get, int rows, int D, 
   }
 }
 
+// FP8 E4M3 (OCP) per group, symmetric, no zero point:
+//     scale = max(absmax / 448, 1e-8)        (IEEE float32 division)
+//     code  = E4M3_RNE(clamp(x / scale, -448, 448))
+// v_cvt_pk_fp8_f32 rounds to nearest even like torch's float8_e4m3fn conversion (checked over
+// every code and every rounding tie on gfx950); the clamp keeps values in the finite range,
+// where the instruction would otherwise give NaN past 464.  The zero point is written as 0.
+template <typename Get>
+__device__ __forceinline__ void quantize_group_fp8(const Get& get, int rows, int D, int8_t* dst, float* scale_out,
+                                                   int16_t* zero_out, int lane) {
+  float am = 0.0f;
+  for (int r = 0; r < rows; ++r) {
+    for (int d = lane; d < D; d += kWave) am = fmaxf(am, fabsf(get(r, d)));
+  }
+  am = wave_max(am);
+  const float scale = fmaxf(am / 448.0f, 1.0e-8f);
+  for (int r = 0; r < rows; ++r) {
+    for (int d = lane; d < D; d += kWave) {
+      const float y = fminf(fmaxf(get(r, d) / scale, -448.0f), 448.0f);
+      dst[(size_t)r * D + d] = (int8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(y, y, 0, false) & 0xff);
+    }
+  }
+  if (lane == 0) {
+    *scale_out = scale;
+    if (zero_out) *zero_out = 0;
+  }
+}
+
 // ---- vectorized group quantizer --------------------------------------------------------------
 // Same arithmetic as quantize_group, for a group of `rows` contiguous source rows of D values
 // with rows*D = CH*512 and D % 8 == 0: lane l holds values [c*512 + 8l, c*512 + 8l + 8) of
@@ -186,7 +213,8 @@ quantize_pages_vec_kernel(const XT* x, int H, int S, int D, int page, int nbps, 
 }
 
 // x [outer, S, D] -> values [outer, nb, bs, D]; group = (o, block); rows past S read as 0.
-template <typename XT>
+// FP8: E4M3 codes (quantize_group_fp8) instead of affine INT8; zero may then be null.
+template <typename XT, bool FP8 = false>
 __global__ void __launch_bounds__(256)
 quantize_blocks_kernel(const XT* x, int64_t outer, int S, int D, int bs, int nb, int8_t* values, float* scale,
                        int16_t* zero) {
@@ -200,12 +228,15 @@ quantize_blocks_kernel(const XT* x, int64_t outer, int S, int D, int bs, int nb,
     const int s = blk * bs + r;
     return s < S ? to_f32(src[(size_t)s * D + d]) : 0.0f;
   };
-  quantize_group(get, bs, D, values + (size_t)grp * bs * D, scale + grp, zero + grp, lane);
+  if constexpr (FP8)
+    quantize_group_fp8(get, bs, D, values + (size_t)grp * bs * D, scale + grp, zero ? zero + grp : nullptr, lane);
+  else
+    quantize_group(get, bs, D, values + (size_t)grp * bs * D, scale + grp, zero + grp, lane);
 }
 
 // dense [B, H, S, D] -> page store [P, H, page, D]; physical page j holds batch-major
 // logical page src[j] (identity when src is null); rows past S read as 0.
-template <typename XT>
+template <typename XT, bool FP8 = false>
 __global__ void __launch_bounds__(256)
 quantize_pages_kernel(const XT* x, int H, int S, int D, int page, int nbps, const int64_t* page_src, int64_t P,
                       int8_t* values, float* scale, int16_t* zero) {
@@ -222,7 +253,10 @@ quantize_pages_kernel(const XT* x, int H, int S, int D, int page, int nbps, cons
     const int s = lb * page + r;
     return s < S ? to_f32(src[(size_t)s * D + d]) : 0.0f;
   };
-  quantize_group(get, page, D, values + (size_t)grp * page * D, scale + grp, zero + grp, lane);
+  if constexpr (FP8)
+    quantize_group_fp8(get, page, D, values + (size_t)grp * page * D, scale + grp, zero ? zero + grp : nullptr, lane);
+  else
+    quantize_group(get, page, D, values + (size_t)grp * page * D, scale + grp, zero + grp, lane);
 }
 
 // Rewrite listed pages (see fs_update_pages_i8).
@@ -445,6 +479,24 @@ dequantize_kernel(const int8_t* values, const float* scale, const int16_t* zero,
     const int64_t sidx = o * nb + blk;
     const int u = (int)values[((size_t)o * nb * bs + s) * D + d] + 128;
     out[e] = from_f32<OT>(((float)u - (float)zero[sidx]) * scale[sidx]);
+  }
+}
+
+// FP8 E4M3 codes -> float32(code) * scale, cropped to S rows.
+template <typename OT>
+__global__ void __launch_bounds__(256)
+dequantize_fp8_kernel(const uint8_t* values, const float* scale, int64_t outer, int nb, int bs, int D, int S,
+                      OT* out) {
+  const int64_t total = outer * (int64_t)S * D;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t od = e / D;
+    const int d = (int)(e - od * D);
+    const int64_t o = od / S;
+    const int s = (int)(od - o * S);
+    const int64_t sidx = o * nb + s / bs;
+    const uint32_t code = values[((size_t)o * nb * bs + s) * D + d];
+    out[e] = from_f32<OT>(__builtin_amdgcn_cvt_pk_f32_fp8(code, false)[0] * scale[sidx]);
   }
 }
 
@@ -686,4 +738,67 @@ extern "C" int fs_quantize_sym_i8(const void* x, int x_dtype, int64_t rows, int 
     case FS_BF16: return launch_quantize_sym((const __hip_bfloat16*)x, rows, head_dim, values, scale, zero, st);
     default: return set_error(FS_ERR_INVALID, "quantize_symmetric: dtype code must be 0, 1 or 2");
   }
+}
+
+extern "C" int fs_quantize_fp8(const void* x, int x_dtype, int64_t outer, int seq_len, int head_dim, int block_size,
+                               uint8_t* values, float* scale, int16_t* zero, void* stream) {
+  if (outer <= 0 || seq_len <= 0 || head_dim <= 0 || block_size <= 0)
+    return set_error(FS_ERR_INVALID, "quantize_fp8: sizes must be positive");
+  if (!x || !values || !scale) return set_error(FS_ERR_INVALID, "quantize_fp8: null pointer");
+  const int nb = (seq_len + block_size - 1) / block_size;
+  const int64_t groups = outer * nb;
+  if ((groups + 3) / 4 > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "quantize_fp8: too many groups");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+  int8_t* v = (int8_t*)values;
+  switch (x_dtype) {
+    case FS_F32: hipLaunchKernelGGL((quantize_blocks_kernel<float, true>), grid, block, 0, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL((quantize_blocks_kernel<__half, true>), grid, block, 0, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL((quantize_blocks_kernel<__hip_bfloat16, true>), grid, block, 0, st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
+    default: return set_error(FS_ERR_INVALID, "quantize_fp8: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("quantize_fp8_per_block");
+}
+
+extern "C" int fs_quantize_pages_fp8(const void* x, int x_dtype, int batch, int heads, int seq_len, int head_dim,
+                                     int page_size, const int64_t* page_src, int64_t num_pages, uint8_t* values,
+                                     float* scale, int16_t* zero, void* stream) {
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0 || page_size <= 0)
+    return set_error(FS_ERR_INVALID, "quantize_pages_fp8: sizes must be positive");
+  if (!x || !values || !scale) return set_error(FS_ERR_INVALID, "quantize_pages_fp8: null pointer");
+  const int nbps = (seq_len + page_size - 1) / page_size;
+  if (num_pages != (int64_t)batch * nbps)
+    return set_error(FS_ERR_INVALID, "quantize_pages_fp8: num_pages must equal batch * ceil(seq_len / page)");
+  const int64_t groups = num_pages * heads;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+  int8_t* v = (int8_t*)values;
+  switch (x_dtype) {
+    case FS_F32: hipLaunchKernelGGL((quantize_pages_kernel<float, true>), grid, block, 0, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL((quantize_pages_kernel<__half, true>), grid, block, 0, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL((quantize_pages_kernel<__hip_bfloat16, true>), grid, block, 0, st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
+    default: return set_error(FS_ERR_INVALID, "quantize_pages_fp8: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("quantize_pages_fp8");
+}
+
+extern "C" int fs_dequantize_fp8(const uint8_t* values, const float* scale, int64_t outer, int n_blocks,
+                                 int block_size, int head_dim, int seq_len, void* out, int out_dtype, void* stream) {
+  if (outer <= 0 || n_blocks <= 0 || block_size <= 0 || head_dim <= 0 || seq_len < 0 ||
+      (int64_t)n_blocks * block_size < seq_len)
+    return set_error(FS_ERR_INVALID, "dequantize_fp8: invalid sizes");
+  if (!values || !scale || !out) return set_error(FS_ERR_INVALID, "dequantize_fp8: null pointer");
+  const int64_t total = outer * (int64_t)seq_len * head_dim;
+  if (total == 0) return FS_OK;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks), block(256);
+  switch (out_dtype) {
+    case FS_F32: hipLaunchKernelGGL(dequantize_fp8_kernel<float>, grid, block, 0, st, values, scale, outer, n_blocks, block_size, head_dim, seq_len, (float*)out); break;
+    case FS_F16: hipLaunchKernelGGL(dequantize_fp8_kernel<__half>, grid, block, 0, st, values, scale, outer, n_blocks, block_size, head_dim, seq_len, (__half*)out); break;
+    case FS_BF16: hipLaunchKernelGGL(dequantize_fp8_kernel<__hip_bfloat16>, grid, block, 0, st, values, scale, outer, n_blocks, block_size, head_dim, seq_len, (__hip_bfloat16*)out); break;
+    default: return set_error(FS_ERR_INVALID, "dequantize_fp8: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("dequantize_fp8_per_block");
 }

@@ -21,8 +21,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from .quant import (QuantizedTensor, dequantize_int8_per_block, estimate_quantized_bytes, quantize_int8_per_block,
-                    quantize_int8_symmetric_per_token)
+from .quant import (FP8_DTYPE, QuantizedTensor, dequantize_int8_per_block, estimate_quantized_bytes, is_fp8,
+                    quantize_fp8_per_block, quantize_int8_per_block, quantize_int8_symmetric_per_token)
 
 _SCALE_FLOOR = 1.0e-8  # quantizing an all-zero block gives int8 -128, scale fp32(1e-8), zero 0
 
@@ -417,11 +417,12 @@ class PagedKVCache:
 
         ``kv_format`` (not in the reference): ``affine_block`` quantizes each page per head
         as the reference does; ``symmetric_token`` stores symmetric absmax INT8 with one scale
-        per token (``quantize_int8_symmetric_per_token``, quant block 1).
+        per token (``quantize_int8_symmetric_per_token``, quant block 1); ``fp8_block`` stores
+        FP8 E4M3 codes with one scale per page and head (``quantize_fp8_per_block``).
         """
 
-        if kv_format not in ("affine_block", "symmetric_token"):
-            raise ValueError("kv_format must be affine_block or symmetric_token")
+        if kv_format not in ("affine_block", "symmetric_token", "fp8_block"):
+            raise ValueError("kv_format must be affine_block, symmetric_token or fp8_block")
 
         if k.ndim != 4 or v.ndim != 4:
             raise ValueError("k and v must be [batch, heads, seq_len, head_dim]")
@@ -455,6 +456,13 @@ class PagedKVCache:
         if kv_format == "symmetric_token":
             k_quant = quantize_int8_symmetric_per_token(cls._physical_pages(k, block_size, perm))
             v_quant = quantize_int8_symmetric_per_token(cls._physical_pages(v, block_size, perm))
+        elif kv_format == "fp8_block":
+            if k.device.type == "cuda":
+                k_quant = cls._quantize_pages(k, block_size, perm, total, fp8=True)
+                v_quant = cls._quantize_pages(v, block_size, perm, total, fp8=True)
+            else:
+                k_quant = quantize_fp8_per_block(cls._physical_pages(k, block_size, perm), block_size=block_size)
+                v_quant = quantize_fp8_per_block(cls._physical_pages(v, block_size, perm), block_size=block_size)
         elif k.device.type == "cuda":
             k_quant = cls._quantize_pages(k, block_size, perm, total)
             v_quant = cls._quantize_pages(v, block_size, perm, total)
@@ -475,13 +483,17 @@ class PagedKVCache:
         return pages if perm is None else pages[perm].contiguous()
 
     @staticmethod
-    def _quantize_pages(x: torch.Tensor, block_size: int, perm: torch.Tensor | None, total: int) -> QuantizedTensor:
+    def _quantize_pages(x: torch.Tensor, block_size: int, perm: torch.Tensor | None, total: int,
+                        fp8: bool = False) -> QuantizedTensor:
         lib = _lib.require()
         batch, heads, seq_len, head_dim = (int(s) for s in x.shape)
         src = _src_for_kernel(x.detach())
         values, scale, zero = _empty_page_store(total, heads, block_size, head_dim, x.device)
+        if fp8:
+            values = values.view(FP8_DTYPE)
         page_src = None if perm is None else perm.to(torch.int64).contiguous()
-        _lib.check(lib.fs_quantize_pages_i8(
+        quantize_pages = lib.fs_quantize_pages_fp8 if fp8 else lib.fs_quantize_pages_i8
+        _lib.check(quantize_pages(
             src.data_ptr(), _lib.dtype_code(src.dtype), batch, heads, seq_len, head_dim, block_size,
             _lib.ptr(page_src), total, values.data_ptr(), scale.data_ptr(), zero.data_ptr(),
             _lib.stream_ptr(x.device)))
@@ -507,6 +519,8 @@ class PagedKVCache:
         the whole store is requantized (block = page), as in the reference.
         """
 
+        if is_fp8(self.k_quant) or is_fp8(self.v_quant):
+            raise ValueError("append requantizes pages in the reference's affine INT8 format; FP8 caches are read-only")
         if k_new.ndim != 4 or v_new.ndim != 4:
             raise ValueError("k_new and v_new must be [batch, heads, tokens, head_dim]")
         if k_new.shape != v_new.shape:

@@ -1,4 +1,5 @@
-"""Affine per-block INT8 quantization (reference src/flashspec/quant.py).
+"""Affine per-block INT8 quantization (reference src/flashspec/quant.py), plus the symmetric
+per-token INT8 and FP8 E4M3 per-block KV formats.
 
 GPU tensors go to the HIP kernels of libflashspec_hip.so (``fs_quantize_i8``,
 ``fs_dequantize_i8``), whose float32 op sequence is bit-identical to the
@@ -148,6 +149,94 @@ def quantize_int8_symmetric_per_token(x: torch.Tensor) -> QuantizedTensor:
     return _quantize_sym_portable(x)
 
 
+# ---- FP8 E4M3 per-block format ----------------------------------------------------------------
+# A KV format beside the reference's (which lists FP8 among the formats to compare,
+# doc/TODO.MD:241-255): OCP FP8 E4M3 codes (torch.float8_e4m3fn) in the same block layout, one
+# fp32 scale per block and no zero point (the zero_point tensor is all 0):
+#     scale = max(absmax / 448, 1e-8);  code = E4M3_RNE(clamp(x / scale, -448, 448))
+# gfx950 converts natively (v_cvt_pk_fp8_f32 / v_cvt_pk_f32_fp8), rounding like torch's cast.
+
+FP8_DTYPE = torch.float8_e4m3fn
+FP8_MAX = 448.0
+
+
+def is_fp8(q: QuantizedTensor) -> bool:
+    """True for the FP8 E4M3 format (values of dtype float8_e4m3fn)."""
+
+    return q.values.dtype == FP8_DTYPE
+
+
+def _quantize_fp8_portable(x: torch.Tensor, block_size: int) -> QuantizedTensor:
+    original_shape = tuple(x.shape)
+    xf = _pad_sequence_dim(x.detach().to(torch.float32), block_size)
+    lead, seq, dim = xf.shape[:-2], xf.shape[-2], xf.shape[-1]
+    blocked = xf.reshape(*lead, seq // block_size, block_size, dim)
+    scale = (blocked.abs().amax(dim=(-2, -1), keepdim=True) / FP8_MAX).clamp_min(1.0e-8)
+    codes = (blocked / scale).clamp(-FP8_MAX, FP8_MAX).to(FP8_DTYPE)
+    return QuantizedTensor(codes, scale, torch.zeros_like(scale, dtype=torch.int16), block_size, original_shape)
+
+
+def _quantize_fp8_hip(x: torch.Tensor, block_size: int) -> QuantizedTensor:
+    lib = _lib.require()
+    original_shape = tuple(x.shape)
+    xd = x.detach()
+    if xd.dtype not in _lib.DTYPE_CODE:
+        xd = xd.to(torch.float32)
+    xd = xd.contiguous()
+    lead = tuple(xd.shape[:-2])
+    seq, dim = int(xd.shape[-2]), int(xd.shape[-1])
+    n_blocks = (seq + block_size - 1) // block_size
+    outer = math.prod(lead) if lead else 1
+    dev = xd.device
+    values = torch.empty((*lead, n_blocks, block_size, dim), dtype=FP8_DTYPE, device=dev)
+    scale = torch.empty((*lead, n_blocks, 1, 1), dtype=torch.float32, device=dev)
+    zero = torch.empty((*lead, n_blocks, 1, 1), dtype=torch.int16, device=dev)
+    if outer > 0:
+        _lib.check(lib.fs_quantize_fp8(
+            xd.data_ptr(), _lib.dtype_code(xd.dtype), outer, seq, dim, block_size,
+            values.data_ptr(), scale.data_ptr(), zero.data_ptr(), _lib.stream_ptr(dev)))
+    return QuantizedTensor(values, scale, zero, block_size, original_shape)
+
+
+def quantize_fp8_per_block(x: torch.Tensor, block_size: int = 16) -> QuantizedTensor:
+    """FP8 E4M3 quantization of ``x`` per ``[block_size, head_dim]`` block, one fp32 scale each.
+
+    Same layout and padding as ``quantize_int8_per_block``; ``values`` are float8_e4m3fn codes
+    and ``zero_point`` is all zero.  Every attention entry point and ``dequantize_int8_per_block``
+    read it.
+    """
+
+    _validate_block_tensor(x, block_size)
+    if x.device.type == "cuda":
+        return _quantize_fp8_hip(x, block_size)
+    return _quantize_fp8_portable(x, block_size)
+
+
+def _dequantize_fp8(q: QuantizedTensor, dtype: torch.dtype | None) -> torch.Tensor:
+    lead = tuple(q.original_shape[:-2])
+    seq, dim = int(q.original_shape[-2]), int(q.original_shape[-1])
+    if q.values.device.type != "cuda":
+        x = q.values.to(torch.float32) * q.scale.to(torch.float32)
+        x = x.reshape(*lead, -1, dim)[..., :seq, :]
+        return x.to(dtype=dtype) if dtype is not None else x
+    lib = _lib.require()
+    values = q.values.contiguous()
+    n_blocks, block = int(values.shape[-3]), int(values.shape[-2])
+    outer = values.numel() // max(1, n_blocks * block * dim)
+    out_dtype = dtype if dtype in _lib.DTYPE_CODE else torch.float32
+    out = torch.empty((*lead, seq, dim), dtype=out_dtype, device=values.device)
+    if out.numel() > 0:
+        scale = q.scale.to(torch.float32).contiguous()
+        if scale.numel() != outer * n_blocks:
+            raise ValueError("scale does not match the quantized values' block count")
+        _lib.check(lib.fs_dequantize_fp8(
+            values.data_ptr(), scale.data_ptr(), outer, n_blocks, block, dim, seq,
+            out.data_ptr(), _lib.dtype_code(out_dtype), _lib.stream_ptr(values.device)))
+    if dtype is not None and dtype != out_dtype:
+        out = out.to(dtype)
+    return out
+
+
 def _dequantize_hip(q: QuantizedTensor, dtype: torch.dtype | None) -> torch.Tensor:
     lib = _lib.require()
     lead = tuple(q.original_shape[:-2])
@@ -171,8 +260,11 @@ def _dequantize_hip(q: QuantizedTensor, dtype: torch.dtype | None) -> torch.Tens
 
 
 def dequantize_int8_per_block(q: QuantizedTensor, dtype: torch.dtype | None = None) -> torch.Tensor:
-    """``((values + 128) - zero_point) * scale``, padding cropped (quant.py:168-204)."""
+    """``((values + 128) - zero_point) * scale``, padding cropped (quant.py:168-204); for the
+    FP8 format (``is_fp8``) ``float(code) * scale``."""
 
+    if is_fp8(q):
+        return _dequantize_fp8(q, dtype)
     if q.values.device.type == "cuda":
         return _dequantize_hip(q, dtype)
     u = q.values.to(torch.int16) + 128
@@ -194,6 +286,14 @@ def build_compression_stats(dense_bytes: float, quant_bytes: float, *, materiali
     }
     stats.update({key: float(value) for key, value in extra.items()})
     return stats
+
+
+def dequantize_fp8_per_block(q: QuantizedTensor, dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``float(code) * scale`` of an FP8 E4M3 ``QuantizedTensor``, padding cropped."""
+
+    if not is_fp8(q):
+        raise ValueError("dequantize_fp8_per_block takes the FP8 E4M3 format (float8_e4m3fn values)")
+    return _dequantize_fp8(q, dtype)
 
 
 def estimate_quantized_bytes(q: QuantizedTensor) -> int:

@@ -72,6 +72,8 @@ def _validate(q, cache, draft_k, draft_v):
         raise ValueError("need at least one draft node")
     if head_dim > 256:
         raise ValueError("head_dim must be <= 256")
+    if cache.k_quant.values.dtype != torch.int8 or cache.v_quant.values.dtype != torch.int8:
+        raise ValueError("tree verification reads INT8 caches (affine_block or symmetric_token)")
     return batch, nodes, heads, head_dim
 
 

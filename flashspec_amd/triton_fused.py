@@ -16,7 +16,7 @@ from typing import Any
 import torch
 
 from . import _lib
-from .quant import QuantizedTensor, build_compression_stats, estimate_quantized_bytes
+from .quant import FP8_DTYPE, QuantizedTensor, build_compression_stats, estimate_quantized_bytes, is_fp8
 from .triton_utils import (
     dispatch_triton_or_fallback,
     launch_plan,
@@ -74,8 +74,9 @@ def _validate_triton_fused_inputs(q: torch.Tensor, k_quant: QuantizedTensor, v_q
         raise ValueError("q dtype must be float16, bfloat16 or float32")
     batch, heads, seq_len, head_dim = k_quant.original_shape
     for name, qt in (("k_quant", k_quant), ("v_quant", v_quant)):
-        if qt.values.dtype != torch.int8 or qt.scale.dtype != torch.float32 or qt.zero_point.dtype != torch.int16:
-            raise ValueError(f"{name} must hold int8 values, float32 scale and int16 zero_point")
+        if qt.values.dtype not in (torch.int8, FP8_DTYPE) or qt.scale.dtype != torch.float32 or \
+                qt.zero_point.dtype != torch.int16:
+            raise ValueError(f"{name} must hold int8 (or float8_e4m3fn) values, float32 scale and int16 zero_point")
         n_blocks = (seq_len + qt.block_size - 1) // qt.block_size
         if tuple(qt.values.shape) != (batch, heads, n_blocks, qt.block_size, head_dim):
             raise ValueError(f"{name}.values must be [batch, heads, n_blocks, block_size, head_dim]")
@@ -83,6 +84,8 @@ def _validate_triton_fused_inputs(q: torch.Tensor, k_quant: QuantizedTensor, v_q
             raise ValueError(f"{name} scale/zero_point must have one entry per block")
     if k_quant.block_size != v_quant.block_size:
         raise ValueError("K/V quant block sizes must match")
+    if k_quant.values.dtype != v_quant.values.dtype:
+        raise ValueError("k_quant and v_quant must use the same format (int8 or float8_e4m3fn values)")
 
 
 def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTensor, v_quant: QuantizedTensor,
@@ -111,10 +114,16 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     if max_splits > 1:
         ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(lib.fs_fused_decode_i8(
-        q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), _lib.ptr(lengths_c),
-        out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads, head_dim, seq_len, n_blocks, block_size,
-        sm_scale, split_tiles, max_splits, waves, stream))
+    if is_fp8(k_quant):
+        _lib.check(lib.fs_fused_decode_fp8(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kv[0].data_ptr(), kv[1].data_ptr(), kv[3].data_ptr(),
+            kv[4].data_ptr(), _lib.ptr(lengths_c), out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads,
+            head_dim, seq_len, n_blocks, block_size, sm_scale, split_tiles, max_splits, waves, stream))
+    else:
+        _lib.check(lib.fs_fused_decode_i8(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), _lib.ptr(lengths_c),
+            out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads, head_dim, seq_len, n_blocks, block_size,
+            sm_scale, split_tiles, max_splits, waves, stream))
     if max_splits > 1:
         _lib.check(lib.fs_combine_splits(
             workspace.data_ptr(), _lib.ptr(lengths_c), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,

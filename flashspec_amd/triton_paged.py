@@ -18,7 +18,7 @@ import torch
 
 from . import _lib
 from .paged import PagedKVCache
-from .quant import build_compression_stats
+from .quant import FP8_DTYPE, build_compression_stats, is_fp8
 from .triton_utils import (
     dispatch_triton_or_fallback,
     launch_plan,
@@ -54,9 +54,13 @@ def _validate_triton_paged_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
         raise ValueError("q dtype must be float16, bfloat16 or float32")
     pages, heads, page, head_dim = cache.k_quant.original_shape
     qb = cache.k_quant.block_size
+    if cache.k_quant.values.dtype != cache.v_quant.values.dtype:
+        raise ValueError("cache K and V must use the same format (int8 or float8_e4m3fn values)")
     for name, qt in (("k_quant", cache.k_quant), ("v_quant", cache.v_quant)):
-        if qt.values.dtype != torch.int8 or qt.scale.dtype != torch.float32 or qt.zero_point.dtype != torch.int16:
-            raise ValueError(f"cache.{name} must hold int8 values, float32 scale and int16 zero_point")
+        if qt.values.dtype not in (torch.int8, FP8_DTYPE) or qt.scale.dtype != torch.float32 or \
+                qt.zero_point.dtype != torch.int16:
+            raise ValueError(f"cache.{name} must hold int8 (or float8_e4m3fn) values, float32 scale and int16 "
+                             "zero_point")
         if tuple(qt.values.shape) != (pages, heads, page // qb, qb, head_dim):
             raise ValueError(f"cache.{name}.values must be [pages, heads, page/quant_block, quant_block, head_dim]")
         if qt.scale.numel() != pages * heads * (page // qb) or qt.zero_point.numel() != pages * heads * (page // qb):
@@ -93,11 +97,18 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
     if max_splits > 1:
         ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(lib.fs_paged_decode_i8(
-        q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), table.data_ptr(),
-        table.element_size(), int(table.shape[1]), lengths.data_ptr(), out.data_ptr(), _lib.ptr(workspace),
-        ws_bytes, batch, heads, head_dim, num_pages, int(cache.block_size), int(kq.block_size), max_seq_len,
-        sm_scale, split_tiles, max_splits, waves, stream))
+    if is_fp8(kq):
+        _lib.check(lib.fs_paged_decode_fp8(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kv[0].data_ptr(), kv[1].data_ptr(), kv[3].data_ptr(),
+            kv[4].data_ptr(), table.data_ptr(), table.element_size(), int(table.shape[1]), lengths.data_ptr(),
+            out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads, head_dim, num_pages, int(cache.block_size),
+            int(kq.block_size), max_seq_len, sm_scale, split_tiles, max_splits, waves, stream))
+    else:
+        _lib.check(lib.fs_paged_decode_i8(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), table.data_ptr(),
+            table.element_size(), int(table.shape[1]), lengths.data_ptr(), out.data_ptr(), _lib.ptr(workspace),
+            ws_bytes, batch, heads, head_dim, num_pages, int(cache.block_size), int(kq.block_size), max_seq_len,
+            sm_scale, split_tiles, max_splits, waves, stream))
     if max_splits > 1:
         _lib.check(lib.fs_combine_splits(
             workspace.data_ptr(), lengths.data_ptr(), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,

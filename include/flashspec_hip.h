@@ -171,11 +171,6 @@ int fs_quantize_i8(const void* x, int x_dtype, int64_t outer, int seq_len, int h
                    int block_size, int8_t* values, float* scale, int16_t* zero, void* stream);
 
 /*
- * Dequantize ((v + 128) - zero) * scale and crop the padding.  Replaces
- * reference src/flashspec/quant.py:168-204.
- *   out [outer, seq_len, head_dim] out_dtype
- */
-/*
  * Symmetric absmax INT8 with one fp32 scale per token row (per head):
  *   scale = max(absmax(row) / 127, 1e-8), q = clamp(rint(x / scale), -127, 127)
  * written in the affine layout of fs_quantize_i8 with block size 1 and zero point 128, so
@@ -187,6 +182,49 @@ int fs_quantize_i8(const void* x, int x_dtype, int64_t outer, int seq_len, int h
 int fs_quantize_sym_i8(const void* x, int x_dtype, int64_t rows, int head_dim,
                        int8_t* values, float* scale, int16_t* zero, void* stream);
 
+/*
+ * FP8 E4M3 (OCP "e4m3fn") KV format: per block of block_size tokens x head_dim (zero-padded
+ * like fs_quantize_i8), one fp32 scale and no zero point:
+ *   scale = max(absmax / 448, 1e-8), code = E4M3 round-to-nearest-even of clamp(x / scale, ±448)
+ * values [outer, nb, block_size, head_dim] codes (torch.float8_e4m3fn bytes), scale
+ * [outer, nb]; `zero` (may be null) is filled with 0 so the INT8 layout is kept.
+ * fs_quantize_pages_fp8 is fs_quantize_pages_i8's page-store form (block = page).
+ * No counterpart in the reference, which lists FP8 among the KV formats to compare
+ * (doc/TODO.MD:241-255) without implementing it.
+ */
+int fs_quantize_fp8(const void* x, int x_dtype, int64_t outer, int seq_len, int head_dim,
+                    int block_size, uint8_t* values, float* scale, int16_t* zero, void* stream);
+int fs_quantize_pages_fp8(const void* x, int x_dtype, int batch, int heads, int seq_len,
+                          int head_dim, int page_size, const int64_t* page_src, int64_t num_pages,
+                          uint8_t* values, float* scale, int16_t* zero, void* stream);
+/* float32(code) * scale, padding cropped; out [outer, seq_len, head_dim] out_dtype. */
+int fs_dequantize_fp8(const uint8_t* values, const float* scale, int64_t outer, int n_blocks,
+                      int block_size, int head_dim, int seq_len, void* out, int out_dtype,
+                      void* stream);
+
+/*
+ * Decode attention over FP8 E4M3 stores: fs_fused_decode_i8 / fs_paged_decode_i8 with FP8
+ * codes and per-block (or per-token, block 1) scales and no zero points; same kernels, plan,
+ * workspace and fs_combine_splits.  No counterpart in the reference (see fs_quantize_fp8).
+ */
+int fs_fused_decode_fp8(const void* q, int q_dtype, const uint8_t* k_values, const float* k_scale,
+                        const uint8_t* v_values, const float* v_scale, const int64_t* lengths,
+                        void* out, void* workspace, int64_t workspace_bytes, int batch, int heads,
+                        int head_dim, int seq_len, int n_blocks, int block_size, float sm_scale,
+                        int split_tiles, int max_splits, int waves_per_block, void* stream);
+int fs_paged_decode_fp8(const void* q, int q_dtype, const uint8_t* k_values, const float* k_scale,
+                        const uint8_t* v_values, const float* v_scale, const void* block_table,
+                        int table_index_bytes, int64_t table_cols, const int64_t* lengths,
+                        void* out, void* workspace, int64_t workspace_bytes, int batch, int heads,
+                        int head_dim, int64_t num_pages, int page_size, int quant_block,
+                        int max_seq_len, float sm_scale, int split_tiles, int max_splits,
+                        int waves_per_block, void* stream);
+
+/*
+ * Dequantize ((v + 128) - zero) * scale and crop the padding.  Replaces
+ * reference src/flashspec/quant.py:168-204.
+ *   out [outer, seq_len, head_dim] out_dtype
+ */
 int fs_dequantize_i8(const int8_t* values, const float* scale, const int16_t* zero,
                      int64_t outer, int n_blocks, int block_size, int head_dim, int seq_len,
                      void* out, int out_dtype, void* stream);

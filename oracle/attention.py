@@ -88,8 +88,8 @@ def reference_attention_f64_loops(q, k, v, lengths=None) -> np.ndarray:
 def fused_dequant_attention(q, k_quant: oq.OracleQuant, v_quant: oq.OracleQuant, lengths=None) -> np.ndarray:
     """Oracle for the contiguous INT8 kernel (attention.py:124-168): dequantize, then attend."""
 
-    k = oq.dequantize_int8_per_block(k_quant)
-    v = oq.dequantize_int8_per_block(v_quant)
+    k = oq.dequantize(k_quant)
+    v = oq.dequantize(v_quant)
     return reference_attention(q, k, v, lengths)
 
 

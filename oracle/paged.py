@@ -65,12 +65,15 @@ def from_dense(
     *,
     lengths: Optional[np.ndarray] = None,
     perm: Optional[np.ndarray] = None,
+    kv_format: str = "affine_block",
 ) -> OracleCache:
     """``PagedKVCache.from_dense`` (paged.py:302-419) with an explicit physical permutation.
 
     ``perm[j]`` is the batch-major page stored at physical slot ``j``
     (``physical = pages[perm]``) and ``block_table = inverse(perm)``
-    (paged.py:384-398).  ``perm=None`` is the contiguous layout.
+    (paged.py:384-398).  ``perm=None`` is the contiguous layout.  ``kv_format="fp8_block"``
+    quantizes the pages with the FP8 E4M3 per-page format of oracle/fp8.py instead of the
+    reference's affine INT8.
     """
 
     B, H, S, D = k.shape
@@ -91,9 +94,15 @@ def from_dense(
         lens = np.asarray(lengths, dtype=np.int64).copy()
         if lens.shape != (B,) or (lens < 0).any() or (lens > S).any():
             raise ValueError("lengths must be [batch] with values in [0, seq_len]")
+    if kv_format == "affine_block":
+        quantize = oq.quantize_int8_per_block
+    elif kv_format == "fp8_block":
+        from .fp8 import quantize_fp8_per_block as quantize
+    else:
+        raise ValueError("kv_format must be 'affine_block' or 'fp8_block'")
     return OracleCache(
-        k_quant=oq.quantize_int8_per_block(pk, block_size),
-        v_quant=oq.quantize_int8_per_block(pv, block_size),
+        k_quant=quantize(pk, block_size),
+        v_quant=quantize(pv, block_size),
         block_table=table,
         lengths=lens,
         block_size=block_size,
@@ -104,8 +113,8 @@ def from_dense(
 def to_dense(cache: OracleCache):
     """Dequantize the whole store, gather by ``table.clamp_min(0)``, crop (paged.py:421-461)."""
 
-    pk = oq.dequantize_int8_per_block(cache.k_quant)
-    pv = oq.dequantize_int8_per_block(cache.v_quant)
+    pk = oq.dequantize(cache.k_quant)
+    pv = oq.dequantize(cache.v_quant)
     table = np.maximum(cache.block_table, 0)
     B, H, D = cache.batch_size, cache.num_heads, cache.head_dim
 

@@ -79,6 +79,17 @@ def dequantize_int8_per_block(q: OracleQuant) -> np.ndarray:
     return x.reshape(*lead, -1, head_dim)[..., :seq_len, :].astype(F32)
 
 
+def dequantize(q: OracleQuant) -> np.ndarray:
+    """Dequantize either KV format: int8 values are the affine INT8 format above, uint8 values
+    the FP8 E4M3 codes of oracle/fp8.py."""
+
+    if q.values.dtype == np.uint8:
+        from .fp8 import dequantize_fp8_per_block
+
+        return dequantize_fp8_per_block(q)
+    return dequantize_int8_per_block(q)
+
+
 def estimate_quantized_bytes(q: OracleQuant) -> int:
     """values + 4 B per scale + 2 B per zero point (quant.py:232-247)."""
 

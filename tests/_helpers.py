@@ -28,15 +28,22 @@ def randn(shape, seed: int, dtype=torch.float16) -> torch.Tensor:
 
 
 def np_of(t: torch.Tensor) -> np.ndarray:
+    """numpy copy; bf16 as float32, FP8 E4M3 codes as uint8 (the oracle's FP8 values)."""
+
     t = t.detach().cpu()
     if t.dtype == torch.bfloat16:
         t = t.to(torch.float32)
+    if t.dtype == torch.float8_e4m3fn:
+        t = t.view(torch.uint8)
     return t.numpy()
 
 
 def to_qt(q: oq.OracleQuant, device) -> fa.QuantizedTensor:
+    values = torch.from_numpy(np.ascontiguousarray(q.values))
+    if values.dtype == torch.uint8:  # the oracle's FP8 codes
+        values = values.view(torch.float8_e4m3fn)
     return fa.QuantizedTensor(
-        torch.from_numpy(np.ascontiguousarray(q.values)).to(device),
+        values.to(device),
         torch.from_numpy(np.ascontiguousarray(q.scale)).to(device),
         torch.from_numpy(np.ascontiguousarray(q.zero_point)).to(device),
         int(q.block_size), tuple(int(s) for s in q.original_shape),

@@ -13,6 +13,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 from oracle import attention as oa
 from oracle import paged as op
@@ -315,3 +316,81 @@ def test_tree_rejects_malformed_parents():
     assert ot.path_mask(np.array([[-1, 0, 0, 2]]))[0].tolist() == [
         [True, False, False, False], [True, True, False, False], [True, False, True, False],
         [True, False, True, True]]
+
+
+# ---- FP8 E4M3 per-block format (oracle/fp8.py): pinned against torch's float8_e4m3fn -------
+
+def _torch_e4m3(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_fp8_table_matches_torch():
+    from oracle import fp8
+
+    ref = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    tab = fp8.e4m3_table()
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isnan(tab), ~fin)
+    assert np.array_equal(tab[fin], ref[fin].astype(np.float64))
+    assert tab[0x7E] == 448.0 and tab[0x01] == 2.0 ** -9 and tab[0x08] == 2.0 ** -6
+
+
+def test_fp8_encoder_matches_torch_on_codes_ties_and_random():
+    from oracle import fp8
+
+    tab = fp8.e4m3_table()
+    pos = np.unique(np.abs(tab[np.isfinite(tab)]))
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)  # every rounding tie (exact in fp32)
+    rng = np.random.default_rng(3)
+    xs = np.concatenate([pos, -pos, mids, -mids, np.nextafter(mids, np.float32(np.inf)),
+                         np.nextafter(mids, np.float32(0)), rng.uniform(-448, 448, 20000),
+                         rng.standard_normal(20000) * 2.0 ** -8, [0.0, -0.0, 448.0, -448.0]]).astype(np.float32)
+    xs = xs[np.abs(xs) <= 448]
+    assert np.array_equal(fp8.encode_e4m3_rne(xs), _torch_e4m3(xs))
+    with pytest.raises(ValueError):
+        fp8.encode_e4m3_rne(np.array([449.0], dtype=np.float32))
+
+
+def test_fp8_block_quantizer_closed_forms():
+    from oracle import fp8
+
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((2, 3, 37, 24)) * np.array([1.0, 1e-3, 50.0])[None, :, None, None]).astype(np.float32)
+    q = fp8.quantize_fp8_per_block(x, 16)
+    assert q.values.dtype == np.uint8 and q.values.shape == (2, 3, 3, 16, 24)
+    assert q.scale.shape == (2, 3, 3, 1, 1) and not q.zero_point.any()
+    # scale = max(absmax / 448, 1e-8) in float32; the block maximum becomes the extreme code
+    blocks = oq.pad_sequence_dim(x, 16).reshape(2, 3, 3, 16, 24)
+    amax = np.abs(blocks).max(axis=(-2, -1), keepdims=True)
+    assert np.array_equal(q.scale, np.maximum(amax / np.float32(448), np.float32(1e-8)).astype(np.float32))
+    flat_v = q.values.reshape(2, 3, 3, -1)
+    flat_x = blocks.reshape(2, 3, 3, -1)
+    arg = np.abs(flat_x).argmax(axis=-1)
+    ext = np.take_along_axis(flat_v, arg[..., None], axis=-1)[..., 0]
+    assert set(np.unique(ext & 0x7F)) == {0x7E}
+    # brute force: every code is the nearest representable value to x / scale (ties even)
+    tab = fp8.e4m3_table()
+    y = np.clip(blocks / q.scale, -448, 448).astype(np.float32)
+    got = tab[q.values].astype(np.float64)
+    fin = tab[np.isfinite(tab)]
+    best = np.abs(y[..., None].astype(np.float64) - fin).min(axis=-1)
+    assert np.array_equal(np.abs(got - y.astype(np.float64)), best)
+    # error bound of a 3-bit mantissa: half an ulp, relative 2^-4 in the normal range
+    back = fp8.dequantize_fp8_per_block(q)
+    normal = np.abs(x / q.scale.repeat(16, axis=-3).reshape(2, 3, 48, 1)[:, :, :37]) >= 2.0 ** -6
+    rel = np.abs(back - x)[normal] / np.abs(x)[normal]
+    assert rel.max() <= 2.0 ** -4 * (1 + 1e-6)
+
+
+def test_fp8_zero_block_and_padding():
+    from oracle import fp8
+
+    x = np.zeros((1, 20, 8), dtype=np.float32)
+    x[0, 3, 2] = -1.5
+    q = fp8.quantize_fp8_per_block(x, 16)
+    assert q.scale[0, 1, 0, 0] == np.float32(1e-8)   # all-zero second block (incl. padding)
+    assert not q.values[0, 1].any()
+    assert q.values[0, 0, 3, 2] == 0xFE               # -448: the block's extreme, negative
+    back = fp8.dequantize_fp8_per_block(q)
+    assert back.shape == x.shape and back[0, 3, 2] == np.float32(-1.5)
+    assert np.array_equal(back[0, 4:], x[0, 4:])
