@@ -218,7 +218,8 @@ def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
 
 # Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths
 # [, format]); quant block 1 = symmetric absmax INT8 with one scale per token
-# (quantize_int8_symmetric_per_token), or one FP8 scale per token with format "fp8".
+# (quantize_int8_symmetric_per_token), or one FP8 scale per token with format "fp8"; format
+# "channel" = per-channel affine INT8 (quantize_int8_per_channel).
 SHAPES = [
     ("metric", 8, 32, 4096, 128, 16, 16, "float16", None),
     ("c3_s2048", 8, 32, 2048, 128, 16, 16, "float16", None),
@@ -242,6 +243,8 @@ SHAPES = [
     ("head_dim_64_fp8", 8, 32, 4096, 64, 16, 16, "float16", None, "fp8"),
     ("q_bfloat16_fp8", 8, 32, 4096, 128, 16, 16, "bfloat16", None, "fp8"),
     ("fp8_per_token", 8, 32, 4096, 128, 16, 1, "float16", None, "fp8"),
+    ("per_channel_block_16", 8, 32, 4096, 128, 16, 16, "float16", None, "channel"),
+    ("per_channel_block_64", 8, 32, 4096, 128, 64, 64, "float16", None, "channel"),
 ]
 
 
@@ -282,7 +285,10 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
             k = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
             v = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
             lt = None if lens is None else torch.tensor(lens, dtype=torch.int64, device=dev)
-            if fmt == "fp8":
+            if fmt == "channel":
+                cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt, kv_format="affine_channel")
+                kq, vq = fa.quantize_int8_per_channel(k, qb), fa.quantize_int8_per_channel(v, qb)
+            elif fmt == "fp8":
                 if qb == 1:
                     pk = fa.PagedKVCache._physical_pages(k, page, None)
                     pv = fa.PagedKVCache._physical_pages(v, page, None)
@@ -310,7 +316,7 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
             sets.append((q, cache, kq, vq, lt))
         lengths = lens or [s] * b
         nbytes = algorithmic_bytes(lengths, h, d, page, q_bytes=torch.finfo(qdtype).bits // 8, quant_block=qb,
-                                   param_bytes=4 if fmt == "fp8" else 6)
+                                   param_bytes={"fp8": 4, "channel": 6 * d}.get(fmt, 6))
         ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(sets[i % ROTATE][0], sets[i % ROTATE][1]),
                        steps, warmup)
         _, st = fa.paged_quant_attention_triton(sets[0][0], sets[0][1], return_stats=True)

@@ -8,7 +8,7 @@ to make ``import flashspec`` resolve here).
 from .attention import fused_dequant_attention, paged_quant_attention, reference_attention
 from .paged import PagedKVAllocator, PagedKVCache
 from .quant import (QuantizedTensor, dequantize_fp8_per_block, dequantize_int8_per_block, quantize_fp8_per_block,
-                    quantize_int8_per_block, quantize_int8_symmetric_per_token)
+                    quantize_int8_per_block, quantize_int8_per_channel, quantize_int8_symmetric_per_token)
 from .tree import tree_verify_attention
 from .triton_fused import fused_dequant_attention_triton
 from .triton_paged import paged_quant_attention_triton
@@ -25,6 +25,7 @@ __all__ = [
     "paged_quant_attention_triton",
     "quantize_fp8_per_block",
     "quantize_int8_per_block",
+    "quantize_int8_per_channel",
     "quantize_int8_symmetric_per_token",
     "reference_attention",
     "tree_verify_attention",

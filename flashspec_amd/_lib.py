@@ -44,6 +44,26 @@ _SIGNATURES = {
          c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_void_p],
     ),
     "fs_tree_mfma_path": (c_int, [c_int, c_int, c_int]),
+    "fs_quantize_i8_channel": (
+        c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]
+    ),
+    "fs_quantize_pages_i8_channel": (
+        c_int,
+        [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p],
+    ),
+    "fs_fused_decode_i8_channel": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+    ),
+    "fs_paged_decode_i8_channel": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
+         c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float,
+         c_int, c_int, c_int, c_void_p],
+    ),
+    "fs_decode_tiled_path_channel": (c_int, [c_int, c_int, c_int]),
     "fs_quantize_fp8": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fs_quantize_pages_fp8": (
         c_int,

@@ -296,18 +296,108 @@ __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& 
   }
 }
 
+// Per-channel quantization (kQmChannel): a lane's query dims folded with the K scales of its 16
+// channels of the current quant block, qk[e] = q[e] * ks[e] * qk_scale, and c = sum qk[e] *
+// kz[e], so that a token's score is sum qk[e] * u[e] - c (over the lanes of the row); the
+// V scales and zero points of the same channels.
+struct ChannelParams {
+  float qk[16];
+  float c;
+  float vs[16], vz[16];
+};
+
+// `meta` = quant block index (-1: unbacked tile or idle lane: all-zero parameters);
+// scale / zero entries of channel d of block m sit at m * D + d.
+__device__ __forceinline__ void load_channel_params(ChannelParams& cp, const DecodeParams& p, int meta, int D,
+                                                    int d0, const float* q) {
+  float ks[16], kz[16];
+  if (meta >= 0) {
+    const size_t at = (size_t)meta * D + d0;
+    const float4* ks4 = (const float4*)(p.sc[0] + at);
+    const float4* vs4 = (const float4*)(p.sc[1] + at);
+    const uint4* kz8 = (const uint4*)(p.zp[0] + at);
+    const uint4* vz8 = (const uint4*)(p.zp[1] + at);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 a = ks4[i], v = vs4[i];
+      ks[4 * i] = a.x; ks[4 * i + 1] = a.y; ks[4 * i + 2] = a.z; ks[4 * i + 3] = a.w;
+      cp.vs[4 * i] = v.x; cp.vs[4 * i + 1] = v.y; cp.vs[4 * i + 2] = v.z; cp.vs[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 a = kz8[i], v = vz8[i];
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        kz[8 * i + 2 * k] = (float)(int16_t)(aw[k] & 0xffffu);
+        kz[8 * i + 2 * k + 1] = (float)(int16_t)(aw[k] >> 16);
+        cp.vz[8 * i + 2 * k] = (float)(int16_t)(vw[k] & 0xffffu);
+        cp.vz[8 * i + 2 * k + 1] = (float)(int16_t)(vw[k] >> 16);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ks[e] = kz[e] = cp.vs[e] = cp.vz[e] = 0.f;
+  }
+  float c = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    cp.qk[e] = q[e] * ks[e] * p.qk_scale;
+    c = fmaf(cp.qk[e], kz[e], c);
+  }
+  cp.c = c;
+}
+
+template <int DP>
+__device__ __forceinline__ void consume_tile_channel(LaneState& st, const TileRegs<DP>& t, const ChannelParams& cp,
+                                                     bool valid, int token0, int len, int g) {
+  constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
+  float s[LPTILE];
+  bool ok[LPTILE];
+  float mnew = st.m;
+#pragma unroll
+  for (int r = 0; r < LPTILE; ++r) {
+    ok[r] = valid && (token0 + r * RPL + g) < len;
+    s[r] = group_sum<LPT>(dot16_u8(cp.qk, t.k[r]) - cp.c);
+    if (ok[r]) mnew = fmaxf(mnew, s[r]);
+  }
+  if (__any(mnew > st.m + kRescaleSlack)) {
+    const float alpha = fast_exp2(st.m - mnew);
+    st.m = mnew;
+    st.l *= alpha;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) st.acc[e] *= alpha;
+  }
+  // the tile's sum p * u and sum p, then acc += vs * (T - vz * P) per channel
+  float T[16], P = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) T[e] = 0.f;
+#pragma unroll
+  for (int r = 0; r < LPTILE; ++r) {
+    const float pr = ok[r] ? fast_exp2(s[r] - st.m) : 0.f;
+    st.l += pr;
+    P += pr;
+    axpy16_u8(T, pr, t.v[r]);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) st.acc[e] = fmaf(cp.vs[e], fmaf(-cp.vz[e], P, T[e]), st.acc[e]);
+}
+
 // Waves per workgroup the tiled kernel may run with: 16, or 8 for head_dim 256 so
 // that its 128-float registers per lane fit without spilling.
-constexpr int max_tiled_waves(int DP) { return DP == 256 ? 8 : kMaxWaves; }
+// Per-channel parameters add ~50 registers per lane: 8 waves there too.
+constexpr int max_tiled_waves(int DP, int QM = kQmBlock) {
+  return (DP == 256 || QM == kQmChannel) ? 8 : kMaxWaves;
+}
 
 // Register layout (64, 128 or 256 dims) that serves a head_dim on the tiled path.
 __host__ __device__ constexpr int padded_head_dim(int D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
 
 template <int DP, typename QT, bool PAGED, int QM, int VF>
-__global__ void __launch_bounds__(kWave * max_tiled_waves(DP))
+__global__ void __launch_bounds__(kWave * max_tiled_waves(DP, QM))
 decode_rows_kernel(const DecodeParams p) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
-  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken;
+  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken, CH = QM == kQmChannel;
   __shared__ float s_acc[kMaxWaves * DP];
   __shared__ float s_ml[2 * kMaxWaves];
 
@@ -360,7 +450,7 @@ decode_rows_kernel(const DecodeParams p) {
   const int nk = first < tile_end ? (tile_end - first + W - 1) / W : 0;  // <= kMaxTilesPerWave
   if (lane >= nk) my_base = my_base1 = -1;
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
-  if (!TOK && my_base >= 0) {
+  if (!TOK && !CH && my_base >= 0) {
     my_ks = p.sc[0][my_meta] * p.qk_scale;
     my_kz = VF == kVfInt8 ? (float)p.zp[0][my_meta] : 0.f;
     my_vs = p.sc[1][my_meta];
@@ -382,7 +472,7 @@ decode_rows_kernel(const DecodeParams p) {
   const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
   const int lane_off = g * D + (active ? 16 * j : 0);
   const int rstride = RPL * D;
-  using QS = typename std::conditional<VF == kVfFp8, QSliceF<QT>, QSlice<QT>>::type;
+  using QS = typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>, QSlice<QT>>::type;
   QS q;
   if (active)
     q.load((const QT*)p.q + (size_t)row * D + 16 * j);
@@ -417,6 +507,15 @@ decode_rows_kernel(const DecodeParams p) {
   auto consume = [&](const TileRegs<DP>& t, int k) {
     RowMeta<LPTILE> rm;
     const bool v0 = readlane_i32(my_base, k) >= 0;
+    if constexpr (CH) {
+      // this lane's 16 channels of the tile's quant block: K scales folded into the query,
+      // V scales / zero points applied once per tile
+      const int meta = readlane_i32(my_meta, k);
+      ChannelParams cp;
+      load_channel_params(cp, p, v0 && active ? meta : -1, D, 16 * j, q.q);
+      consume_tile_channel<DP>(st, t, cp, v0, (first + W * k) * kTile, len, g);
+      return;
+    }
     if constexpr (TOK) {
 #pragma unroll
       for (int r = 0; r < LPTILE; ++r) {
@@ -523,7 +622,7 @@ decode_rows_kernel(const DecodeParams p) {
 
 // ---- generic path: any head_dim <= 256, any page / quant block --------------------------------
 
-template <typename QT, bool PAGED, int VF>
+template <typename QT, bool PAGED, int VF, bool CH = false>
 __global__ void __launch_bounds__(1024)
 decode_generic_kernel(const DecodeParams p) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -567,15 +666,21 @@ decode_generic_kernel(const DecodeParams p) {
       sidx = (int64_t)row * p.n_blocks + blk;
       voff = (sidx * p.quant_block + o) * D;
     }
-    const float ks = p.sc[0][sidx], kz = VF == kVfInt8 ? (float)p.zp[0][sidx] : 0.f;
-    const float vs = p.sc[1][sidx], vz = VF == kVfInt8 ? (float)p.zp[1][sidx] : 0.f;
+    // per-channel stores (CH): entries of channel d of block sidx at sidx * D + d
+    const float ks = CH ? 0.f : p.sc[0][sidx], kz = (VF == kVfInt8 && !CH) ? (float)p.zp[0][sidx] : 0.f;
+    const float vs = CH ? 0.f : p.sc[1][sidx], vz = (VF == kVfInt8 && !CH) ? (float)p.zp[1][sidx] : 0.f;
     float dot = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int d = lane + c * kWave;
       if (d < D) {
         const int8_t b = p.kv[0][voff + d];
-        dot = fmaf(q[c], (VF == kVfFp8 ? fp8_value(b) : (float)((int)b + 128) - kz) * ks, dot);
+        if constexpr (CH) {
+          const size_t at = (size_t)sidx * D + d;
+          dot = fmaf(q[c], ((float)((int)b + 128) - (float)p.zp[0][at]) * p.sc[0][at], dot);
+        } else {
+          dot = fmaf(q[c], (VF == kVfFp8 ? fp8_value(b) : (float)((int)b + 128) - kz) * ks, dot);
+        }
       }
     }
     const float s = wave_sum(dot) * p.qk_scale;
@@ -586,7 +691,13 @@ decode_generic_kernel(const DecodeParams p) {
     for (int c = 0; c < 4; ++c) {
       const int d = lane + c * kWave;
       const int8_t b = d < D ? p.kv[1][voff + d] : (int8_t)0;
-      const float v = d < D ? (VF == kVfFp8 ? fp8_value(b) : (float)((int)b + 128) - vz) * vs : 0.f;
+      float v = 0.f;
+      if constexpr (CH) {
+        const size_t at = (size_t)sidx * D + (d < D ? d : 0);
+        v = d < D ? ((float)((int)b + 128) - (float)p.zp[1][at]) * p.sc[1][at] : 0.f;
+      } else {
+        v = d < D ? (VF == kVfFp8 ? fp8_value(b) : (float)((int)b + 128) - vz) * vs : 0.f;
+      }
       acc[c] = fmaf(pr, v, acc[c] * alpha);
     }
     m = mn;
@@ -663,8 +774,10 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
 // Tiled path: head_dim a multiple of 16 up to 256 (served by the 64-, 128- or 256-dim
 // register layout), quant blocks a multiple of 8 tokens with whole quant blocks per page, or
 // one parameter set per token (quant block 1) on contiguous rows or pages of 16k tokens.
-static bool tiled_path(int head_dim, int page_size, int quant_block) {
+// Per-channel stores take the tiled path with quant blocks of a multiple of 16 tokens.
+static bool tiled_path(int head_dim, int page_size, int quant_block, bool per_channel = false) {
   if (head_dim < 16 || head_dim > 256 || head_dim % 16 != 0 || page_size <= 0) return false;
+  if (per_channel) return quant_block > 0 && quant_block % kTile == 0 && page_size % quant_block == 0;
   if (quant_block == 1) return page_size == 1 || page_size % kTile == 0;  // contiguous rows, or 16-token pages
   return quant_block % 8 == 0 && page_size % quant_block == 0;
 }
@@ -680,10 +793,14 @@ static void launch_tiled_vf(const DecodeParams& p, dim3 grid, dim3 block, hipStr
 
 template <typename QT, bool PAGED, int QM>
 static void launch_tiled(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
-  if (p.vfmt == kVfFp8)
-    launch_tiled_vf<QT, PAGED, QM, kVfFp8>(p, grid, block, st);
-  else
-    launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);
+  if constexpr (QM == kQmChannel) {
+    launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);  // per-channel stores are INT8
+  } else {
+    if (p.vfmt == kVfFp8)
+      launch_tiled_vf<QT, PAGED, QM, kVfFp8>(p, grid, block, st);
+    else
+      launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);
+  }
 }
 
 template <typename QT, bool PAGED>
@@ -691,7 +808,9 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
   const dim3 block(kWave * waves_per_block);
   if (tiled) {
     const dim3 grid((unsigned)((int64_t)p.rows * p.max_splits));
-    if (p.quant_block == 1)
+    if (p.per_channel)
+      launch_tiled<QT, PAGED, kQmChannel>(p, grid, block, st);
+    else if (p.quant_block == 1)
       launch_tiled<QT, PAGED, kQmToken>(p, grid, block, st);
     else if (p.quant_block % kTile != 0)
       launch_tiled<QT, PAGED, kQmSub>(p, grid, block, st);
@@ -700,7 +819,9 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
   } else {
     const int64_t waves = (int64_t)p.rows * p.max_splits;
     const dim3 grid((unsigned)((waves + waves_per_block - 1) / waves_per_block));
-    if (p.vfmt == kVfFp8)
+    if (p.per_channel)
+      hipLaunchKernelGGL((decode_generic_kernel<QT, PAGED, kVfInt8, true>), grid, block, 0, st, p);
+    else if (p.vfmt == kVfFp8)
       hipLaunchKernelGGL((decode_generic_kernel<QT, PAGED, kVfFp8>), grid, block, 0, st, p);
     else
       hipLaunchKernelGGL((decode_generic_kernel<QT, PAGED, kVfInt8>), grid, block, 0, st, p);
@@ -744,8 +865,9 @@ static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, 
     if (waves_per_block != 1 && waves_per_block != 2 && waves_per_block != 4 && waves_per_block != 8 &&
         waves_per_block != 16)
       return set_error(FS_ERR_INVALID, "waves_per_block must be 1, 2, 4, 8 or 16");
-    if (tiled && waves_per_block > max_tiled_waves(padded_head_dim(p.head_dim)))
-      return set_error(FS_ERR_INVALID, "waves_per_block must be <= 8 for head_dim > 128 on the tiled path");
+    if (tiled && waves_per_block > max_tiled_waves(padded_head_dim(p.head_dim), p.per_channel ? kQmChannel : kQmBlock))
+      return set_error(FS_ERR_INVALID,
+                       "waves_per_block must be <= 8 for head_dim > 128 or per-channel stores on the tiled path");
     if (tiled && p.split_tiles > kMaxTilesPerWave * waves_per_block)
       return set_error(FS_ERR_INVALID, "split_tiles must be <= 64 * waves_per_block on the tiled path");
   }
@@ -774,13 +896,19 @@ extern "C" int fs_decode_tiled_path(int head_dim, int page_size, int quant_block
   return tiled_path(head_dim, page_size, quant_block) ? 1 : 0;
 }
 
+extern "C" int fs_decode_tiled_path_channel(int head_dim, int page_size, int quant_block) {
+  return tiled_path(head_dim, page_size, quant_block, true) ? 1 : 0;
+}
+
 static int fused_decode(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
                         const int16_t* k_zero, const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
                         const int64_t* lengths, void* out, void* workspace, int64_t workspace_bytes, int batch,
                         int heads, int head_dim, int seq_len, int n_blocks, int block_size, float sm_scale,
-                        int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream) {
+                        int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream,
+                        int per_channel = 0) {
   DecodeParams p{};
   p.vfmt = vfmt;
+  p.per_channel = per_channel;
   p.q = q;
   p.kv[0] = k_values; p.kv[1] = v_values;
   p.sc[0] = k_scale; p.sc[1] = v_scale;
@@ -794,7 +922,7 @@ static int fused_decode(const void* q, int q_dtype, const int8_t* k_values, cons
   p.qk_scale = sm_scale * kLog2e;
   if (batch <= 0) return set_error(FS_ERR_INVALID, "batch must be positive");
   bind_workspace(p, workspace);
-  const bool tiled = tiled_path(head_dim, block_size, block_size);
+  const bool tiled = tiled_path(head_dim, block_size, block_size, per_channel != 0);
   if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes)) return rc;
   if (block_size <= 0 || n_blocks <= 0 || (int64_t)n_blocks * block_size < seq_len)
     return set_error(FS_ERR_INVALID, "n_blocks * block_size must cover seq_len");
@@ -832,9 +960,10 @@ int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* 
                         void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads,
                         int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
                         float sm_scale, int split_tiles, int max_splits, int waves_per_block,
-                        bool row_kernel, int vfmt) {
+                        bool row_kernel, int vfmt, int per_channel) {
   p = DecodeParams{};
   p.vfmt = vfmt;
+  p.per_channel = per_channel;
   p.q = q;
   p.kv[0] = k_values; p.kv[1] = v_values;
   p.sc[0] = k_scale; p.sc[1] = v_scale;
@@ -851,7 +980,7 @@ int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* 
   if (batch <= 0 || nq <= 0) return set_error(FS_ERR_INVALID, "batch and nodes must be positive");
   if ((int64_t)batch * nq * heads > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "too many query rows");
   bind_workspace(p, workspace);
-  tiled = tiled_path(head_dim, page_size, quant_block);
+  tiled = tiled_path(head_dim, page_size, quant_block, per_channel != 0);
   if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes, row_kernel)) return rc;
   if (!block_table || !lengths) return set_error(FS_ERR_INVALID, "block_table and lengths are required");
   if (table_index_bytes != 4 && table_index_bytes != 8) return set_error(FS_ERR_INVALID, "table_index_bytes must be 4 or 8");
@@ -869,13 +998,14 @@ static int paged_decode(const void* q, int q_dtype, const int8_t* k_values, cons
                         const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
                         void* out, void* workspace, int64_t workspace_bytes, int batch, int heads, int head_dim,
                         int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
-                        int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream) {
+                        int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream,
+                        int per_channel = 0) {
   DecodeParams p;
   bool tiled = false;
   if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
                             table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, 1, heads,
                             head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
-                            max_splits, waves_per_block, true, vfmt))
+                            max_splits, waves_per_block, true, vfmt, per_channel))
     return rc;
   return launch_decode<true>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }
@@ -891,6 +1021,31 @@ extern "C" int fs_paged_decode_i8(const void* q, int q_dtype, const int8_t* k_va
                       table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, heads, head_dim,
                       num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles, max_splits,
                       waves_per_block, kVfInt8, stream);
+}
+
+extern "C" int fs_fused_decode_i8_channel(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                          const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                          const int16_t* v_zero, const int64_t* lengths, void* out, void* workspace,
+                                          int64_t workspace_bytes, int batch, int heads, int head_dim, int seq_len,
+                                          int n_blocks, int block_size, float sm_scale, int split_tiles,
+                                          int max_splits, int waves_per_block, void* stream) {
+  return fused_decode(q, q_dtype, k_values, k_scale, k_zero, v_values, v_scale, v_zero, lengths, out, workspace,
+                      workspace_bytes, batch, heads, head_dim, seq_len, n_blocks, block_size, sm_scale, split_tiles,
+                      max_splits, waves_per_block, kVfInt8, stream, 1);
+}
+
+extern "C" int fs_paged_decode_i8_channel(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                          const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                          const int16_t* v_zero, const void* block_table, int table_index_bytes,
+                                          int64_t table_cols, const int64_t* lengths, void* out, void* workspace,
+                                          int64_t workspace_bytes, int batch, int heads, int head_dim,
+                                          int64_t num_pages, int page_size, int quant_block, int max_seq_len,
+                                          float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                                          void* stream) {
+  return paged_decode(q, q_dtype, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
+                      table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, heads, head_dim,
+                      num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles, max_splits,
+                      waves_per_block, kVfInt8, stream, 1);
 }
 
 extern "C" int fs_paged_decode_fp8(const void* q, int q_dtype, const uint8_t* k_values, const float* k_scale,

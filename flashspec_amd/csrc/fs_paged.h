@@ -16,6 +16,7 @@ enum QuantMode : int {
   kQmBlock = 0,  // quant block a multiple of 16 tokens: one entry per tile
   kQmSub = 1,    // quant block an odd multiple of 8 tokens (or 8-token pages): one per 8-token half
   kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
+  kQmChannel = 3,  // per quant block (a multiple of 16 tokens) one entry per channel
 };
 
 // Value format of the K/V store: affine INT8 (values int8 = u - 128, scale, zero point) or FP8
@@ -50,6 +51,7 @@ struct DecodeParams {
   int nq;
   int force_partials;
   int vfmt;  // ValueFormat
+  int per_channel;  // scale / zero hold head_dim entries per quant block (INT8 only)
   // Multi-query tree kernel with one split: it finishes the rows itself (path tokens from
   // draft_k / draft_v, which then have q's dtype, and parents) instead of leaving partials.
   int fuse_tail;
@@ -192,7 +194,8 @@ int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_va
                  const void* block_table, int table_index_bytes, int64_t table_cols, const int64_t* lengths,
                  void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads, int head_dim,
                  int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
-                 int max_splits, int waves_per_block, bool row_kernel = true, int vfmt = kVfInt8);
+                 int max_splits, int waves_per_block, bool row_kernel = true, int vfmt = kVfInt8,
+                 int per_channel = 0);
 
 // The paged decode row kernel on `p` (fs_decode.hip).
 int launch_paged_rows(const DecodeParams& p, int q_dtype, bool tiled, int waves_per_block, hipStream_t st);

@@ -69,6 +69,47 @@ __device__ __forceinline__ void quantize_group_fp8(const Get& get, int rows, int
   }
 }
 
+// Affine INT8 per channel over a group of `rows` tokens: quantize_group's float32 op sequence
+// applied to each channel column (one scale / zero point per channel, D of each per group).
+template <typename Get>
+__device__ __forceinline__ void quantize_channel_group(const Get& get, int rows, int D, int8_t* dst,
+                                                       float* scale_out, int16_t* zero_out, int lane) {
+  for (int d = lane; d < D; d += kWave) {
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    for (int r = 0; r < rows; ++r) {
+      const float x = get(r, d);
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
+    }
+    const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
+    const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
+    for (int r = 0; r < rows; ++r) {
+      const float qv = fminf(fmaxf(__builtin_rintf(get(r, d) / scale + zero), 0.0f), 255.0f);
+      dst[(size_t)r * D + d] = (int8_t)((int)qv - 128);
+    }
+    scale_out[d] = scale;
+    zero_out[d] = (int16_t)zero;
+  }
+}
+
+// Group formats of the element-wise block / page quantizers.
+enum GroupFormat : int {
+  kGfAffine = 0,   // affine INT8, one scale / zero per group
+  kGfFp8 = 1,      // FP8 E4M3, one scale per group, zero 0
+  kGfChannel = 2,  // affine INT8, one scale / zero per channel of the group
+};
+
+template <int GF, typename Get>
+__device__ __forceinline__ void quantize_any_group(const Get& get, int rows, int D, int8_t* dst, float* scale,
+                                                   int16_t* zero, int64_t grp, int lane) {
+  if constexpr (GF == kGfFp8)
+    quantize_group_fp8(get, rows, D, dst, scale + grp, zero ? zero + grp : nullptr, lane);
+  else if constexpr (GF == kGfChannel)
+    quantize_channel_group(get, rows, D, dst, scale + grp * D, zero + grp * D, lane);
+  else
+    quantize_group(get, rows, D, dst, scale + grp, zero + grp, lane);
+}
+
 // ---- vectorized group quantizer --------------------------------------------------------------
 // Same arithmetic as quantize_group, for a group of `rows` contiguous source rows of D values
 // with rows*D = CH*512 and D % 8 == 0: lane l holds values [c*512 + 8l, c*512 + 8l + 8) of
@@ -213,8 +254,9 @@ quantize_pages_vec_kernel(const XT* x, int H, int S, int D, int page, int nbps, 
 }
 
 // x [outer, S, D] -> values [outer, nb, bs, D]; group = (o, block); rows past S read as 0.
-// FP8: E4M3 codes (quantize_group_fp8) instead of affine INT8; zero may then be null.
-template <typename XT, bool FP8 = false>
+// GF: group format (GroupFormat); with kGfFp8 zero may be null, with kGfChannel scale and zero
+// hold D entries per group.
+template <typename XT, int GF = kGfAffine>
 __global__ void __launch_bounds__(256)
 quantize_blocks_kernel(const XT* x, int64_t outer, int S, int D, int bs, int nb, int8_t* values, float* scale,
                        int16_t* zero) {
@@ -228,15 +270,12 @@ quantize_blocks_kernel(const XT* x, int64_t outer, int S, int D, int bs, int nb,
     const int s = blk * bs + r;
     return s < S ? to_f32(src[(size_t)s * D + d]) : 0.0f;
   };
-  if constexpr (FP8)
-    quantize_group_fp8(get, bs, D, values + (size_t)grp * bs * D, scale + grp, zero ? zero + grp : nullptr, lane);
-  else
-    quantize_group(get, bs, D, values + (size_t)grp * bs * D, scale + grp, zero + grp, lane);
+  quantize_any_group<GF>(get, bs, D, values + (size_t)grp * bs * D, scale, zero, grp, lane);
 }
 
 // dense [B, H, S, D] -> page store [P, H, page, D]; physical page j holds batch-major
 // logical page src[j] (identity when src is null); rows past S read as 0.
-template <typename XT, bool FP8 = false>
+template <typename XT, int GF = kGfAffine>
 __global__ void __launch_bounds__(256)
 quantize_pages_kernel(const XT* x, int H, int S, int D, int page, int nbps, const int64_t* page_src, int64_t P,
                       int8_t* values, float* scale, int16_t* zero) {
@@ -253,10 +292,7 @@ quantize_pages_kernel(const XT* x, int H, int S, int D, int page, int nbps, cons
     const int s = lb * page + r;
     return s < S ? to_f32(src[(size_t)s * D + d]) : 0.0f;
   };
-  if constexpr (FP8)
-    quantize_group_fp8(get, page, D, values + (size_t)grp * page * D, scale + grp, zero ? zero + grp : nullptr, lane);
-  else
-    quantize_group(get, page, D, values + (size_t)grp * page * D, scale + grp, zero + grp, lane);
+  quantize_any_group<GF>(get, page, D, values + (size_t)grp * page * D, scale, zero, grp, lane);
 }
 
 // Rewrite listed pages (see fs_update_pages_i8).
@@ -752,9 +788,9 @@ extern "C" int fs_quantize_fp8(const void* x, int x_dtype, int64_t outer, int se
   const dim3 grid = wave_grid(groups), block(256);
   int8_t* v = (int8_t*)values;
   switch (x_dtype) {
-    case FS_F32: hipLaunchKernelGGL((quantize_blocks_kernel<float, true>), grid, block, 0, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
-    case FS_F16: hipLaunchKernelGGL((quantize_blocks_kernel<__half, true>), grid, block, 0, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
-    case FS_BF16: hipLaunchKernelGGL((quantize_blocks_kernel<__hip_bfloat16, true>), grid, block, 0, st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
+    case FS_F32: hipLaunchKernelGGL((quantize_blocks_kernel<float, kGfFp8>), grid, block, 0, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL((quantize_blocks_kernel<__half, kGfFp8>), grid, block, 0, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL((quantize_blocks_kernel<__hip_bfloat16, kGfFp8>), grid, block, 0, st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, v, scale, zero); break;
     default: return set_error(FS_ERR_INVALID, "quantize_fp8: dtype code must be 0, 1 or 2");
   }
   return check_launch("quantize_fp8_per_block");
@@ -774,9 +810,9 @@ extern "C" int fs_quantize_pages_fp8(const void* x, int x_dtype, int batch, int 
   const dim3 grid = wave_grid(groups), block(256);
   int8_t* v = (int8_t*)values;
   switch (x_dtype) {
-    case FS_F32: hipLaunchKernelGGL((quantize_pages_kernel<float, true>), grid, block, 0, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
-    case FS_F16: hipLaunchKernelGGL((quantize_pages_kernel<__half, true>), grid, block, 0, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
-    case FS_BF16: hipLaunchKernelGGL((quantize_pages_kernel<__hip_bfloat16, true>), grid, block, 0, st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
+    case FS_F32: hipLaunchKernelGGL((quantize_pages_kernel<float, kGfFp8>), grid, block, 0, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL((quantize_pages_kernel<__half, kGfFp8>), grid, block, 0, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL((quantize_pages_kernel<__hip_bfloat16, kGfFp8>), grid, block, 0, st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, v, scale, zero); break;
     default: return set_error(FS_ERR_INVALID, "quantize_pages_fp8: dtype code must be 0, 1 or 2");
   }
   return check_launch("quantize_pages_fp8");
@@ -801,4 +837,44 @@ extern "C" int fs_dequantize_fp8(const uint8_t* values, const float* scale, int6
     default: return set_error(FS_ERR_INVALID, "dequantize_fp8: dtype code must be 0, 1 or 2");
   }
   return check_launch("dequantize_fp8_per_block");
+}
+
+extern "C" int fs_quantize_i8_channel(const void* x, int x_dtype, int64_t outer, int seq_len, int head_dim,
+                                      int block_size, int8_t* values, float* scale, int16_t* zero, void* stream) {
+  if (outer <= 0 || seq_len <= 0 || head_dim <= 0 || block_size <= 0)
+    return set_error(FS_ERR_INVALID, "quantize_channel: sizes must be positive");
+  if (!x || !values || !scale || !zero) return set_error(FS_ERR_INVALID, "quantize_channel: null pointer");
+  const int nb = (seq_len + block_size - 1) / block_size;
+  const int64_t groups = outer * nb;
+  if ((groups + 3) / 4 > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "quantize_channel: too many groups");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+  switch (x_dtype) {
+    case FS_F32: hipLaunchKernelGGL((quantize_blocks_kernel<float, kGfChannel>), grid, block, 0, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL((quantize_blocks_kernel<__half, kGfChannel>), grid, block, 0, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL((quantize_blocks_kernel<__hip_bfloat16, kGfChannel>), grid, block, 0, st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero); break;
+    default: return set_error(FS_ERR_INVALID, "quantize_channel: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("quantize_int8_per_channel");
+}
+
+extern "C" int fs_quantize_pages_i8_channel(const void* x, int x_dtype, int batch, int heads, int seq_len,
+                                            int head_dim, int page_size, const int64_t* page_src, int64_t num_pages,
+                                            int8_t* values, float* scale, int16_t* zero, void* stream) {
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0 || page_size <= 0)
+    return set_error(FS_ERR_INVALID, "quantize_pages_channel: sizes must be positive");
+  if (!x || !values || !scale || !zero) return set_error(FS_ERR_INVALID, "quantize_pages_channel: null pointer");
+  const int nbps = (seq_len + page_size - 1) / page_size;
+  if (num_pages != (int64_t)batch * nbps)
+    return set_error(FS_ERR_INVALID, "quantize_pages_channel: num_pages must equal batch * ceil(seq_len / page)");
+  const int64_t groups = num_pages * heads;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = wave_grid(groups), block(256);
+  switch (x_dtype) {
+    case FS_F32: hipLaunchKernelGGL((quantize_pages_kernel<float, kGfChannel>), grid, block, 0, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;
+    case FS_F16: hipLaunchKernelGGL((quantize_pages_kernel<__half, kGfChannel>), grid, block, 0, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;
+    case FS_BF16: hipLaunchKernelGGL((quantize_pages_kernel<__hip_bfloat16, kGfChannel>), grid, block, 0, st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero); break;
+    default: return set_error(FS_ERR_INVALID, "quantize_pages_channel: dtype code must be 0, 1 or 2");
+  }
+  return check_launch("quantize_pages_channel");
 }

@@ -22,7 +22,8 @@ import torch
 
 from . import _lib
 from .quant import (FP8_DTYPE, QuantizedTensor, dequantize_int8_per_block, estimate_quantized_bytes, is_fp8,
-                    quantize_fp8_per_block, quantize_int8_per_block, quantize_int8_symmetric_per_token)
+                    is_per_channel, quantize_fp8_per_block, quantize_int8_per_block, quantize_int8_per_channel,
+                    quantize_int8_symmetric_per_token)
 
 _SCALE_FLOOR = 1.0e-8  # quantizing an all-zero block gives int8 -128, scale fp32(1e-8), zero 0
 
@@ -34,10 +35,11 @@ def _normalize_device(device: torch.device | str) -> torch.device:
     return dev
 
 
-def _empty_page_store(pages: int, heads: int, page: int, dim: int, device: torch.device):
+def _empty_page_store(pages: int, heads: int, page: int, dim: int, device: torch.device, per_channel: bool = False):
     values = torch.empty((pages, heads, 1, page, dim), dtype=torch.int8, device=device)
-    scale = torch.empty((pages, heads, 1, 1, 1), dtype=torch.float32, device=device)
-    zero = torch.empty((pages, heads, 1, 1, 1), dtype=torch.int16, device=device)
+    params = dim if per_channel else 1
+    scale = torch.empty((pages, heads, 1, 1, params), dtype=torch.float32, device=device)
+    zero = torch.empty((pages, heads, 1, 1, params), dtype=torch.int16, device=device)
     return values, scale, zero
 
 
@@ -418,11 +420,13 @@ class PagedKVCache:
         ``kv_format`` (not in the reference): ``affine_block`` quantizes each page per head
         as the reference does; ``symmetric_token`` stores symmetric absmax INT8 with one scale
         per token (``quantize_int8_symmetric_per_token``, quant block 1); ``fp8_block`` stores
-        FP8 E4M3 codes with one scale per page and head (``quantize_fp8_per_block``).
+        FP8 E4M3 codes with one scale per page and head (``quantize_fp8_per_block``);
+        ``affine_channel`` stores affine INT8 with one scale / zero point per page, head and
+        channel (``quantize_int8_per_channel``).
         """
 
-        if kv_format not in ("affine_block", "symmetric_token", "fp8_block"):
-            raise ValueError("kv_format must be affine_block, symmetric_token or fp8_block")
+        if kv_format not in ("affine_block", "symmetric_token", "fp8_block", "affine_channel"):
+            raise ValueError("kv_format must be affine_block, symmetric_token, fp8_block or affine_channel")
 
         if k.ndim != 4 or v.ndim != 4:
             raise ValueError("k and v must be [batch, heads, seq_len, head_dim]")
@@ -456,6 +460,13 @@ class PagedKVCache:
         if kv_format == "symmetric_token":
             k_quant = quantize_int8_symmetric_per_token(cls._physical_pages(k, block_size, perm))
             v_quant = quantize_int8_symmetric_per_token(cls._physical_pages(v, block_size, perm))
+        elif kv_format == "affine_channel":
+            if k.device.type == "cuda":
+                k_quant = cls._quantize_pages(k, block_size, perm, total, per_channel=True)
+                v_quant = cls._quantize_pages(v, block_size, perm, total, per_channel=True)
+            else:
+                k_quant = quantize_int8_per_channel(cls._physical_pages(k, block_size, perm), block_size=block_size)
+                v_quant = quantize_int8_per_channel(cls._physical_pages(v, block_size, perm), block_size=block_size)
         elif kv_format == "fp8_block":
             if k.device.type == "cuda":
                 k_quant = cls._quantize_pages(k, block_size, perm, total, fp8=True)
@@ -484,15 +495,20 @@ class PagedKVCache:
 
     @staticmethod
     def _quantize_pages(x: torch.Tensor, block_size: int, perm: torch.Tensor | None, total: int,
-                        fp8: bool = False) -> QuantizedTensor:
+                        fp8: bool = False, per_channel: bool = False) -> QuantizedTensor:
         lib = _lib.require()
         batch, heads, seq_len, head_dim = (int(s) for s in x.shape)
         src = _src_for_kernel(x.detach())
-        values, scale, zero = _empty_page_store(total, heads, block_size, head_dim, x.device)
+        values, scale, zero = _empty_page_store(total, heads, block_size, head_dim, x.device, per_channel)
         if fp8:
             values = values.view(FP8_DTYPE)
         page_src = None if perm is None else perm.to(torch.int64).contiguous()
-        quantize_pages = lib.fs_quantize_pages_fp8 if fp8 else lib.fs_quantize_pages_i8
+        if fp8:
+            quantize_pages = lib.fs_quantize_pages_fp8
+        elif per_channel:
+            quantize_pages = lib.fs_quantize_pages_i8_channel
+        else:
+            quantize_pages = lib.fs_quantize_pages_i8
         _lib.check(quantize_pages(
             src.data_ptr(), _lib.dtype_code(src.dtype), batch, heads, seq_len, head_dim, block_size,
             _lib.ptr(page_src), total, values.data_ptr(), scale.data_ptr(), zero.data_ptr(),
@@ -519,8 +535,9 @@ class PagedKVCache:
         the whole store is requantized (block = page), as in the reference.
         """
 
-        if is_fp8(self.k_quant) or is_fp8(self.v_quant):
-            raise ValueError("append requantizes pages in the reference's affine INT8 format; FP8 caches are read-only")
+        if is_fp8(self.k_quant) or is_fp8(self.v_quant) or is_per_channel(self.k_quant):
+            raise ValueError("append requantizes pages in the reference's per-page affine INT8 format; FP8 and "
+                             "per-channel caches are read-only")
         if k_new.ndim != 4 or v_new.ndim != 4:
             raise ValueError("k_new and v_new must be [batch, heads, tokens, head_dim]")
         if k_new.shape != v_new.shape:

@@ -149,6 +149,70 @@ def quantize_int8_symmetric_per_token(x: torch.Tensor) -> QuantizedTensor:
     return _quantize_sym_portable(x)
 
 
+# ---- per-channel affine INT8 -----------------------------------------------------------------
+# A KV format beside the reference's (which lists per-channel scales among the formats to
+# compare, doc/TODO.MD:241-255): the reference's per-block op sequence applied to each channel
+# column of a block, so scale / zero_point are [..., n_blocks, 1, head_dim] and every
+# dequantize formula here broadcasts over them unchanged.
+
+
+def is_per_channel(q: QuantizedTensor) -> bool:
+    """True when scale / zero_point hold one entry per channel of each block."""
+
+    return q.values.shape[-1] > 1 and q.scale.shape[-1] == q.values.shape[-1]
+
+
+def _quantize_channel_portable(x: torch.Tensor, block_size: int) -> QuantizedTensor:
+    original_shape = tuple(x.shape)
+    xf = _pad_sequence_dim(x.detach().to(torch.float32), block_size)
+    lead, seq, dim = xf.shape[:-2], xf.shape[-2], xf.shape[-1]
+    blocked = xf.reshape(*lead, seq // block_size, block_size, dim)
+    lo = blocked.amin(dim=-2, keepdim=True)
+    hi = blocked.amax(dim=-2, keepdim=True)
+    scale = ((hi - lo) / 255.0).clamp_min(1.0e-8)
+    zero = torch.round(-lo / scale).clamp(0, 255)
+    codes = torch.round(blocked / scale + zero).clamp(0, 255)
+    values = (codes.to(torch.int16) - 128).to(torch.int8)
+    return QuantizedTensor(values, scale, zero.to(torch.int16), block_size, original_shape)
+
+
+def _quantize_channel_hip(x: torch.Tensor, block_size: int) -> QuantizedTensor:
+    lib = _lib.require()
+    original_shape = tuple(x.shape)
+    xd = x.detach()
+    if xd.dtype not in _lib.DTYPE_CODE:
+        xd = xd.to(torch.float32)
+    xd = xd.contiguous()
+    lead = tuple(xd.shape[:-2])
+    seq, dim = int(xd.shape[-2]), int(xd.shape[-1])
+    n_blocks = (seq + block_size - 1) // block_size
+    outer = math.prod(lead) if lead else 1
+    dev = xd.device
+    values = torch.empty((*lead, n_blocks, block_size, dim), dtype=torch.int8, device=dev)
+    scale = torch.empty((*lead, n_blocks, 1, dim), dtype=torch.float32, device=dev)
+    zero = torch.empty((*lead, n_blocks, 1, dim), dtype=torch.int16, device=dev)
+    if outer > 0:
+        _lib.check(lib.fs_quantize_i8_channel(
+            xd.data_ptr(), _lib.dtype_code(xd.dtype), outer, seq, dim, block_size,
+            values.data_ptr(), scale.data_ptr(), zero.data_ptr(), _lib.stream_ptr(dev)))
+    return QuantizedTensor(values, scale, zero, block_size, original_shape)
+
+
+def quantize_int8_per_channel(x: torch.Tensor, block_size: int = 16) -> QuantizedTensor:
+    """Affine INT8 with one scale / zero point per ``block_size`` tokens and per channel.
+
+    Each channel column of a block is quantized as ``quantize_int8_per_block`` would quantize
+    that ``[block_size, 1]`` column; ``scale`` / ``zero_point`` are ``[..., n_blocks, 1, D]``.
+    The decode kernels read it with quant blocks of a multiple of 16 tokens (other shapes run
+    the element-wise kernel).
+    """
+
+    _validate_block_tensor(x, block_size)
+    if x.device.type == "cuda":
+        return _quantize_channel_hip(x, block_size)
+    return _quantize_channel_portable(x, block_size)
+
+
 # ---- FP8 E4M3 per-block format ----------------------------------------------------------------
 # A KV format beside the reference's (which lists FP8 among the formats to compare,
 # doc/TODO.MD:241-255): OCP FP8 E4M3 codes (torch.float8_e4m3fn) in the same block layout, one
@@ -265,7 +329,7 @@ def dequantize_int8_per_block(q: QuantizedTensor, dtype: torch.dtype | None = No
 
     if is_fp8(q):
         return _dequantize_fp8(q, dtype)
-    if q.values.device.type == "cuda":
+    if q.values.device.type == "cuda" and not is_per_channel(q):
         return _dequantize_hip(q, dtype)
     u = q.values.to(torch.int16) + 128
     x = (u.to(torch.float32) - q.zero_point.to(torch.float32)) * q.scale.to(torch.float32)

@@ -24,7 +24,7 @@ import torch
 
 from . import _lib
 from .paged import PagedKVCache
-from .quant import build_compression_stats
+from .quant import build_compression_stats, is_per_channel
 from .triton_utils import TREE_NODE_GROUP, device_cu_count, launch_plan, plan_tree_splits
 
 __all__ = ["tree_verify_attention", "validate_parents", "path_mask", "tree_shape"]
@@ -72,8 +72,10 @@ def _validate(q, cache, draft_k, draft_v):
         raise ValueError("need at least one draft node")
     if head_dim > 256:
         raise ValueError("head_dim must be <= 256")
-    if cache.k_quant.values.dtype != torch.int8 or cache.v_quant.values.dtype != torch.int8:
-        raise ValueError("tree verification reads INT8 caches (affine_block or symmetric_token)")
+    if cache.k_quant.values.dtype != torch.int8 or cache.v_quant.values.dtype != torch.int8 or \
+            is_per_channel(cache.k_quant):
+        raise ValueError("tree verification reads INT8 caches with per-block or per-token scales "
+                         "(affine_block or symmetric_token)")
     return batch, nodes, heads, head_dim
 
 

@@ -16,7 +16,8 @@ from typing import Any
 import torch
 
 from . import _lib
-from .quant import FP8_DTYPE, QuantizedTensor, build_compression_stats, estimate_quantized_bytes, is_fp8
+from .quant import (FP8_DTYPE, QuantizedTensor, build_compression_stats, estimate_quantized_bytes, is_fp8,
+                    is_per_channel)
 from .triton_utils import (
     dispatch_triton_or_fallback,
     launch_plan,
@@ -80,12 +81,16 @@ def _validate_triton_fused_inputs(q: torch.Tensor, k_quant: QuantizedTensor, v_q
         n_blocks = (seq_len + qt.block_size - 1) // qt.block_size
         if tuple(qt.values.shape) != (batch, heads, n_blocks, qt.block_size, head_dim):
             raise ValueError(f"{name}.values must be [batch, heads, n_blocks, block_size, head_dim]")
-        if qt.scale.numel() != batch * heads * n_blocks or qt.zero_point.numel() != batch * heads * n_blocks:
-            raise ValueError(f"{name} scale/zero_point must have one entry per block")
+        per = head_dim if is_per_channel(qt) else 1
+        if qt.scale.numel() != batch * heads * n_blocks * per or qt.zero_point.numel() != batch * heads * n_blocks * per:
+            raise ValueError(f"{name} scale/zero_point must have one entry per block (or per block and channel)")
     if k_quant.block_size != v_quant.block_size:
         raise ValueError("K/V quant block sizes must match")
-    if k_quant.values.dtype != v_quant.values.dtype:
-        raise ValueError("k_quant and v_quant must use the same format (int8 or float8_e4m3fn values)")
+    if k_quant.values.dtype != v_quant.values.dtype or is_per_channel(k_quant) != is_per_channel(v_quant):
+        raise ValueError("k_quant and v_quant must use the same format (int8 or float8_e4m3fn values, "
+                         "per-block or per-channel scales)")
+    if is_per_channel(k_quant) and is_fp8(k_quant):
+        raise ValueError("per-channel scales are supported for INT8 stores")
 
 
 def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTensor, v_quant: QuantizedTensor,
@@ -107,8 +112,9 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     out = torch.empty_like(q_c)
     sm_scale = 1.0 / math.sqrt(float(head_dim))
     rows = batch * heads
+    per_channel = is_per_channel(k_quant)
     tiled, waves, split_tiles, max_splits, block_n = launch_plan(seq_len, rows, head_dim, block_size, block_size,
-                                                                 dev)
+                                                                 dev, per_channel=per_channel)
     stream = _lib.stream_ptr(dev)
     workspace, ws_bytes = None, 0
     if max_splits > 1:
@@ -120,7 +126,8 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
             kv[4].data_ptr(), _lib.ptr(lengths_c), out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads,
             head_dim, seq_len, n_blocks, block_size, sm_scale, split_tiles, max_splits, waves, stream))
     else:
-        _lib.check(lib.fs_fused_decode_i8(
+        decode = lib.fs_fused_decode_i8_channel if per_channel else lib.fs_fused_decode_i8
+        _lib.check(decode(
             q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), _lib.ptr(lengths_c),
             out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads, head_dim, seq_len, n_blocks, block_size,
             sm_scale, split_tiles, max_splits, waves, stream))

@@ -18,7 +18,7 @@ import torch
 
 from . import _lib
 from .paged import PagedKVCache
-from .quant import FP8_DTYPE, build_compression_stats, is_fp8
+from .quant import FP8_DTYPE, build_compression_stats, is_fp8, is_per_channel
 from .triton_utils import (
     dispatch_triton_or_fallback,
     launch_plan,
@@ -54,8 +54,12 @@ def _validate_triton_paged_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
         raise ValueError("q dtype must be float16, bfloat16 or float32")
     pages, heads, page, head_dim = cache.k_quant.original_shape
     qb = cache.k_quant.block_size
-    if cache.k_quant.values.dtype != cache.v_quant.values.dtype:
-        raise ValueError("cache K and V must use the same format (int8 or float8_e4m3fn values)")
+    if cache.k_quant.values.dtype != cache.v_quant.values.dtype or \
+            is_per_channel(cache.k_quant) != is_per_channel(cache.v_quant):
+        raise ValueError("cache K and V must use the same format (int8 or float8_e4m3fn values, per-block or "
+                         "per-channel scales)")
+    if is_per_channel(cache.k_quant) and is_fp8(cache.k_quant):
+        raise ValueError("per-channel scales are supported for INT8 stores")
     for name, qt in (("k_quant", cache.k_quant), ("v_quant", cache.v_quant)):
         if qt.values.dtype not in (torch.int8, FP8_DTYPE) or qt.scale.dtype != torch.float32 or \
                 qt.zero_point.dtype != torch.int16:
@@ -63,8 +67,11 @@ def _validate_triton_paged_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
                              "zero_point")
         if tuple(qt.values.shape) != (pages, heads, page // qb, qb, head_dim):
             raise ValueError(f"cache.{name}.values must be [pages, heads, page/quant_block, quant_block, head_dim]")
-        if qt.scale.numel() != pages * heads * (page // qb) or qt.zero_point.numel() != pages * heads * (page // qb):
-            raise ValueError(f"cache.{name} scale/zero_point must have one entry per quant block")
+        per = head_dim if is_per_channel(qt) else 1
+        n_params = pages * heads * (page // qb) * per
+        if qt.scale.numel() != n_params or qt.zero_point.numel() != n_params:
+            raise ValueError(f"cache.{name} scale/zero_point must have one entry per quant block (or per block and "
+                             "channel)")
     if cache.block_table.ndim != 2 or cache.block_table.dtype not in (torch.int32, torch.int64):
         raise ValueError("block_table must be a 2-D int32/int64 tensor")
     if cache.lengths.ndim != 1 or cache.lengths.shape[0] != cache.batch_size:
@@ -90,8 +97,9 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
     out = torch.empty_like(q_c)
     sm_scale = 1.0 / math.sqrt(float(head_dim))
     rows = batch * heads
+    per_channel = is_per_channel(kq)
     tiled, waves, split_tiles, max_splits, block_n = launch_plan(
-        max_seq_len, rows, head_dim, int(cache.block_size), int(kq.block_size), dev)
+        max_seq_len, rows, head_dim, int(cache.block_size), int(kq.block_size), dev, per_channel=per_channel)
     stream = _lib.stream_ptr(dev)
     workspace, ws_bytes = None, 0
     if max_splits > 1:
@@ -104,7 +112,8 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
             out.data_ptr(), _lib.ptr(workspace), ws_bytes, batch, heads, head_dim, num_pages, int(cache.block_size),
             int(kq.block_size), max_seq_len, sm_scale, split_tiles, max_splits, waves, stream))
     else:
-        _lib.check(lib.fs_paged_decode_i8(
+        decode = lib.fs_paged_decode_i8_channel if per_channel else lib.fs_paged_decode_i8
+        _lib.check(decode(
             q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), table.data_ptr(),
             table.element_size(), int(table.shape[1]), lengths.data_ptr(), out.data_ptr(), _lib.ptr(workspace),
             ws_bytes, batch, heads, head_dim, num_pages, int(cache.block_size), int(kq.block_size), max_seq_len,

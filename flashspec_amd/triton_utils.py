@@ -218,13 +218,19 @@ def plan_tree_splits(seq_len: int, units: int, head_dim: int, cu_count: int) -> 
     return split_tiles, math.ceil(tiles / split_tiles), waves
 
 
-def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, device):
+def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, device,
+                per_channel: bool = False):
     """(tiled, waves_per_block, split_tiles, max_splits, block_n) for one decode launch."""
 
     from . import _lib
 
-    tiled = bool(_lib.require().fs_decode_tiled_path(head_dim, page_size, quant_block))
-    max_waves = 8 if head_dim > 128 else MAX_TILED_WAVES  # register budget of the 256-dim register layout
+    lib = _lib.require()
+    if per_channel:
+        tiled = bool(lib.fs_decode_tiled_path_channel(head_dim, page_size, quant_block))
+    else:
+        tiled = bool(lib.fs_decode_tiled_path(head_dim, page_size, quant_block))
+    # register budget: the 256-dim register layout and per-channel parameters run 8 waves
+    max_waves = 8 if head_dim > 128 or per_channel else MAX_TILED_WAVES
     waves = forced_tiled_waves() if tiled else resolve_num_warps()
     if tiled and waves is not None:
         waves = min(waves, max_waves)

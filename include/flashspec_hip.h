@@ -221,6 +221,39 @@ int fs_paged_decode_fp8(const void* q, int q_dtype, const uint8_t* k_values, con
                         int waves_per_block, void* stream);
 
 /*
+ * Per-channel affine INT8 KV format: per block of block_size tokens, one scale / zero point per
+ * channel, each channel column quantized with fs_quantize_i8's float32 op sequence; scale / zero
+ * [outer, nb, head_dim] (pages: [num_pages, heads, head_dim]).  The decode entry points take the
+ * arguments of fs_fused_decode_i8 / fs_paged_decode_i8 with those arrays; their tiled path needs
+ * quant blocks of a multiple of 16 tokens (fs_decode_tiled_path_channel), workgroups of at most 8
+ * waves, and otherwise runs the element-wise kernel.  No counterpart in the reference, which lists
+ * per-channel scales among the KV formats to compare (doc/TODO.MD:241-255).
+ */
+int fs_quantize_i8_channel(const void* x, int x_dtype, int64_t outer, int seq_len, int head_dim,
+                           int block_size, int8_t* values, float* scale, int16_t* zero, void* stream);
+int fs_quantize_pages_i8_channel(const void* x, int x_dtype, int batch, int heads, int seq_len,
+                                 int head_dim, int page_size, const int64_t* page_src,
+                                 int64_t num_pages, int8_t* values, float* scale, int16_t* zero,
+                                 void* stream);
+int fs_fused_decode_i8_channel(const void* q, int q_dtype,
+                               const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                               const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                               const int64_t* lengths, void* out, void* workspace,
+                               int64_t workspace_bytes, int batch, int heads, int head_dim,
+                               int seq_len, int n_blocks, int block_size, float sm_scale,
+                               int split_tiles, int max_splits, int waves_per_block, void* stream);
+int fs_paged_decode_i8_channel(const void* q, int q_dtype,
+                               const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                               const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                               const void* block_table, int table_index_bytes, int64_t table_cols,
+                               const int64_t* lengths, void* out, void* workspace,
+                               int64_t workspace_bytes, int batch, int heads, int head_dim,
+                               int64_t num_pages, int page_size, int quant_block, int max_seq_len,
+                               float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                               void* stream);
+int fs_decode_tiled_path_channel(int head_dim, int page_size, int quant_block);
+
+/*
  * Dequantize ((v + 128) - zero) * scale and crop the padding.  Replaces
  * reference src/flashspec/quant.py:168-204.
  *   out [outer, seq_len, head_dim] out_dtype

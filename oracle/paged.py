@@ -72,8 +72,9 @@ def from_dense(
     ``perm[j]`` is the batch-major page stored at physical slot ``j``
     (``physical = pages[perm]``) and ``block_table = inverse(perm)``
     (paged.py:384-398).  ``perm=None`` is the contiguous layout.  ``kv_format="fp8_block"``
-    quantizes the pages with the FP8 E4M3 per-page format of oracle/fp8.py instead of the
-    reference's affine INT8.
+    quantizes the pages with the FP8 E4M3 per-page format of oracle/fp8.py, and
+    ``"affine_channel"`` with per-page, per-channel affine INT8 (quant.quantize_int8_per_channel),
+    instead of the reference's per-page affine INT8.
     """
 
     B, H, S, D = k.shape
@@ -96,10 +97,12 @@ def from_dense(
             raise ValueError("lengths must be [batch] with values in [0, seq_len]")
     if kv_format == "affine_block":
         quantize = oq.quantize_int8_per_block
+    elif kv_format == "affine_channel":
+        quantize = oq.quantize_int8_per_channel
     elif kv_format == "fp8_block":
         from .fp8 import quantize_fp8_per_block as quantize
     else:
-        raise ValueError("kv_format must be 'affine_block' or 'fp8_block'")
+        raise ValueError("kv_format must be 'affine_block', 'affine_channel' or 'fp8_block'")
     return OracleCache(
         k_quant=quantize(pk, block_size),
         v_quant=quantize(pv, block_size),

@@ -79,6 +79,36 @@ def dequantize_int8_per_block(q: OracleQuant) -> np.ndarray:
     return x.reshape(*lead, -1, head_dim)[..., :seq_len, :].astype(F32)
 
 
+def quantize_int8_per_channel(x: np.ndarray, block_size: int = 16) -> OracleQuant:
+    """Affine INT8 with one scale / zero point per block of ``block_size`` tokens and per
+    channel: a KV format offered beside the reference's (which lists per-channel scales among
+    the formats to compare, doc/TODO.MD:241-255).  Each channel column of a block is quantized
+    exactly as the reference's per-block quantizer would quantize that [block_size, 1] column
+    (same float32 op sequence, padding included), which tests/test_oracle.py checks; scale and
+    zero_point are [..., n_blocks, 1, head_dim], so dequantize_int8_per_block's broadcast formula
+    reads it unchanged.
+    """
+
+    if x.ndim < 2:
+        raise ValueError("x needs sequence and feature axes")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    if x.shape[-1] <= 0 or x.shape[-2] <= 0:
+        raise ValueError("sequence and feature axes must be non-empty")
+    original_shape = tuple(int(s) for s in x.shape)
+    xf = pad_sequence_dim(np.asarray(x).astype(F32), block_size)
+    lead = xf.shape[:-2]
+    n_blocks = xf.shape[-2] // block_size
+    blocked = xf.reshape(*lead, n_blocks, block_size, xf.shape[-1])
+    mn = blocked.min(axis=-2, keepdims=True)
+    mx = blocked.max(axis=-2, keepdims=True)
+    scale = np.maximum((mx - mn) / F32(255.0), SCALE_FLOOR).astype(F32)
+    zp = np.clip(np.rint(-mn / scale), F32(0), F32(255)).astype(F32)
+    qu = np.clip(np.rint(blocked / scale + zp), F32(0), F32(255))
+    values = (qu.astype(np.int16) - 128).astype(np.int8)
+    return OracleQuant(values, scale, zp.astype(np.int16), block_size, original_shape)
+
+
 def dequantize(q: OracleQuant) -> np.ndarray:
     """Dequantize either KV format: int8 values are the affine INT8 format above, uint8 values
     the FP8 E4M3 codes of oracle/fp8.py."""

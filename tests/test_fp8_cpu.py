@@ -50,3 +50,23 @@ def test_fp8_argument_checks():
         fa.PagedKVCache.from_dense(torch.zeros(1, 1, 4, 8), torch.zeros(1, 1, 4, 8), 4, kv_format="fp4")
     with pytest.raises(ValueError):
         fa.dequantize_fp8_per_block(fa.quantize_int8_per_block(torch.zeros(1, 16, 8), 16))
+
+
+# ---- per-channel affine INT8 (portable path) ---------------------------------------------------
+
+@pytest.mark.parametrize("shape,bs,dtype", [((2, 3, 45, 24), 16, torch.float32), ((1, 2, 64, 128), 32, torch.float16),
+                                            ((2, 1, 10, 8), 4, torch.bfloat16)])
+def test_portable_per_channel_bit_exact(shape, bs, dtype):
+    from oracle import quant as oq
+
+    g = torch.Generator().manual_seed(sum(shape) + 1)
+    x = (torch.randn(shape, generator=g) * torch.rand(shape[-1], generator=g) * 20).to(dtype)
+    got = fa.quantize_int8_per_channel(x, bs)
+    assert got.scale.shape[-1] == shape[-1]
+    assert_quant_equal(from_qt(got), oq.quantize_int8_per_channel(x.to(torch.float32).numpy(), bs), "per-channel")
+    cache = fa.PagedKVCache.from_dense(x.to(torch.float32).reshape(1, *x.shape[-3:]) if x.ndim == 3 else
+                                       x.to(torch.float32), x.to(torch.float32) if x.ndim == 4 else
+                                       x.to(torch.float32).reshape(1, *x.shape[-3:]), bs, kv_format="affine_channel")
+    with pytest.raises(ValueError):
+        cache.append(torch.zeros(cache.batch_size, cache.num_heads, 1, cache.head_dim),
+                     torch.zeros(cache.batch_size, cache.num_heads, 1, cache.head_dim))

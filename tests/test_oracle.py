@@ -394,3 +394,25 @@ def test_fp8_zero_block_and_padding():
     back = fp8.dequantize_fp8_per_block(q)
     assert back.shape == x.shape and back[0, 3, 2] == np.float32(-1.5)
     assert np.array_equal(back[0, 4:], x[0, 4:])
+
+
+# ---- per-channel affine INT8 (quant.quantize_int8_per_channel) -------------------------------
+
+def test_per_channel_equals_per_block_on_each_column():
+    """Each channel column of a block is the reference's per-block quantizer on that column
+    (which the reference's golden vectors pin), padding and all."""
+
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((2, 3, 45, 12)) * rng.uniform(0.01, 30, size=12)).astype(np.float32)
+    pc = oq.quantize_int8_per_channel(x, 16)
+    assert pc.values.shape == (2, 3, 3, 16, 12) and pc.scale.shape == (2, 3, 3, 1, 12)
+    for d in range(12):
+        col = oq.quantize_int8_per_block(x[..., d:d + 1], 16)
+        assert np.array_equal(pc.values[..., d:d + 1], col.values)
+        assert np.array_equal(pc.scale[..., d:d + 1], col.scale)
+        assert np.array_equal(pc.zero_point[..., d:d + 1], col.zero_point)
+    back = oq.dequantize_int8_per_block(pc)
+    assert back.shape == x.shape
+    assert np.abs(back - x).max() <= 0.5 * pc.scale.max() * (1 + 1e-5)
+    # the generic dequantize dispatch reads it as the affine format
+    assert np.array_equal(oq.dequantize(pc), back)
