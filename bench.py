@@ -498,7 +498,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBPS, 4),
             "traffic": load_traffic(config_key),
-            "kernel": "decode_rows_kernel<128, __half, true> (paged_quant_attention)",
+            "kernel": "decode_rows_kernel<128, __half, true, 0, 0> (paged_quant_attention)",
             "kernel_avg_us": round(kernel_us, 2),
             "kernel_avg_us_source": "timed-region HIP events / steps (one launch per step)" if single_launch
                                     else "per-launch HIP event pairs",
