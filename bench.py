@@ -244,7 +244,11 @@ SHAPES = [
     ("q_bfloat16_fp8", 8, 32, 4096, 128, 16, 16, "bfloat16", None, "fp8"),
     ("fp8_per_token", 8, 32, 4096, 128, 16, 1, "float16", None, "fp8"),
     ("per_channel_block_16", 8, 32, 4096, 128, 16, 16, "float16", None, "channel"),
+    ("per_channel_block_32", 8, 32, 4096, 128, 32, 32, "float16", None, "channel"),
     ("per_channel_block_64", 8, 32, 4096, 128, 64, 64, "float16", None, "channel"),
+    ("per_channel_block_128", 8, 32, 4096, 128, 128, 128, "float16", None, "channel"),
+    ("per_channel_head_dim_64_block_64", 8, 32, 4096, 64, 64, 64, "float16", None, "channel"),
+    ("per_channel_head_dim_256_block_64", 8, 32, 2048, 256, 64, 64, "float16", None, "channel"),
 ]
 
 

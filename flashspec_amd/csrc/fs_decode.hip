@@ -306,43 +306,74 @@ struct ChannelParams {
   float vs[16], vz[16];
 };
 
-// `meta` = quant block index (-1: unbacked tile or idle lane: all-zero parameters);
-// scale / zero entries of channel d of block m sit at m * D + d.
-__device__ __forceinline__ void load_channel_params(ChannelParams& cp, const DecodeParams& p, int meta, int D,
-                                                    int d0, const float* q) {
-  float ks[16], kz[16];
+// The raw parameters of a lane's 16 channels of one quant block as loaded (K / V scales, K / V
+// zero points as packed int16): loaded ahead of the tile that uses them and converted there.
+struct ChannelRaw {
+  float4 ks[4], vs[4];
+  uint4 kz[2], vz[2];
+};
+
+// `meta` = quant block index, wave-uniform (-1: unbacked block: all-zero parameters, without
+// loads); scale / zero entries of channel d of block m sit at m * D + d.  Lanes past head_dim
+// (d0 < 0) read channels 0..15 of the block: finite values that meet a zero query.
+__device__ __forceinline__ void load_channel_raw(ChannelRaw& r, const DecodeParams& p, int meta, int D, int d0) {
   if (meta >= 0) {
-    const size_t at = (size_t)meta * D + d0;
+    const size_t at = (size_t)meta * D + (d0 >= 0 ? d0 : 0);
     const float4* ks4 = (const float4*)(p.sc[0] + at);
     const float4* vs4 = (const float4*)(p.sc[1] + at);
     const uint4* kz8 = (const uint4*)(p.zp[0] + at);
     const uint4* vz8 = (const uint4*)(p.zp[1] + at);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float4 a = ks4[i], v = vs4[i];
-      ks[4 * i] = a.x; ks[4 * i + 1] = a.y; ks[4 * i + 2] = a.z; ks[4 * i + 3] = a.w;
-      cp.vs[4 * i] = v.x; cp.vs[4 * i + 1] = v.y; cp.vs[4 * i + 2] = v.z; cp.vs[4 * i + 3] = v.w;
+      r.ks[i] = ks4[i];
+      r.vs[i] = vs4[i];
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint4 a = kz8[i], v = vz8[i];
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, vw[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        kz[8 * i + 2 * k] = (float)(int16_t)(aw[k] & 0xffffu);
-        kz[8 * i + 2 * k + 1] = (float)(int16_t)(aw[k] >> 16);
-        cp.vz[8 * i + 2 * k] = (float)(int16_t)(vw[k] & 0xffffu);
-        cp.vz[8 * i + 2 * k + 1] = (float)(int16_t)(vw[k] >> 16);
-      }
+      r.kz[i] = kz8[i];
+      r.vz[i] = vz8[i];
     }
   } else {
+    const float4 zf = make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint4 zu = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) ks[e] = kz[e] = cp.vs[e] = cp.vz[e] = 0.f;
+    for (int i = 0; i < 4; ++i) {
+      r.ks[i] = zf;
+      r.vs[i] = zf;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      r.kz[i] = zu;
+      r.vz[i] = zu;
+    }
+  }
+}
+
+__device__ __forceinline__ void channel_params(ChannelParams& cp, const ChannelRaw& r, float qk_scale,
+                                               const float* q) {
+  float ks[16], kz[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 a = r.ks[i], v = r.vs[i];
+    ks[4 * i] = a.x; ks[4 * i + 1] = a.y; ks[4 * i + 2] = a.z; ks[4 * i + 3] = a.w;
+    cp.vs[4 * i] = v.x; cp.vs[4 * i + 1] = v.y; cp.vs[4 * i + 2] = v.z; cp.vs[4 * i + 3] = v.w;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t aw[4] = {r.kz[i].x, r.kz[i].y, r.kz[i].z, r.kz[i].w};
+    const uint32_t vw[4] = {r.vz[i].x, r.vz[i].y, r.vz[i].z, r.vz[i].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      kz[8 * i + 2 * k] = (float)(int16_t)(aw[k] & 0xffffu);
+      kz[8 * i + 2 * k + 1] = (float)(int16_t)(aw[k] >> 16);
+      cp.vz[8 * i + 2 * k] = (float)(int16_t)(vw[k] & 0xffffu);
+      cp.vz[8 * i + 2 * k + 1] = (float)(int16_t)(vw[k] >> 16);
+    }
   }
   float c = 0.f;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    cp.qk[e] = q[e] * ks[e] * p.qk_scale;
+    cp.qk[e] = q[e] * ks[e] * qk_scale;
     c = fmaf(cp.qk[e], kz[e], c);
   }
   cp.c = c;
@@ -387,7 +418,7 @@ __device__ __forceinline__ void consume_tile_channel(LaneState& st, const TileRe
 // that its 128-float registers per lane fit without spilling.
 // Per-channel parameters add ~50 registers per lane: 8 waves there too.
 constexpr int max_tiled_waves(int DP, int QM = kQmBlock) {
-  return (DP == 256 || QM == kQmChannel) ? 8 : kMaxWaves;
+  return (DP == 256 || QM == kQmChannel || QM == kQmChannelBlocks) ? 8 : kMaxWaves;
 }
 
 // Register layout (64, 128 or 256 dims) that serves a head_dim on the tiled path.
@@ -397,7 +428,8 @@ template <int DP, typename QT, bool PAGED, int QM, int VF>
 __global__ void __launch_bounds__(kWave * max_tiled_waves(DP, QM))
 decode_rows_kernel(const DecodeParams p) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
-  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken, CH = QM == kQmChannel;
+  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken, CHB = QM == kQmChannelBlocks;
+  constexpr bool CH = QM == kQmChannel || CHB;
   __shared__ float s_acc[kMaxWaves * DP];
   __shared__ float s_ml[2 * kMaxWaves];
 
@@ -419,25 +451,46 @@ decode_rows_kernel(const DecodeParams p) {
   // the store in step, which keeps page accesses dense, and the fixed order makes results
   // bit-reproducible.  The table loads are sized by max_seq_len so they go out together
   // with the row-length load.
+  // CHB (per-channel parameters, one [D] set per quant block of G >= 2 tiles): waves take whole
+  // quant blocks instead, blocks sb0 + w, sb0 + w + W, ... of the split with the G tiles of
+  // each in turn, so that one parameter load serves G tiles (the host keeps every split a
+  // whole number of blocks).
+  const int G = CHB ? p.quant_block / kTile : 1;
+  const int sb0 = CHB ? split * p.split_tiles / G : 0;
   const int first = split * p.split_tiles + w;
+  // tiles of this wave below tile `end`
+  auto wave_tiles = [&](int end) {
+    if constexpr (CHB) {
+      const int eb = (end + G - 1) / G;
+      return sb0 + w < eb ? (eb - sb0 - w + W - 1) / W * G : 0;
+    } else {
+      return first < end ? (end - first + W - 1) / W : 0;
+    }
+  };
   const int tiles_max = (p.seq_len + kTile - 1) / kTile;
   const int end_max = min(tiles_max, (split + 1) * p.split_tiles);
-  const int nk_max = first < end_max ? (end_max - first + W - 1) / W : 0;
+  const int nk_max = wave_tiles(end_max);
+  // the wave's lane-th tile
+  int my_tile = first + W * lane;
+  if constexpr (CHB) {
+    const int bi = lane / G;
+    my_tile = (sb0 + w + W * bi) * G + (lane - bi * G);
+  }
   // SUB (8-token quant blocks or pages): each tile is two sub-tiles with their own base and
   // quantization parameters, held as a second set of lane registers.
   int my_base = -1, my_meta = 0, my_base1 = -1, my_meta1 = 0;
-  if (lane < nk_max) {
+  if (lane < nk_max && my_tile < end_max) {
     if constexpr (SUB) {
-      const TileIndex t0 = sub_index<PAGED>(p, b, h, row, 2 * (first + W * lane));
-      const TileIndex t1 = sub_index<PAGED>(p, b, h, row, 2 * (first + W * lane) + 1);
+      const TileIndex t0 = sub_index<PAGED>(p, b, h, row, 2 * my_tile);
+      const TileIndex t1 = sub_index<PAGED>(p, b, h, row, 2 * my_tile + 1);
       my_base = t0.data;
       my_meta = t0.meta;
       my_base1 = t1.data;
       my_meta1 = t1.meta;
     } else if constexpr (TOK) {
-      my_base = token_index<PAGED>(p, b, h, row, first + W * lane);
+      my_base = token_index<PAGED>(p, b, h, row, my_tile);
     } else {
-      const TileIndex ti = tile_index<PAGED>(p, b, h, row, first + W * lane);
+      const TileIndex ti = tile_index<PAGED>(p, b, h, row, my_tile);
       my_base = ti.data;
       my_meta = ti.meta;
     }
@@ -447,8 +500,9 @@ decode_rows_kernel(const DecodeParams p) {
   const int nsplit = row_splits(len, p.split_tiles);
   if (split >= nsplit) return;  // whole workgroup, before any barrier
   const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
-  const int nk = first < tile_end ? (tile_end - first + W - 1) / W : 0;  // <= kMaxTilesPerWave
-  if (lane >= nk) my_base = my_base1 = -1;
+  const int nk = wave_tiles(tile_end);  // <= kMaxTilesPerWave
+  // CHB: tiles of the row's last block past its end stay in the loop as empty tiles
+  if (lane >= nk || my_tile >= tile_end) my_base = my_base1 = -1;
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
   if (!TOK && !CH && my_base >= 0) {
     my_ks = p.sc[0][my_meta] * p.qk_scale;
@@ -496,7 +550,21 @@ decode_rows_kernel(const DecodeParams p) {
     if constexpr (PAGED) return kTile;
     else return p.n_blocks - (first + W * k) * kTile;
   };
+  // CHB: a block's raw parameters, its converted parameters, and the position in its block of
+  // the next tile loaded / consumed.  A block's parameters go out with its first tile, ahead
+  // of the tile's values, and are converted when that tile is consumed (one raw set suffices:
+  // blocks of two or more tiles convert it before the next block's first tile is loaded).
+  ChannelRaw rr;
+  ChannelParams cp;
+  int ld_in_block = 0, in_block = 0;
   auto load = [&](TileRegs<DP>& t, int k) {
+    if constexpr (CHB) {
+      if (ld_in_block == 0) {
+        const int bk = base_of(k);
+        load_channel_raw(rr, p, bk >= 0 ? readlane_i32(my_meta, k) : -1, D, active ? 16 * j : -1);
+      }
+      if (++ld_in_block == G) ld_in_block = 0;
+    }
     if constexpr (SUB)
       load_tile_sub<DP>(t, kbase, vbase, base_of(k), base1_of(k), D, g, active ? 16 * j : 0);
     else if constexpr (TOK)
@@ -507,13 +575,22 @@ decode_rows_kernel(const DecodeParams p) {
   auto consume = [&](const TileRegs<DP>& t, int k) {
     RowMeta<LPTILE> rm;
     const bool v0 = readlane_i32(my_base, k) >= 0;
-    if constexpr (CH) {
-      // this lane's 16 channels of the tile's quant block: K scales folded into the query,
-      // V scales / zero points applied once per tile
-      const int meta = readlane_i32(my_meta, k);
-      ChannelParams cp;
-      load_channel_params(cp, p, v0 && active ? meta : -1, D, 16 * j, q.q);
-      consume_tile_channel<DP>(st, t, cp, v0, (first + W * k) * kTile, len, g);
+    if constexpr (CHB) {
+      // this lane's 16 channels of the quant block, converted at its first tile: K scales
+      // folded into the query, V scales / zero points applied once per tile.  A block's first
+      // tile is backed whenever any of its tiles is (pages hold whole blocks; only the row's
+      // end cuts a block short).
+      if (in_block == 0) channel_params(cp, rr, p.qk_scale, q.q);
+      if (++in_block == G) in_block = 0;
+      consume_tile_channel<DP>(st, t, cp, v0, readlane_i32(my_tile, k) * kTile, len, g);
+      return;
+    } else if constexpr (CH) {
+      // single-tile blocks (or the 256-dim layout): the tile's own parameters, loaded here
+      ChannelRaw rt;
+      ChannelParams ct;
+      load_channel_raw(rt, p, v0 ? readlane_i32(my_meta, k) : -1, D, active ? 16 * j : -1);
+      channel_params(ct, rt, p.qk_scale, q.q);
+      consume_tile_channel<DP>(st, t, ct, v0, (first + W * k) * kTile, len, g);
       return;
     }
     if constexpr (TOK) {
@@ -777,9 +854,19 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
 // Per-channel stores take the tiled path with quant blocks of a multiple of 16 tokens.
 static bool tiled_path(int head_dim, int page_size, int quant_block, bool per_channel = false) {
   if (head_dim < 16 || head_dim > 256 || head_dim % 16 != 0 || page_size <= 0) return false;
-  if (per_channel) return quant_block > 0 && quant_block % kTile == 0 && page_size % quant_block == 0;
+  if (per_channel)  // a wave holds at least one whole quant block: at most 64 tiles
+    return quant_block > 0 && quant_block % kTile == 0 && quant_block <= kTile * kMaxTilesPerWave &&
+           page_size % quant_block == 0;
   if (quant_block == 1) return page_size == 1 || page_size % kTile == 0;  // contiguous rows, or 16-token pages
   return quant_block % 8 == 0 && page_size % quant_block == 0;
+}
+
+// Per-channel stores whose quant blocks span two or more tiles take the whole-block form of the
+// tiled kernel (kQmChannelBlocks), on the 64- and 128-dim register layouts; single-tile blocks
+// and the 256-dim layout, which has no registers to spare for a block's parameters in flight,
+// load each tile's parameters as they consume it (kQmChannel).
+static bool channel_whole_blocks(const DecodeParams& p) {
+  return p.quant_block / kTile >= 2 && padded_head_dim(p.head_dim) <= 128;
 }
 
 template <typename QT, bool PAGED, int QM, int VF>
@@ -787,13 +874,16 @@ static void launch_tiled_vf(const DecodeParams& p, dim3 grid, dim3 block, hipStr
   switch (padded_head_dim(p.head_dim)) {
     case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
     case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
-    default: hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
+    default:  // the whole-block per-channel form is dispatched on the 64- and 128-dim layouts only
+      if constexpr (QM != kQmChannelBlocks)
+        hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, QM, VF>), grid, block, 0, st, p);
+      break;
   }
 }
 
 template <typename QT, bool PAGED, int QM>
 static void launch_tiled(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
-  if constexpr (QM == kQmChannel) {
+  if constexpr (QM == kQmChannel || QM == kQmChannelBlocks) {
     launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);  // per-channel stores are INT8
   } else {
     if (p.vfmt == kVfFp8)
@@ -808,7 +898,9 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
   const dim3 block(kWave * waves_per_block);
   if (tiled) {
     const dim3 grid((unsigned)((int64_t)p.rows * p.max_splits));
-    if (p.per_channel)
+    if (p.per_channel && channel_whole_blocks(p))
+      launch_tiled<QT, PAGED, kQmChannelBlocks>(p, grid, block, st);
+    else if (p.per_channel)
       launch_tiled<QT, PAGED, kQmChannel>(p, grid, block, st);
     else if (p.quant_block == 1)
       launch_tiled<QT, PAGED, kQmToken>(p, grid, block, st);
@@ -870,6 +962,15 @@ static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, 
                        "waves_per_block must be <= 8 for head_dim > 128 or per-channel stores on the tiled path");
     if (tiled && p.split_tiles > kMaxTilesPerWave * waves_per_block)
       return set_error(FS_ERR_INVALID, "split_tiles must be <= 64 * waves_per_block on the tiled path");
+    if (tiled && p.per_channel && channel_whole_blocks(p)) {
+      // waves take whole quant blocks of G tiles: splits hold whole blocks, a wave <= 64 tiles
+      const int G = p.quant_block / kTile;
+      if (p.split_tiles % G != 0)
+        return set_error(FS_ERR_INVALID, "split_tiles must be a multiple of quant_block / 16 for per-channel stores");
+      if ((int64_t)G * ((p.split_tiles / G + waves_per_block - 1) / waves_per_block) > kMaxTilesPerWave)
+        return set_error(FS_ERR_INVALID,
+                         "per-channel stores: quant_block / 16 * ceil(split blocks / waves_per_block) must be <= 64");
+    }
   }
   if ((int64_t)p.rows * p.max_splits > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "decode grid too large");
   if (!p.q || !p.kv[0] || !p.kv[1] || !p.sc[0] || !p.sc[1] || !p.out ||

@@ -17,6 +17,7 @@ enum QuantMode : int {
   kQmSub = 1,    // quant block an odd multiple of 8 tokens (or 8-token pages): one per 8-token half
   kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
   kQmChannel = 3,  // per quant block (a multiple of 16 tokens) one entry per channel
+  kQmChannelBlocks = 4,  // kQmChannel with quant blocks of >= 2 tiles: waves take whole blocks
 };
 
 // Value format of the K/V store: affine INT8 (values int8 = u - 128, scale, zero point) or FP8

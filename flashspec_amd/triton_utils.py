@@ -144,29 +144,37 @@ def forced_tiled_waves() -> int | None:
 
 
 def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: bool = True,
-                waves: int | None = None, max_waves: int = MAX_TILED_WAVES) -> tuple[int, int, int]:
+                waves: int | None = None, max_waves: int = MAX_TILED_WAVES,
+                tile_group: int = 1) -> tuple[int, int, int]:
     """Return ``(split_tiles, max_splits, waves_per_block)`` for one decode launch.
 
     ``rows`` rows of up to ``seq_len`` tokens; ``waves`` fixes the workgroup size
-    (tiled path) or the waves grouped per workgroup (generic path).
+    (tiled path) or the waves grouped per workgroup (generic path).  ``tile_group`` > 1
+    (per-channel stores on the tiled path, quant_block / 16): waves take whole groups of that
+    many tiles, so splits hold whole groups and a wave at most 64 tiles.
     """
 
     tiles = max(1, math.ceil(seq_len / TILE_TOKENS))
     forced = forced_num_splits(seq_len, block_n)
     if tiled:
+        grp = max(1, tile_group)
+        groups = math.ceil(tiles / grp)
         if forced is not None:
             n = forced
         else:
             n = max(1, math.ceil(cu_count / max(1, rows)))
             n = min(n, max(1, math.ceil(tiles / MIN_SPLIT_TILES)))
-        split_tiles = math.ceil(tiles / n)
+        n = min(n, groups)
+        split_groups = math.ceil(groups / n)
         if waves is None:
+            per_wave = max(MIN_TILES_PER_WAVE, grp)
             waves = 1
-            while waves < max_waves and 2 * waves * MIN_TILES_PER_WAVE <= split_tiles:
+            while waves < max_waves and 2 * waves * per_wave <= split_groups * grp:
                 waves *= 2
-        cap = MAX_TILES_PER_WAVE * waves
-        if split_tiles > cap:
-            split_tiles = math.ceil(tiles / math.ceil(tiles / cap))
+        cap = MAX_TILES_PER_WAVE // grp * waves
+        if split_groups > cap:
+            split_groups = math.ceil(groups / math.ceil(groups / cap))
+        split_tiles = split_groups * grp
     else:
         if forced is not None:
             split_tiles = math.ceil(tiles / forced)
@@ -235,6 +243,7 @@ def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_bl
     if tiled and waves is not None:
         waves = min(waves, max_waves)
     block_n = resolve_block_n()
+    group = quant_block // TILE_TOKENS if tiled and per_channel else 1
     split_tiles, max_splits, waves = plan_splits(seq_len, rows, block_n, device_cu_count(device), tiled=tiled,
-                                                 waves=waves, max_waves=max_waves)
+                                                 waves=waves, max_waves=max_waves, tile_group=group)
     return tiled, waves, split_tiles, max_splits, block_n

@@ -122,6 +122,18 @@ def test_split_plan_covers_every_tile(clean_env):
                         assert split_tiles <= 64 * waves
                         if fixed:
                             assert waves == fixed
+    # per-channel stores: splits hold whole quant blocks of `grp` tiles, a wave at most 64 tiles
+    for grp in (2, 3, 4, 8, 64):
+        for seq_len in (1, 17, 300, 1000, 4096, 65536):
+            for rows in (1, 8, 256):
+                for fixed in (None, 1, 8):
+                    split_tiles, max_splits, waves = triton_utils.plan_splits(
+                        seq_len, rows, 128, 256, waves=fixed, max_waves=8, tile_group=grp)
+                    tiles = -(-seq_len // 16)
+                    assert split_tiles % grp == 0 and waves in (1, 2, 4, 8)
+                    assert grp * -(-(split_tiles // grp) // waves) <= 64
+                    assert split_tiles * max_splits >= tiles > split_tiles * (max_splits - 1)
+    assert triton_utils.plan_splits(4096, 256, 128, 256, max_waves=8, tile_group=4) == (256, 1, 8)
     plan = triton_utils.plan_splits
     # metric shape: 256 rows on 256 CUs -> one 16-wave workgroup per row, no second launch
     assert plan(4096, 256, 128, 256) == (256, 1, 16)

@@ -64,6 +64,17 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.fs_decode_tiled_path(128, 16, 8) == 1 and lib.fs_decode_tiled_path(128, 24, 24) == 1
     assert lib.fs_decode_tiled_path(128, 4, 4) == 0 and lib.fs_decode_tiled_path(72, 16, 16) == 0
     assert lib.fs_decode_tiled_path(128, 48, 32) == 0 and lib.fs_decode_tiled_path(512, 16, 16) == 0
+    # per-channel stores with 64-token blocks: waves take whole blocks, so a split holds whole
+    # blocks of 4 tiles and a wave at most 64 tiles
+    rc = lib.fs_fused_decode_i8_channel(1, 1, 1, 1, 1, 1, 1, 1, None, 1, 1, 1 << 20, 1, 1, 128, 4096, 64, 64,
+                                        0.1, 30, 9, 8, None)
+    assert rc == _lib.FS_ERR_INVALID and "multiple of quant_block / 16" in lib.fs_last_error().decode()
+    # 48-token blocks: 85 blocks over 4 waves is 22 blocks = 66 tiles for the first wave
+    rc = lib.fs_fused_decode_i8_channel(1, 1, 1, 1, 1, 1, 1, 1, None, 1, None, 0, 1, 1, 128, 4080, 85, 48,
+                                        0.1, 255, 1, 4, None)
+    assert rc == _lib.FS_ERR_INVALID and "<= 64" in lib.fs_last_error().decode()
+    assert lib.fs_decode_tiled_path_channel(128, 64, 64) == 1 and lib.fs_decode_tiled_path_channel(128, 8, 8) == 0
+    assert lib.fs_decode_tiled_path_channel(128, 2048, 2048) == 0  # a block of more than 64 tiles
     # unsupported dtype code in quantize
     rc = lib.fs_quantize_i8(1, 9, 1, 16, 128, 16, 1, 1, 1, None)
     assert rc == _lib.FS_ERR_INVALID

@@ -88,6 +88,8 @@ def test_from_dense_per_channel_pages_bit_exact(layout):
     (2, 4, 300, 128, 16, torch.float16, None, True),
     (2, 4, 300, 128, 64, torch.bfloat16, [300, 17], True),
     (3, 2, 257, 64, 32, torch.float32, [257, 0, 100], True),
+    (2, 4, 500, 128, 48, torch.float16, [500, 97], True),      # 3 tiles per block
+    (1, 4, 2000, 64, 128, torch.float16, [1990], True),        # 8 tiles per block, ragged last block
     (1, 4, 700, 256, 16, torch.float16, None, True),
     (2, 3, 90, 96, 16, torch.float16, [90, 45], True),
     (2, 3, 90, 128, 8, torch.float16, [90, 45], False),   # 8-token blocks: element-wise kernel
@@ -140,3 +142,21 @@ def test_paged_per_channel_split_k(monkeypatch):
     assert st["num_splits"] == 4.0
     ref = oa.paged_quant_attention(np_of(q.float()), from_cache(cache))
     assert_attention_close(got, ref, torch.float16, "per-channel split")
+
+
+@pytest.mark.parametrize("splits", ["1", "3"])
+def test_paged_per_channel_whole_block_waves(monkeypatch, splits):
+    """64-token blocks: waves take whole blocks of 4 tiles; splits of whole blocks, ragged rows."""
+    announce(f"paged per-channel page64 splits={splits}")
+    B, H, S, D = 3, 4, 2048, 128
+    q = randn((B, H, D), 61)
+    k, v = _channel_scaled((B, H, S, D), 62), _channel_scaled((B, H, S, D), 63)
+    lens = torch.tensor([2048, 1000, 77], dtype=torch.int64)
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=64, lengths=lens.to(DEV),
+                                       block_table_pattern="shuffled", layout_seed=9, kv_format="affine_channel")
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", splits)
+    got, st = fa.paged_quant_attention_triton(q.to(DEV), cache, return_stats=True)
+    sync()
+    assert st["tiled_path"] == 1.0 and st["num_splits"] == float(splits)
+    ref = oa.paged_quant_attention(np_of(q.float()), from_cache(cache))
+    assert_attention_close(got, ref, torch.float16, "per-channel whole-block waves")
