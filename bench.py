@@ -53,9 +53,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--layout", default="contiguous", choices=["contiguous", "shuffled", "interleaved"])
-    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "serving", "shapes", "tree"],
+    ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "readbw", "serving", "shapes", "tree"],
                     help="full: the JSON line; paged: only the timed paged steps (for rocprofv3); "
                          "copy: a plain 256 MiB device copy, to calibrate rocprofv3 byte counters; "
+                         "readbw: the library's plain streaming read of 256 MiB (the practical read ceiling); "
                          "serving: only the 64-request serving decode step; shapes: the SHAPES table; "
                          "tree: tree verification for 1-16 draft nodes")
     return ap.parse_args()
@@ -86,6 +87,33 @@ def make_inputs(torch, fa, dev, seed: int, layout: str):
     vq = fa.quantize_int8_per_block(v, PAGE)
     del k, v
     return q, cache, kq, vq
+
+
+STREAM_READ_BYTES = 256 << 20
+STREAM_READ_BLOCKS = 2048
+
+
+def stream_read_ceiling(torch, dev, steps: int = 60) -> dict:
+    """Practical HBM read ceiling: the library's plain streaming-read kernel (`fs_stream_read`,
+    16-byte loads, grid-stride) over 3 rotated 256 MiB buffers, like the decode's rotated
+    inputs; mean of `steps` launches on torch's current stream."""
+
+    from flashspec_amd import _lib
+
+    lib = _lib.require()
+    bufs = [torch.full((STREAM_READ_BYTES,), i + 1, dtype=torch.uint8, device=dev) for i in range(ROTATE)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = _lib.stream_ptr(dev)
+
+    def read(i):
+        _lib.check(lib.fs_stream_read(bufs[i % ROTATE].data_ptr(), STREAM_READ_BYTES, sink.data_ptr(),
+                                      STREAM_READ_BLOCKS, stream))
+
+    ms = time_loop(torch, read, steps, 6)
+    del bufs
+    return {"kernel": "stream_read_kernel", "bytes_per_launch": STREAM_READ_BYTES, "rotated_buffers": ROTATE,
+            "workgroups": STREAM_READ_BLOCKS, "us": round(ms * 1e3, 2),
+            "GBps": round(STREAM_READ_BYTES / (ms * 1e-3) / 1e9, 1)}
 
 
 def time_loop(torch, fn, steps: int, warmup: int) -> float:
@@ -421,6 +449,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.mode == "copy":
         return copy_calibration(torch, args.steps)
+    if args.mode == "readbw":
+        print(json.dumps({"mode": "readbw", **stream_read_ceiling(torch, dev, args.steps)}), flush=True)
+        return 0
     if args.mode == "shapes":
         shapes_bench(torch, fa, dev, min(args.steps, 100), min(args.warmup, 10))
         return 0
@@ -512,6 +543,13 @@ def main() -> int:
         "device": torch.cuda.get_device_name(dev),
     }
     del sets
+    torch.cuda.empty_cache()
+    try:
+        ceiling = stream_read_ceiling(torch, dev)
+        result["stream_read"] = ceiling
+        result["roofline"]["frac_of_stream_read"] = round(achieved / ceiling["GBps"], 4)
+    except Exception as exc:  # reported, never hides the metric line
+        result["stream_read"] = {"error": f"{type(exc).__name__}: {exc}"}
     torch.cuda.empty_cache()
     try:
         result["quantize"] = quantize_bench(torch, fa, dev)

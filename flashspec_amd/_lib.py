@@ -64,6 +64,7 @@ _SIGNATURES = {
          c_int, c_int, c_int, c_void_p],
     ),
     "fs_decode_tiled_path_channel": (c_int, [c_int, c_int, c_int]),
+    "fs_stream_read": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p]),
     "fs_quantize_fp8": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fs_quantize_pages_fp8": (
         c_int,

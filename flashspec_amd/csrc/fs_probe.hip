@@ -1,0 +1,34 @@
+// Measurement helper: a plain streaming read of one device buffer.  Its rate on the same GPU is
+// the practical HBM read ceiling that the decode kernels' reads are compared against (the
+// published 8 TB/s is a peak no read pattern reaches).  No counterpart in the reference.
+#include "fs_common.h"
+
+namespace fs {
+
+// Grid-stride 16-byte loads, one per lane per step.  The XOR of every word read reaches memory
+// only when it equals `magic`, which keeps the loads from being dropped while writing nothing
+// in practice (and, if it ever matches, one word of the caller's `sink`).
+__global__ void __launch_bounds__(256) stream_read_kernel(const uint4* __restrict__ src, int64_t n16,
+                                                          unsigned* sink, unsigned magic) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  unsigned acc = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const uint4 v = src[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == magic) sink[0] = acc;
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" int fs_stream_read(const void* src, int64_t bytes, unsigned* sink, int blocks, void* stream) {
+  if (!src || !sink) return set_error(FS_ERR_INVALID, "null tensor pointer");
+  if (bytes <= 0 || bytes % 16 != 0) return set_error(FS_ERR_INVALID, "bytes must be a positive multiple of 16");
+  if ((uintptr_t)src % 16 != 0) return set_error(FS_ERR_INVALID, "src must be 16-byte aligned");
+  if (blocks <= 0 || blocks > 65536) return set_error(FS_ERR_INVALID, "blocks must be in [1, 65536]");
+  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4*)src,
+                     bytes / 16, sink, 0x9e3779b9u);
+  return check_launch("stream_read_kernel");
+}
