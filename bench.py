@@ -367,7 +367,7 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
     return out
 
 
-TREE_CASES = ((4, (1, 4, 8, 16, 64)), (8, (16,)))  # (requests, draft-node counts)
+TREE_CASES = ((4, (1, 4, 8, 16, 32, 64)), (8, (16, 64)))  # (requests, draft-node counts)
 
 
 def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
@@ -409,7 +409,8 @@ def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
                    "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                    "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
                    "single_query_decode_us": round(dec_ms * 1e3, 2), "vs_decode": round(ms / dec_ms, 3),
-                   "num_splits": st["num_splits"], "waves": st["num_warps"], "mfma_prefix": st["mfma_prefix"]}
+                   "num_splits": st["num_splits"], "waves": st["num_warps"], "mfma_prefix": st["mfma_prefix"],
+                   "nodes_per_workgroup": st["nodes_per_workgroup"]}
             out.append(row)
             print(json.dumps({"mode": "tree", **row}), flush=True)
             del ins

@@ -328,7 +328,7 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
                            heads, D, qk_scale, lane);
 }
 
-template <int DP, typename QT, int QM>
+template <int DP, typename QT, int QM, int NG>
 __global__ void __launch_bounds__(kWave * tree_waves_cap_dp(DP))
 tree_prefix_mfma_kernel(const DecodeParams p) {
   constexpr bool TOK = QM == kQmToken;
@@ -343,12 +343,12 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int W = blockDim.x / kWave;
   const int nq = p.nq;
-  const int groups = (nq + kNodeGroup - 1) / kNodeGroup;
+  const int groups = (nq + NG * kNodeGroup - 1) / (NG * kNodeGroup);
   const TreeUnit u = tree_unit(p, groups, blockIdx.x, gridDim.x);
   const int b = u.b, h = u.h, split = u.split;
-  const int nl = lane & 15;  // node within the group (and token row of the K slice)
+  const int nl = lane & 15;  // node within a 16-node group (and token row of the K slice)
   const int g = lane >> 4;   // lane group: tokens 4g..4g+3, dims of K slice 16(4c+g)+i
-  const int node = u.grp * kNodeGroup + nl;
+  const int node0 = u.grp * NG * kNodeGroup;  // the workgroup's first node; group gi starts at node0 + 16 gi
 
   const int len = row_length(p.lengths, b, p.seq_len);
   const int nsplit = row_splits(len, p.split_tiles);
@@ -388,10 +388,16 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   const float vref = vmax > 0.f ? vmax : 1.f;
   const float inv_vref = 1.f / vref;
 
-  MqQuery<QT, DP> q;
-  const size_t qrow = (((size_t)b * nq + node) * p.heads + h) * D;
-  q.load((const QT*)p.q + (node < nq ? qrow : 0), node < nq, g);
-  const float qmul = q.mul * (TOK ? p.qk_scale : 1.f);
+  // the NG node groups' queries (nodes past nq: zero queries, never written)
+  MqQuery<QT, DP> q[NG];
+  float qmul[NG];
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const int node = node0 + gi * kNodeGroup + nl;
+    const size_t qrow = (((size_t)b * nq + node) * p.heads + h) * D;
+    q[gi].load((const QT*)p.q + (node < nq ? qrow : 0), node < nq, g);
+    qmul[gi] = q[gi].mul * (TOK ? p.qk_scale : 1.f);
+  }
 
   const int8_t* kbase = p.kv[0];
   const int8_t* vbase = p.kv[1];
@@ -422,52 +428,67 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     }
   };
 
-  float m = kNegBig, l = 0.f;
-  f32x4_t acc[J];
+  float m[NG], l[NG];
+  f32x4_t acc[NG][J];
 #pragma unroll
-  for (int jb = 0; jb < J; ++jb) acc[jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int gi = 0; gi < NG; ++gi) {
+    m[gi] = kNegBig;
+    l[gi] = 0.f;
+#pragma unroll
+    for (int jb = 0; jb < J; ++jb) acc[gi][jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
-  // Scores of tile k (4 tokens 4g + r of node l % 16, masked to kNegBig), the tile's value
-  // factors vs / vref and fp16 -(1024 + zv) for those tokens.
-  auto scores = [&](const MqTile<DP, TOK>& t, int k, float (&sc)[4], float (&vfac)[4], f16x4_t& nzv) {
+  // Scores of tile k for each node group (4 tokens 4g + r of node l % 16, masked to kNegBig),
+  // the tile's value factors vs / vref and fp16 -(1024 + zv) for those tokens.  The K bytes are
+  // converted once for all groups.
+  auto scores = [&](const MqTile<DP, TOK>& t, int k, float (&sc)[NG][4], float (&vfac)[4], f16x4_t& nzv) {
     const bool backed = k < nk && off_of(k) >= 0;
     const int token0 = (first + W * k) * kTile + 4 * g;
-    float kmul[4], kzo[4];
+    float ksc[4], kzo[4];
     int vz[4];
     if constexpr (TOK) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        kmul[r] = t.ks[r] * qmul;
+        ksc[r] = t.ks[r];
         kzo[r] = (float)(1024 + t.kz[r]);
         vfac[r] = t.vs[r] * inv_vref;
         vz[r] = t.vz[r];
       }
     } else {
       const int kk = k < nk ? k : 0;
-      const float ks = readlane_f32(my_ks, kk) * qmul, vf = readlane_f32(my_vs, kk) * inv_vref;
+      const float ks = readlane_f32(my_ks, kk), vf = readlane_f32(my_vs, kk) * inv_vref;
       const int vzz = readlane_i32(my_vz, kk);
       const float kz = (float)(1024 + readlane_i32(my_kz, kk));
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        kmul[r] = ks;
+        ksc[r] = ks;
         kzo[r] = kz;
         vfac[r] = vf;
         vz[r] = vzz;
       }
     }
     // S[t = 4g + r][n = l % 16] = sum_d q (1024 + u) - (1024 + zk) * sum_d q
-    f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t sacc[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) sacc[gi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const uint4 raw = t.k[s >> 1];
       const f16x8_t kf = (s & 1) ? k_step_f16(raw.z, raw.w) : k_step_f16(raw.x, raw.y);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.hi[s], sacc, 0, 0, 0);
-      if constexpr (MqQuery<QT, DP>::kLo) sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.lo[s], sacc, 0, 0, 0);
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        sacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q[gi].hi[s], sacc[gi], 0, 0, 0);
+        if constexpr (MqQuery<QT, DP>::kLo)
+          sacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q[gi].lo[s], sacc[gi], 0, 0, 0);
+      }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool ok = backed && token0 + r < len;
-      sc[r] = ok ? fmaf(-kzo[r], q.sum, sacc[r]) * kmul[r] : kNegBig;
+    for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = backed && token0 + r < len;
+        sc[gi][r] = ok ? fmaf(-kzo[r], q[gi].sum, sacc[gi][r]) * (ksc[r] * qmul[gi]) : kNegBig;
+      }
     }
     // -(1024 + z) straight from the integer (exact in fp16 for zero points in [0, 255]); no
     // fp32 step, which the vectorizer would pair into fp32 vector ops
@@ -477,43 +498,47 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
 
   // Tiles k and k + 1 (k + 1 may lie past the wave's tiles: masked): the P.V product runs on
   // the pair as 16x16x32 MFMAs whose 32-token dimension takes tokens 4g..4g+3 of both tiles
-  // from lane group g -- where the Q.K products left their weights.
+  // from lane group g -- where the Q.K products left their weights.  The V bytes are converted
+  // once for all node groups.
   auto consume_pair = [&](const MqTile<DP, TOK>& ta, const MqTile<DP, TOK>& tb, int k) {
-    float sa[4], sb[4], fa[4], fb[4];
+    float sa[NG][4], sb[NG][4], fa[4], fb[4];
     f16x4_t za, zb;
     scores(ta, k, sa, fa, za);
     scores(tb, k + 1, sb, fb, zb);
-    float mt = kNegBig;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mt = fmaxf(mt, fmaxf(sa[r], sb[r]));
-    // The four lanes of a node share its running max m.  Each lane tests its own tokens; only
-    // when one of them exceeds m by the slack does the wave take the max over the node's four
-    // lanes and rescale (all lanes of a node then agree on the new m again).
-    if (__any(mt > m + kRescaleSlack)) {
-      mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-      const float mnew = fmaxf(m, mt);
-      const float alpha = fast_exp2(m - mnew);
-      m = mnew;
-      l *= alpha;
-#pragma unroll
-      for (int jb = 0; jb < J; ++jb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[jb][r] *= alpha;
-      }
-    }
     // weights as fp16 hi + lo (about 22 significant bits, like the fp32 weights of the row
     // kernel): two P.V products per block
-    f16x8_t pw, pl;
+    f16x8_t pw[NG], pl[NG];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float sv = e < 4 ? sa[e] : sb[e - 4];
-      const float pr = sv > kNegBig ? fast_exp2(sv - m) : 0.f;
-      l += pr;
-      const float pv = pr * (e < 4 ? fa[e] : fb[e - 4]);
-      const _Float16 ph = (_Float16)pv;
-      pw[e] = ph;
-      pl[e] = (_Float16)(pv - (float)ph);
+    for (int gi = 0; gi < NG; ++gi) {
+      float mt = kNegBig;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, fmaxf(sa[gi][r], sb[gi][r]));
+      // The four lanes of a node share its running max m.  Each lane tests its own tokens;
+      // only when one of them exceeds m by the slack does the wave take the max over the
+      // node's four lanes and rescale (all lanes of a node then agree on the new m again).
+      if (__any(mt > m[gi] + kRescaleSlack)) {
+        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+        const float mnew = fmaxf(m[gi], mt);
+        const float alpha = fast_exp2(m[gi] - mnew);
+        m[gi] = mnew;
+        l[gi] *= alpha;
+#pragma unroll
+        for (int jb = 0; jb < J; ++jb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[gi][jb][r] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sv = e < 4 ? sa[gi][e] : sb[gi][e - 4];
+        const float pr = sv > kNegBig ? fast_exp2(sv - m[gi]) : 0.f;
+        l[gi] += pr;
+        const float pv = pr * (e < 4 ? fa[e] : fb[e - 4]);
+        const _Float16 ph = (_Float16)pv;
+        pw[gi][e] = ph;
+        pl[gi][e] = (_Float16)(pv - (float)ph);
+      }
     }
 #pragma unroll
     for (int jb = 0; jb < J; ++jb) {
@@ -538,8 +563,11 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
           break;
       }
       const f16x8_t vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pw, acc[jb], 0, 0, 0);
-      acc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, acc[jb], 0, 0, 0);
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        acc[gi][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pw[gi], acc[gi][jb], 0, 0, 0);
+        acc[gi][jb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[gi], acc[gi][jb], 0, 0, 0);
+      }
     }
   };
 
@@ -557,64 +585,71 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     consume_pair(tc, td, k + 2);
   }
 
-  // node totals over the four lane groups; accumulator to value units
-  l += __shfl_xor(l, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
-  float* my_acc = s_acc + (size_t)(w * kNodeGroup + nl) * ROW;
-#pragma unroll
-  for (int jb = 0; jb < J; ++jb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) my_acc[J * (4 * g + r) + jb] = acc[jb][r] * vref;
-  }
-  if (g == 0) {
-    s_ml[2 * (w * kNodeGroup + nl)] = m;
-    s_ml[2 * (w * kNodeGroup + nl) + 1] = l;
-  }
   const int pl = p.fuse_tail ? tree_parent_lane(p.parents, b, nq, lane) : -1;
-  __syncthreads();
-  const int nodes_here = min(kNodeGroup, nq - u.grp * kNodeGroup);
-  for (int e = threadIdx.x; e < nodes_here * D; e += blockDim.x) {
-    const int n = e / D, d = e - n * D;
-    float M = kNegBig;
-    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, s_ml[2 * (ww * kNodeGroup + n)]);
-    float L = 0.f, a = 0.f;
-    for (int ww = 0; ww < W; ++ww) {
-      const float f = fast_exp2(s_ml[2 * (ww * kNodeGroup + n)] - M);
-      L = fmaf(s_ml[2 * (ww * kNodeGroup + n) + 1], f, L);
-      a = fmaf(s_acc[(size_t)(ww * kNodeGroup + n) * ROW + d], f, a);
-    }
-    if (p.fuse_tail) {
-      s_fin[n * ROW + d] = a;
-      if (d == 0) {
-        s_finml[2 * n] = M;
-        s_finml[2 * n + 1] = L;
-      }
-    } else {
-      const int row = (b * nq + u.grp * kNodeGroup + n) * p.heads + h;
-      const size_t ws = (size_t)row * p.max_splits + split;
-      p.part_acc[ws * D + d] = a;
-      if (d == 0) {
-        p.part_ml[2 * ws] = M;
-        p.part_ml[2 * ws + 1] = L;
-      }
-    }
-  }
-  if (!p.fuse_tail) return;
-  // one split: the workgroup finishes its nodes' rows (path tokens, output), wave w taking
-  // nodes w, w + W, ...
-  __syncthreads();
-  for (int n = w; n < nodes_here; n += W) {
-    const int node = u.grp * kNodeGroup + n;
-    const size_t row = ((size_t)b * nq + node) * p.heads + h;
-    float fin[4];
+  // The node groups merge one at a time through the same LDS buffers.
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = lane + c * kWave;
-      fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
+  for (int gi = 0; gi < NG; ++gi) {
+    const int gnode0 = node0 + gi * kNodeGroup;
+    const int nodes_here = min(kNodeGroup, nq - gnode0);  // uniform; <= 0: a group past nq
+    if (gi > 0) __syncthreads();  // the previous group's merge and tail are done with the LDS
+    // node totals over the four lane groups; accumulator to value units
+    float lt = l[gi];
+    lt += __shfl_xor(lt, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+    float* my_acc = s_acc + (size_t)(w * kNodeGroup + nl) * ROW;
+#pragma unroll
+    for (int jb = 0; jb < J; ++jb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) my_acc[J * (4 * g + r) + jb] = acc[gi][jb][r] * vref;
     }
-    tree_path_finish<QT, QT>(s_finml[2 * n], s_finml[2 * n + 1], fin, pl, (const QT*)p.q + row * D,
-                             (const QT*)p.draft_k, (const QT*)p.draft_v, p.parents, (QT*)p.out + row * D, b, node,
-                             h, nq, p.heads, D, p.qk_scale, lane);
+    if (g == 0) {
+      s_ml[2 * (w * kNodeGroup + nl)] = m[gi];
+      s_ml[2 * (w * kNodeGroup + nl) + 1] = lt;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nodes_here * D; e += blockDim.x) {
+      const int n = e / D, d = e - n * D;
+      float M = kNegBig;
+      for (int ww = 0; ww < W; ++ww) M = fmaxf(M, s_ml[2 * (ww * kNodeGroup + n)]);
+      float L = 0.f, a = 0.f;
+      for (int ww = 0; ww < W; ++ww) {
+        const float f = fast_exp2(s_ml[2 * (ww * kNodeGroup + n)] - M);
+        L = fmaf(s_ml[2 * (ww * kNodeGroup + n) + 1], f, L);
+        a = fmaf(s_acc[(size_t)(ww * kNodeGroup + n) * ROW + d], f, a);
+      }
+      if (p.fuse_tail) {
+        s_fin[n * ROW + d] = a;
+        if (d == 0) {
+          s_finml[2 * n] = M;
+          s_finml[2 * n + 1] = L;
+        }
+      } else {
+        const int row = (b * nq + gnode0 + n) * p.heads + h;
+        const size_t ws = (size_t)row * p.max_splits + split;
+        p.part_acc[ws * D + d] = a;
+        if (d == 0) {
+          p.part_ml[2 * ws] = M;
+          p.part_ml[2 * ws + 1] = L;
+        }
+      }
+    }
+    if (!p.fuse_tail) continue;
+    // one split: the workgroup finishes the group's rows (path tokens, output), wave w taking
+    // nodes w, w + W, ...
+    __syncthreads();
+    for (int n = w; n < nodes_here; n += W) {
+      const int node = gnode0 + n;
+      const size_t row = ((size_t)b * nq + node) * p.heads + h;
+      float fin[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = lane + c * kWave;
+        fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
+      }
+      tree_path_finish<QT, QT>(s_finml[2 * n], s_finml[2 * n + 1], fin, pl, (const QT*)p.q + row * D,
+                               (const QT*)p.draft_k, (const QT*)p.draft_v, p.parents, (QT*)p.out + row * D, b, node,
+                               h, nq, p.heads, D, p.qk_scale, lane);
+    }
   }
 }
 
@@ -629,40 +664,87 @@ bool tree_mfma_path(int head_dim, int page_size, int quant_block) {
 
 int tree_mfma_max_waves(int head_dim) { return tree_waves_cap_dp(head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256)); }
 
+// Most draft nodes one wave can serve: two 16-node groups (one K/V conversion for both) on the
+// 64-dim layout and on the 128-dim one with fp16 / bf16 queries and block parameters; 16
+// otherwise.  The other cases have no registers for a second group: at 8 waves per workgroup a
+// lane holds at most 256, and fp32 queries (hi + lo operands), the per-token parameters of
+// token mode and the 256-dim layout would spill.
+int tree_max_nodes_per_wave(int head_dim, bool q_fp32, bool tok) {
+  if (head_dim > 128 || (head_dim > 64 && (q_fp32 || tok))) return kNodeGroup;
+  return 2 * kNodeGroup;
+}
+
+// The library's choice: 32-node workgroups only where 16-node ones would need more than one
+// workgroup per CU (B4 H32, 64 nodes: 84.4 instead of 106.7 us on MI355X); at one round they
+// would halve the grid and push the plan to split the rows, which costs the separate tail
+// launch (B4 H32, 32 nodes: 62.5 instead of 54.0 us per call).
+int tree_nodes_per_wave(int head_dim, int nodes, bool q_fp32, bool tok, int64_t batch_heads, int cu_count) {
+  if (nodes <= kNodeGroup || tree_max_nodes_per_wave(head_dim, q_fp32, tok) == kNodeGroup) return kNodeGroup;
+  const int64_t groups16 = batch_heads * ((nodes + kNodeGroup - 1) / kNodeGroup);
+  return groups16 > cu_count ? 2 * kNodeGroup : kNodeGroup;
+}
+
+template <int DP, typename QT, int NG>
+static void launch_mq_ng(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
+  if (tok) {
+    if constexpr (NG == 1 || DP <= 64)
+      hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken, NG>), grid, block, 0, st, p);
+  } else {
+    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock, NG>), grid, block, 0, st, p);
+  }
+}
+
 template <int DP, typename QT>
-static void launch_mq(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
-  if (tok)
-    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken>), grid, block, 0, st, p);
-  else
-    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock>), grid, block, 0, st, p);
+static void launch_mq(const DecodeParams& p, bool tok, int per_wave, dim3 grid, dim3 block, hipStream_t st) {
+  constexpr bool q_fp32 = std::is_same<QT, float>::value;
+  if constexpr (DP == 64 || (DP == 128 && !q_fp32)) {
+    if (per_wave == 2 * kNodeGroup) {
+      launch_mq_ng<DP, QT, 2>(p, tok, grid, block, st);
+      return;
+    }
+  }
+  launch_mq_ng<DP, QT, 1>(p, tok, grid, block, st);
 }
 
 template <typename QT>
-static void launch_mq_q(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
+static void launch_mq_q(const DecodeParams& p, bool tok, int per_wave, dim3 grid, dim3 block, hipStream_t st) {
   switch (p.head_dim) {
-    case 64: launch_mq<64, QT>(p, tok, grid, block, st); break;
-    case 128: launch_mq<128, QT>(p, tok, grid, block, st); break;
-    default: launch_mq<256, QT>(p, tok, grid, block, st); break;
+    case 64: launch_mq<64, QT>(p, tok, per_wave, grid, block, st); break;
+    case 128: launch_mq<128, QT>(p, tok, per_wave, grid, block, st); break;
+    default: launch_mq<256, QT>(p, tok, per_wave, grid, block, st); break;
   }
 }
 
 // Preconditions checked by the caller: paged store, valid pointers, workspace for rows x
-// max_splits partials, tree_mfma_path() true.
-int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves, hipStream_t st) {
+// max_splits partials, tree_mfma_path() true.  per_wave: draft nodes per workgroup, 16 or 32
+// (0: the library's choice for the current device).
+int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves, int per_wave, hipStream_t st) {
   if (waves < 1 || waves > tree_mfma_max_waves(p.head_dim))
     return set_error(FS_ERR_INVALID, "tree verify: waves_per_block must be in [1, 8] ([1, 4] for head_dim 256)");
   if (p.split_tiles > kMaxTilesPerWave * waves)
     return set_error(FS_ERR_INVALID, "tree verify: split_tiles must be <= 64 * waves_per_block");
-  const int groups = (p.nq + kNodeGroup - 1) / kNodeGroup;
+  const bool tok = p.quant_block == 1;
+  const bool q_fp32 = q_dtype == FS_F32;
+  const int batch_heads = p.rows / p.nq;
+  if (per_wave == 0) {
+    int dev = 0, cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return set_error(FS_ERR_RUNTIME, "tree verify: cannot read the device's CU count");
+    per_wave = tree_nodes_per_wave(p.head_dim, p.nq, q_fp32, tok, batch_heads, cu);
+  } else if (per_wave != kNodeGroup &&
+             (per_wave != 2 * kNodeGroup || tree_max_nodes_per_wave(p.head_dim, q_fp32, tok) != per_wave)) {
+    return set_error(FS_ERR_INVALID, "tree verify: 32-node workgroups need head_dim 64, or head_dim 128 with fp16 / "
+                                     "bf16 queries and quant blocks of 16k tokens");
+  }
+  const int groups = (p.nq + per_wave - 1) / per_wave;
   const int batch = p.rows / (p.heads * p.nq);
   const int64_t units = (int64_t)batch * p.heads * groups * p.max_splits;
   if (units > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "tree verify grid too large");
   const dim3 grid((unsigned)units), block(kWave * waves);
-  const bool tok = p.quant_block == 1;
   switch (q_dtype) {
-    case FS_F32: launch_mq_q<float>(p, tok, grid, block, st); break;
-    case FS_F16: launch_mq_q<__half>(p, tok, grid, block, st); break;
-    case FS_BF16: launch_mq_q<__hip_bfloat16>(p, tok, grid, block, st); break;
+    case FS_F32: launch_mq_q<float>(p, tok, per_wave, grid, block, st); break;
+    case FS_F16: launch_mq_q<__half>(p, tok, per_wave, grid, block, st); break;
+    case FS_BF16: launch_mq_q<__hip_bfloat16>(p, tok, per_wave, grid, block, st); break;
     default: return set_error(FS_ERR_INVALID, "q dtype code must be 0 (f32), 1 (f16) or 2 (bf16)");
   }
   return check_launch("tree_prefix_mfma");
@@ -697,6 +779,11 @@ extern "C" int fs_tree_mfma_path(int head_dim, int page_size, int quant_block) {
   return tree_mfma_path(head_dim, page_size, quant_block) ? 1 : 0;
 }
 
+extern "C" int fs_tree_nodes_per_workgroup(int head_dim, int nodes, int q_dtype, int quant_block, int64_t batch_heads,
+                                           int cu_count) {
+  return tree_nodes_per_wave(head_dim, nodes, q_dtype == FS_F32, quant_block == 1, batch_heads, cu_count);
+}
+
 extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
                                  const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
                                  const int16_t* v_zero, const void* block_table, int table_index_bytes,
@@ -706,10 +793,11 @@ extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_val
                                  int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
                                  int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
                                  void* stream) {
-  if (prefix_kernel < 0 || prefix_kernel > 2)
-    return set_error(FS_ERR_INVALID, "prefix_kernel must be 0 (auto), 1 (row kernel) or 2 (multi-query kernel)");
+  if (prefix_kernel < 0 || prefix_kernel > 4)
+    return set_error(FS_ERR_INVALID, "prefix_kernel must be 0 (auto), 1 (row kernel), 2 (multi-query kernel), "
+                                     "3 or 4 (multi-query kernel with 16- or 32-node workgroups)");
   const bool mq_ok = tree_mfma_path(head_dim, page_size, quant_block);
-  if (prefix_kernel == 2 && !mq_ok)
+  if (prefix_kernel >= 2 && !mq_ok)
     return set_error(FS_ERR_INVALID, "the multi-query tree kernel needs head_dim 64/128/256, pages of 16k tokens "
                                      "and quant blocks of 16k tokens (or 1)");
   const bool mq = mq_ok && prefix_kernel != 1;
@@ -735,7 +823,8 @@ extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_val
     p.draft_k = draft_k;
     p.draft_v = draft_v;
     p.parents = parents;
-    if (int rc = launch_tree_prefix_mfma(p, q_dtype, waves_per_block, st)) return rc;
+    const int per_wave = prefix_kernel == 3 ? kNodeGroup : (prefix_kernel == 4 ? 2 * kNodeGroup : 0);
+    if (int rc = launch_tree_prefix_mfma(p, q_dtype, waves_per_block, per_wave, st)) return rc;
     if (p.fuse_tail) return FS_OK;
   } else if (int rc = launch_paged_rows(p, q_dtype, tiled, waves_per_block, st)) {
     return rc;

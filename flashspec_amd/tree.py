@@ -7,7 +7,8 @@ request b carries N draft nodes in topological order with ``parents[b, n]`` in [
 (n and its ancestors), never to siblings or other branches.  Draft K/V are unquantized.
 
 On GPU, ``fs_tree_verify_i8`` runs a multi-query prefix kernel (one wave reads each prefix
-tile once for 16 nodes, matrix-core products; head_dim 64/128/256, pages of 16k tokens) or,
+tile once for 16 nodes, or 32 for larger trees where registers allow, with matrix-core products;
+head_dim 64/128/256, pages of 16k tokens) or,
 for other stores, the paged decode kernel with one query row per node; a tail merges the
 prefix state with the path tokens (inside the prefix kernel when it runs one split).  On CPU
 the dense tree-mask formulation runs in torch.
@@ -16,6 +17,7 @@ the dense tree-mask formulation runs in torch.
 from __future__ import annotations
 
 import math
+import os
 from collections import OrderedDict
 from typing import Any
 
@@ -25,7 +27,7 @@ import torch
 from . import _lib
 from .paged import PagedKVCache
 from .quant import build_compression_stats, is_per_channel
-from .triton_utils import TREE_NODE_GROUP, device_cu_count, launch_plan, plan_tree_splits
+from .triton_utils import device_cu_count, launch_plan, plan_tree_splits
 
 __all__ = ["tree_verify_attention", "validate_parents", "path_mask", "tree_shape"]
 
@@ -118,8 +120,15 @@ def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
                          "quant blocks of 1 or a multiple of 16 tokens")
     use_mfma = mfma_ok and kernel != "rows"
     if use_mfma:
-        units = batch * heads * math.ceil(nodes / TREE_NODE_GROUP)
-        split_tiles, max_splits, waves = plan_tree_splits(max_seq_len, units, head_dim, device_cu_count(dev))
+        cu = device_cu_count(dev)
+        qcode, qb = _lib.dtype_code(q.dtype), int(kq.block_size)
+        per_wg = int(lib.fs_tree_nodes_per_workgroup(head_dim, nodes, qcode, qb, batch * heads, cu))
+        forced = os.environ.get("FLASHSPEC_TREE_NODES_PER_WG")
+        if forced == "16" or (forced == "32" and nodes > 16 and
+                              lib.fs_tree_nodes_per_workgroup(head_dim, nodes, qcode, qb, batch * heads, 0) == 32):
+            per_wg = int(forced)  # 32 only where a wave has the registers for it
+        units = batch * heads * math.ceil(nodes / per_wg)
+        split_tiles, max_splits, waves = plan_tree_splits(max_seq_len, units, head_dim, cu)
         tiled, block_n = True, 16
     else:
         tiled, waves, split_tiles, max_splits, block_n = launch_plan(max_seq_len, rows, head_dim,
@@ -133,10 +142,11 @@ def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
         table.data_ptr(), table.element_size(), int(table.shape[1]), lengths.data_ptr(), dk_c.data_ptr(),
         dv_c.data_ptr(), _lib.dtype_code(dk_c.dtype), parents_dev.data_ptr(), out.data_ptr(), workspace.data_ptr(),
         ws_bytes, batch, nodes, heads, head_dim, int(kq.values.shape[0]), int(cache.block_size), int(kq.block_size),
-        max_seq_len, 1.0 / math.sqrt(head_dim), split_tiles, max_splits, waves, _KERNELS[kernel] if kernel != "auto"
-        else (2 if use_mfma else 1), _lib.stream_ptr(dev)))
+        max_seq_len, 1.0 / math.sqrt(head_dim), split_tiles, max_splits, waves,
+        (3 if per_wg == 16 else 4) if use_mfma else 1, _lib.stream_ptr(dev)))
     plan = {"num_splits": float(max_splits), "split_tiles": float(split_tiles), "num_warps": float(waves),
-            "block_n": float(block_n), "tiled_path": float(tiled), "mfma_prefix": float(use_mfma)}
+            "block_n": float(block_n), "tiled_path": float(tiled), "mfma_prefix": float(use_mfma),
+            "nodes_per_workgroup": float(per_wg if use_mfma else 1)}
     return out, plan
 
 
@@ -159,7 +169,7 @@ def tree_verify_attention(q: torch.Tensor, cache: PagedKVCache, draft_k: torch.T
     at the first parent outside [-1, own index) (never reading out of bounds).
 
     ``kernel`` picks the GPU prefix kernel: ``"mfma"`` reads each prefix tile once for 16
-    nodes with matrix-core products (head_dim 64/128/256, pages of 16k tokens, quant blocks
+    (or 32) nodes with matrix-core products (head_dim 64/128/256, pages of 16k tokens, quant blocks
     of 1 or 16k tokens), ``"rows"`` runs the paged decode with one query row per node (any
     store), ``"auto"`` the first where it applies.
     """

@@ -186,7 +186,6 @@ def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: 
     return split_tiles, math.ceil(tiles / split_tiles), waves
 
 
-TREE_NODE_GROUP = 16  # draft nodes served by one wave of the multi-query tree kernel
 # One 8-wave workgroup of the multi-query kernel holds a CU (its ~140 registers per lane leave
 # room for 3 waves per SIMD): the plan splits only while the grid fits one workgroup per CU.
 # Measured on MI355X, B4 H32 S4096 D128, 16 nodes: 2 splits (256 workgroups) 33.5 us,
@@ -203,10 +202,12 @@ def tree_max_waves(head_dim: int) -> int:
 def plan_tree_splits(seq_len: int, units: int, head_dim: int, cu_count: int) -> tuple[int, int, int]:
     """``(split_tiles, max_splits, waves_per_block)`` of the multi-query tree kernel.
 
-    ``units`` = batch * heads * ceil(nodes / 16) workgroups per split.  Workgroups of 8 waves
-    (4 for head_dim 256, whose register layout is twice as wide); as many splits as keep the
-    grid within one workgroup per CU, at least two tiles per wave; ``FLASHSPEC_NUM_SPLITS`` /
-    ``FLASHSPEC_NUM_WARPS`` override as for the decode plan.
+    ``units`` = batch * heads * ceil(nodes / per_workgroup) workgroups per split, with
+    ``per_workgroup`` from ``fs_tree_nodes_per_workgroup`` (16, or 32 for trees of more than 16
+    nodes where registers allow).  Workgroups of 8 waves (4 for head_dim 256, whose register
+    layout is twice as wide); as many splits as keep the grid within one workgroup per CU, at
+    least two tiles per wave; ``FLASHSPEC_NUM_SPLITS`` / ``FLASHSPEC_NUM_WARPS`` override as for
+    the decode plan.
     """
 
     tiles = max(1, math.ceil(seq_len / TILE_TOKENS))

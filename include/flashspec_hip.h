@@ -117,9 +117,13 @@ int fs_paged_decode_i8(const void* q, int q_dtype,
  * (b, n, h) row in `workspace`; a tail kernel merges them with the path tokens (fp32 online
  * softmax) and writes `out`.  Prefix kernels (`prefix_kernel`):
  *   1 = the paged decode with one query row per node (any store the decode serves);
- *   2 = the multi-query kernel: one wave reads each 16-token tile once for 16 nodes with
- *       MFMA products (fs_tree_mfma_path() stores; waves_per_block 1/2/4/8, <= 4 for
- *       head_dim 256; split plan over batch*heads*ceil(nodes/16) workgroups per split);
+ *   2 = the multi-query kernel: one wave reads each 16-token tile once for the 16 or 32
+ *       nodes of its workgroup with MFMA products (fs_tree_mfma_path() stores;
+ *       waves_per_block 1/2/4/8, <= 4 for head_dim 256), the node count being
+ *       fs_tree_nodes_per_workgroup() for the current device; split plan over
+ *       batch*heads*ceil(nodes/node count) workgroups per split;
+ *   3, 4 = 2 with 16- or 32-node workgroups (32 where fs_tree_nodes_per_workgroup() can
+ *       return it for some grid; FS_ERR_INVALID otherwise);
  *   0 = 2 where fs_tree_mfma_path() holds, else 1.
  * With the multi-query kernel, one split (max_splits == 1) and drafts in q's dtype, the prefix
  * kernel finishes the rows itself (path tokens and output; no tail launch, workspace unused).
@@ -149,6 +153,18 @@ int fs_tree_verify_i8(const void* q, int q_dtype,
  * page.  No counterpart in the reference (tree verification is not implemented there).
  */
 int fs_tree_mfma_path(int head_dim, int page_size, int quant_block);
+
+/*
+ * Draft nodes one workgroup of the multi-query tree kernel serves (each of its waves reads a
+ * tile once for all of them), as fs_tree_verify_i8 with prefix_kernel 0 or 2 chooses them on a
+ * device of `cu_count` CUs: 32 when a wave has the registers for two 16-node groups (head_dim
+ * 64, or head_dim 128 with fp16 / bf16 queries and quant_block > 1), nodes > 16, and
+ * batch_heads * ceil(nodes / 16) workgroups would exceed cu_count; else 16.  The split plan
+ * counts batch_heads * ceil(nodes / this) workgroups per split.  No counterpart in the
+ * reference.
+ */
+int fs_tree_nodes_per_workgroup(int head_dim, int nodes, int q_dtype, int quant_block, int64_t batch_heads,
+                                int cu_count);
 
 /*
  * Merge the per-split partial states a decode call with max_splits > 1 left in

@@ -75,6 +75,15 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert rc == _lib.FS_ERR_INVALID and "<= 64" in lib.fs_last_error().decode()
     assert lib.fs_decode_tiled_path_channel(128, 64, 64) == 1 and lib.fs_decode_tiled_path_channel(128, 8, 8) == 0
     assert lib.fs_decode_tiled_path_channel(128, 2048, 2048) == 0  # a block of more than 64 tiles
+    # nodes per workgroup of the multi-query tree kernel: 32 where a wave has registers for two
+    # 16-node groups and 16-node workgroups would not fit the CUs in one round
+    npw = lib.fs_tree_nodes_per_workgroup
+    f32, f16, bf16 = 0, 1, 2  # FS_F32, FS_F16, FS_BF16
+    assert npw(128, 16, f16, 16, 128, 256) == 16 and npw(128, 17, f16, 16, 128, 256) == 16
+    assert npw(128, 17, f16, 16, 129, 256) == 32 and npw(128, 64, bf16, 16, 128, 256) == 32
+    assert npw(64, 64, f32, 1, 128, 256) == 32 and npw(128, 32, f16, 16, 128, 256) == 16
+    assert npw(128, 64, f32, 16, 128, 256) == 16 and npw(128, 64, f16, 1, 128, 256) == 16
+    assert npw(256, 64, f16, 16, 128, 256) == 16
     # unsupported dtype code in quantize
     rc = lib.fs_quantize_i8(1, 9, 1, 16, 128, 16, 1, 1, 1, None)
     assert rc == _lib.FS_ERR_INVALID

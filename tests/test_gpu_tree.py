@@ -34,7 +34,7 @@ def _require_gpu(monkeypatch):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     assert _lib.available(), _lib.LOAD_ERROR
-    for key in ("FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_WARPS"):
+    for key in ("FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_WARPS", "FLASHSPEC_TREE_NODES_PER_WG"):
         monkeypatch.delenv(key, raising=False)
 
 
@@ -157,6 +157,7 @@ MFMA_CASES = [
     (2, 4, 333, 256, 3, 32, "symmetric_token", torch.float16, [333, 200]),
     (1, 16, 4096, 64, 16, 16, "affine_block", torch.float32, [4096]),
     (1, 2, 200, 64, 70, 16, "affine_block", torch.float16, [200]),          # > 64 nodes: tail walks memory
+    (2, 4, 1500, 128, 33, 16, "affine_block", torch.bfloat16, [1500, 900]),
 ]
 
 
@@ -200,6 +201,32 @@ def test_tree_mfma_forced_plans(monkeypatch, splits, warps):
     assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, "forced plan")
 
 
+# 32-node workgroups (two 16-node groups per wave), forced where the default plan would pick
+# 16: (B, H, S, D, N, kv_format, q dtype, lengths, splits)
+NG2_CASES = [
+    (1, 4, 700, 128, 17, "affine_block", torch.float16, [700], None),          # one node of the second group
+    (2, 2, 257, 64, 40, "symmetric_token", torch.bfloat16, [257, 16], None),  # a workgroup with an empty group
+    (2, 4, 1500, 128, 33, "affine_block", torch.bfloat16, [1500, 900], "3"),  # split partials, tail kernel
+    (1, 2, 200, 64, 70, "affine_block", torch.float32, [200], "1"),           # fused tail, > 64 nodes
+    (2, 4, 700, 128, 48, "affine_block", torch.bfloat16, [700, 333], "1"),    # fused tail, 1.5 workgroups
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,N,fmt,q_dtype,lengths,splits", NG2_CASES)
+def test_tree_mfma_32_node_workgroups(monkeypatch, B, H, S, D, N, fmt, q_dtype, lengths, splits):
+    announce(f"tree mfma 32-node workgroups B{B} H{H} S{S} D{D} N{N} {fmt} {q_dtype} splits={splits}")
+    monkeypatch.setenv("FLASHSPEC_TREE_NODES_PER_WG", "32")
+    if splits is not None:
+        monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", splits)
+    parents = _random_parents(B, N, S + 3 * N)
+    got, ref, stats = _run(B, H, S, D, N, parents, lengths, kv_format=fmt, q_dtype=q_dtype, draft_dtype=q_dtype,
+                           seed=S + 2 * N, kernel="mfma")
+    assert stats["nodes_per_workgroup"] == 32.0
+    if splits is not None:
+        assert stats["num_splits"] == float(splits)
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), q_dtype, "32-node workgroups")
+
+
 def test_tree_mfma_agrees_with_row_kernel():
     """Both prefix kernels on one input: within the attention tolerance of each other."""
 
@@ -235,7 +262,8 @@ def test_tree_deep_chain_64_nodes():
 
 
 @pytest.mark.parametrize("D,fmt,dtype,N", [(128, "affine_block", torch.float16, 16), (64, "symmetric_token", torch.bfloat16, 40),
-                                          (256, "affine_block", torch.float32, 9), (128, "symmetric_token", torch.float16, 70)])
+                                          (256, "affine_block", torch.float32, 9), (128, "symmetric_token", torch.float16, 70),
+                                          (128, "affine_block", torch.bfloat16, 48)])
 def test_tree_mfma_fused_tail(monkeypatch, D, fmt, dtype, N):
     """One split and drafts in q's dtype: the multi-query kernel finishes the rows itself (its
     LDS-merged prefix state plus the path tokens; > 64 nodes walk parents in memory)."""
