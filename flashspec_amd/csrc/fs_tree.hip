@@ -784,29 +784,33 @@ extern "C" int fs_tree_nodes_per_workgroup(int head_dim, int nodes, int q_dtype,
   return tree_nodes_per_wave(head_dim, nodes, q_dtype == FS_F32, quant_block == 1, batch_heads, cu_count);
 }
 
-extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
-                                 const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
-                                 const int16_t* v_zero, const void* block_table, int table_index_bytes,
-                                 int64_t table_cols, const int64_t* lengths, const void* draft_k, const void* draft_v,
-                                 int draft_dtype, const int64_t* parents, void* out, void* workspace,
-                                 int64_t workspace_bytes, int batch, int nodes, int heads, int head_dim,
-                                 int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
-                                 int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
-                                 void* stream) {
+// Shared by the tree entry points: `vfmt` / `per_channel` name the store's format (INT8 affine
+// blocks or tokens, FP8 E4M3, per-channel INT8).  The multi-query prefix kernel reads the INT8
+// block and token formats; the others run the row-kernel prefix.
+static int tree_verify(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                       const int8_t* v_values, const float* v_scale, const int16_t* v_zero, const void* block_table,
+                       int table_index_bytes, int64_t table_cols, const int64_t* lengths, const void* draft_k,
+                       const void* draft_v, int draft_dtype, const int64_t* parents, void* out, void* workspace,
+                       int64_t workspace_bytes, int batch, int nodes, int heads, int head_dim, int64_t num_pages,
+                       int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
+                       int max_splits, int waves_per_block, int prefix_kernel, void* stream, int vfmt, int per_channel) {
   if (prefix_kernel < 0 || prefix_kernel > 4)
     return set_error(FS_ERR_INVALID, "prefix_kernel must be 0 (auto), 1 (row kernel), 2 (multi-query kernel), "
                                      "3 or 4 (multi-query kernel with 16- or 32-node workgroups)");
-  const bool mq_ok = tree_mfma_path(head_dim, page_size, quant_block);
+  const bool int8_affine = vfmt == kVfInt8 && !per_channel;
+  const bool mq_ok = int8_affine && tree_mfma_path(head_dim, page_size, quant_block);
   if (prefix_kernel >= 2 && !mq_ok)
-    return set_error(FS_ERR_INVALID, "the multi-query tree kernel needs head_dim 64/128/256, pages of 16k tokens "
-                                     "and quant blocks of 16k tokens (or 1)");
+    return set_error(FS_ERR_INVALID, int8_affine ? "the multi-query tree kernel needs head_dim 64/128/256, pages of 16k "
+                                                   "tokens and quant blocks of 16k tokens (or 1)"
+                                                 : "the multi-query tree kernel reads INT8 caches with per-block or "
+                                                   "per-token parameters; use the row kernel (prefix_kernel 1)");
   const bool mq = mq_ok && prefix_kernel != 1;
   DecodeParams p;
   bool tiled = false;
   if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
                             table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, nodes,
                             heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
-                            max_splits, waves_per_block, !mq))
+                            max_splits, waves_per_block, !mq, vfmt, per_channel))
     return rc;
   if (!draft_k || !draft_v || !parents) return set_error(FS_ERR_INVALID, "tree verify: null draft or parents pointer");
   if (draft_dtype != FS_F32 && draft_dtype != FS_F16 && draft_dtype != FS_BF16)
@@ -835,4 +839,48 @@ extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_val
     case FS_BF16: return launch_tree_tail_q<__hip_bfloat16>(p, draft_k, draft_v, draft_dtype, parents, nodes, st);
     default: return set_error(FS_ERR_INVALID, "q dtype code must be 0 (f32), 1 (f16) or 2 (bf16)");
   }
+}
+
+extern "C" int fs_tree_verify_i8(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                 const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                 const int16_t* v_zero, const void* block_table, int table_index_bytes,
+                                 int64_t table_cols, const int64_t* lengths, const void* draft_k, const void* draft_v,
+                                 int draft_dtype, const int64_t* parents, void* out, void* workspace,
+                                 int64_t workspace_bytes, int batch, int nodes, int heads, int head_dim,
+                                 int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
+                                 int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
+                                 void* stream) {
+  return tree_verify(q, q_dtype, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table, table_index_bytes,
+                     table_cols, lengths, draft_k, draft_v, draft_dtype, parents, out, workspace, workspace_bytes, batch,
+                     nodes, heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
+                     max_splits, waves_per_block, prefix_kernel, stream, kVfInt8, 0);
+}
+
+extern "C" int fs_tree_verify_fp8(const void* q, int q_dtype, const uint8_t* k_values, const float* k_scale,
+                                  const uint8_t* v_values, const float* v_scale, const void* block_table,
+                                  int table_index_bytes, int64_t table_cols, const int64_t* lengths,
+                                  const void* draft_k, const void* draft_v, int draft_dtype, const int64_t* parents,
+                                  void* out, void* workspace, int64_t workspace_bytes, int batch, int nodes, int heads,
+                                  int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
+                                  float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                                  int prefix_kernel, void* stream) {
+  return tree_verify(q, q_dtype, (const int8_t*)k_values, k_scale, nullptr, (const int8_t*)v_values, v_scale, nullptr,
+                     block_table, table_index_bytes, table_cols, lengths, draft_k, draft_v, draft_dtype, parents, out,
+                     workspace, workspace_bytes, batch, nodes, heads, head_dim, num_pages, page_size, quant_block,
+                     max_seq_len, sm_scale, split_tiles, max_splits, waves_per_block, prefix_kernel, stream, kVfFp8, 0);
+}
+
+extern "C" int fs_tree_verify_i8_channel(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                         const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                         const int16_t* v_zero, const void* block_table, int table_index_bytes,
+                                         int64_t table_cols, const int64_t* lengths, const void* draft_k,
+                                         const void* draft_v, int draft_dtype, const int64_t* parents, void* out,
+                                         void* workspace, int64_t workspace_bytes, int batch, int nodes, int heads,
+                                         int head_dim, int64_t num_pages, int page_size, int quant_block,
+                                         int max_seq_len, float sm_scale, int split_tiles, int max_splits,
+                                         int waves_per_block, int prefix_kernel, void* stream) {
+  return tree_verify(q, q_dtype, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table, table_index_bytes,
+                     table_cols, lengths, draft_k, draft_v, draft_dtype, parents, out, workspace, workspace_bytes, batch,
+                     nodes, heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
+                     max_splits, waves_per_block, prefix_kernel, stream, kVfInt8, 1);
 }

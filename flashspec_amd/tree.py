@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from .paged import PagedKVCache
-from .quant import build_compression_stats, is_per_channel
+from .quant import build_compression_stats, is_fp8, is_per_channel
 from .triton_utils import device_cu_count, launch_plan, plan_tree_splits
 
 __all__ = ["tree_verify_attention", "validate_parents", "path_mask", "tree_shape"]
@@ -74,10 +74,9 @@ def _validate(q, cache, draft_k, draft_v):
         raise ValueError("need at least one draft node")
     if head_dim > 256:
         raise ValueError("head_dim must be <= 256")
-    if cache.k_quant.values.dtype != torch.int8 or cache.v_quant.values.dtype != torch.int8 or \
-            is_per_channel(cache.k_quant):
-        raise ValueError("tree verification reads INT8 caches with per-block or per-token scales "
-                         "(affine_block or symmetric_token)")
+    kq, vq = cache.k_quant, cache.v_quant
+    if is_fp8(kq) != is_fp8(vq) or is_per_channel(kq) != is_per_channel(vq):
+        raise ValueError("k and v caches must share one KV format")
     return batch, nodes, heads, head_dim
 
 
@@ -114,10 +113,13 @@ def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
     lengths = cache.lengths.to(torch.int64).contiguous()
     rows = batch * nodes * heads
     max_seq_len = int(cache.max_seq_len)
-    mfma_ok = bool(lib.fs_tree_mfma_path(head_dim, int(cache.block_size), int(kq.block_size)))
+    fp8, per_channel = is_fp8(kq), is_per_channel(kq)
+    mfma_ok = not fp8 and not per_channel and bool(lib.fs_tree_mfma_path(head_dim, int(cache.block_size),
+                                                                          int(kq.block_size)))
     if kernel == "mfma" and not mfma_ok:
-        raise ValueError("kernel='mfma' needs head_dim 64/128/256, pages of a multiple of 16 tokens and "
-                         "quant blocks of 1 or a multiple of 16 tokens")
+        raise ValueError("kernel='mfma' needs an INT8 cache with per-block or per-token parameters, head_dim "
+                         "64/128/256, pages of a multiple of 16 tokens and quant blocks of 1 or a multiple of 16 "
+                         "tokens")
     use_mfma = mfma_ok and kernel != "rows"
     if use_mfma:
         cu = device_cu_count(dev)
@@ -132,13 +134,17 @@ def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
         tiled, block_n = True, 16
     else:
         tiled, waves, split_tiles, max_splits, block_n = launch_plan(max_seq_len, rows, head_dim,
-                                                                     int(cache.block_size), int(kq.block_size), dev)
+                                                                     int(cache.block_size), int(kq.block_size), dev,
+                                                                     per_channel=per_channel)
     ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty_like(q_c)
-    _lib.check(lib.fs_tree_verify_i8(
-        q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kq.values.data_ptr(), kq.scale.data_ptr(),
-        kq.zero_point.data_ptr(), vq.values.data_ptr(), vq.scale.data_ptr(), vq.zero_point.data_ptr(),
+    store = ([kq.values.data_ptr(), kq.scale.data_ptr(), vq.values.data_ptr(), vq.scale.data_ptr()] if fp8 else
+             [kq.values.data_ptr(), kq.scale.data_ptr(), kq.zero_point.data_ptr(), vq.values.data_ptr(),
+              vq.scale.data_ptr(), vq.zero_point.data_ptr()])
+    entry = lib.fs_tree_verify_fp8 if fp8 else (lib.fs_tree_verify_i8_channel if per_channel else lib.fs_tree_verify_i8)
+    _lib.check(entry(
+        q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *store,
         table.data_ptr(), table.element_size(), int(table.shape[1]), lengths.data_ptr(), dk_c.data_ptr(),
         dv_c.data_ptr(), _lib.dtype_code(dk_c.dtype), parents_dev.data_ptr(), out.data_ptr(), workspace.data_ptr(),
         ws_bytes, batch, nodes, heads, head_dim, int(kq.values.shape[0]), int(cache.block_size), int(kq.block_size),

@@ -148,6 +148,35 @@ int fs_tree_verify_i8(const void* q, int q_dtype,
                       void* stream);
 
 /*
+ * fs_tree_verify_i8 over an FP8 E4M3 store (fs_quantize_pages_fp8 layout: codes and fp32 scales,
+ * no zero points) and over a per-channel INT8 store (fs_quantize_pages_i8_channel layout: scale /
+ * zero [num_pages, heads, page_size/quant_block, head_dim]).  Both run the row-kernel prefix
+ * (prefix_kernel 0 or 1; 2-4 are rejected: the multi-query kernel reads the INT8 block and
+ * token formats) and the same tail.  Arguments as for fs_tree_verify_i8.  No counterpart in the
+ * reference.
+ */
+int fs_tree_verify_fp8(const void* q, int q_dtype,
+                       const uint8_t* k_values, const float* k_scale,
+                       const uint8_t* v_values, const float* v_scale,
+                       const void* block_table, int table_index_bytes, int64_t table_cols,
+                       const int64_t* lengths, const void* draft_k, const void* draft_v, int draft_dtype,
+                       const int64_t* parents, void* out, void* workspace, int64_t workspace_bytes,
+                       int batch, int nodes, int heads, int head_dim, int64_t num_pages,
+                       int page_size, int quant_block, int max_seq_len, float sm_scale,
+                       int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
+                       void* stream);
+int fs_tree_verify_i8_channel(const void* q, int q_dtype,
+                              const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                              const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                              const void* block_table, int table_index_bytes, int64_t table_cols,
+                              const int64_t* lengths, const void* draft_k, const void* draft_v, int draft_dtype,
+                              const int64_t* parents, void* out, void* workspace, int64_t workspace_bytes,
+                              int batch, int nodes, int heads, int head_dim, int64_t num_pages,
+                              int page_size, int quant_block, int max_seq_len, float sm_scale,
+                              int split_tiles, int max_splits, int waves_per_block, int prefix_kernel,
+                              void* stream);
+
+/*
  * 1 when fs_tree_verify_i8 can run its multi-query prefix kernel on this store: head_dim 64,
  * 128 or 256, page_size a multiple of 16, quant_block 1 or a multiple of 16 dividing the
  * page.  No counterpart in the reference (tree verification is not implemented there).

@@ -89,13 +89,28 @@ def test_tree_verify_matches_oracle(B, H, S, D, N, kind, lengths, kernel):
 
 @pytest.mark.parametrize("page,kv_format,q_dtype", [(8, "affine_block", torch.float16),
                                                     (16, "symmetric_token", torch.bfloat16),
-                                                    (32, "affine_block", torch.float32)])
+                                                    (32, "affine_block", torch.float32),
+                                                    (16, "fp8_block", torch.float16),
+                                                    (32, "fp8_block", torch.bfloat16),
+                                                    (16, "affine_channel", torch.float16),
+                                                    (64, "affine_channel", torch.float32)])
 def test_tree_verify_formats(page, kv_format, q_dtype):
     announce(f"tree verify page{page} {kv_format} {q_dtype}")
     B, H, S, D, N = 2, 4, 260, 128, 6
     parents = _random_parents(B, N, page)
-    got, ref, _ = _run(B, H, S, D, N, parents, [260, 100], page=page, kv_format=kv_format, q_dtype=q_dtype)
+    got, ref, stats = _run(B, H, S, D, N, parents, [260, 100], page=page, kv_format=kv_format, q_dtype=q_dtype)
+    # FP8 and per-channel stores run the row-kernel prefix (the multi-query kernel reads INT8
+    # block / token parameters)
+    assert stats["mfma_prefix"] == float(kv_format in ("affine_block", "symmetric_token") and page % 16 == 0)
     assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), q_dtype, kv_format)
+
+
+@pytest.mark.parametrize("kv_format", ["fp8_block", "affine_channel"])
+def test_tree_mfma_rejects_other_formats(kv_format):
+    announce(f"tree mfma rejects {kv_format}")
+    B, H, S, D, N = 1, 2, 64, 64, 3
+    with pytest.raises(ValueError):
+        _run(B, H, S, D, N, [[-1, 0, 0]], [64], kv_format=kv_format, kernel="mfma")
 
 
 def test_tree_verify_split_rows(monkeypatch):

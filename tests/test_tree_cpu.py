@@ -13,11 +13,12 @@ from oracle import tree as ot
 from tests._helpers import from_cache
 
 
-def _case(B, H, S, D, N, seed, lengths, page=16):
+def _case(B, H, S, D, N, seed, lengths, page=16, kv_format="affine_block"):
     g = torch.Generator().manual_seed(seed)
     k = torch.randn((B, H, S, D), generator=g)
     v = torch.randn((B, H, S, D), generator=g)
-    cache = fa.PagedKVCache.from_dense(k, v, page, lengths=torch.tensor(lengths), block_table_pattern="shuffled")
+    cache = fa.PagedKVCache.from_dense(k, v, page, lengths=torch.tensor(lengths), block_table_pattern="shuffled",
+                                       kv_format=kv_format)
     q = torch.randn((B, N, H, D), generator=g)
     dk = torch.randn((B, N, H, D), generator=g)
     dv = torch.randn((B, N, H, D), generator=g)
@@ -33,6 +34,17 @@ def test_portable_tree_matches_oracle(parents):
     np.testing.assert_allclose(got.numpy(), ref, rtol=1e-5, atol=1e-5)
     assert stats["materializes_dense_kv"] == 1.0 and stats["tree_nodes"] == 5.0
     assert stats["tree_depth"] == float(max(int(m.sum()) for m in ot.path_mask(np.array(parents)).reshape(-1, 5)))
+
+
+@pytest.mark.parametrize("kv_format", ["fp8_block", "affine_channel", "symmetric_token"])
+def test_portable_tree_other_formats(kv_format):
+    """The portable path reads every KV format through the cache's own dequantization."""
+
+    parents = [[-1, 0, 0, 1], [-1, -1, 1, 2]]
+    q, cache, dk, dv = _case(2, 2, 40, 16, 4, 5, [40, 23], kv_format=kv_format)
+    got = fa.tree_verify_attention(q, cache, dk, dv, torch.tensor(parents))
+    ref = ot.tree_verify_attention(q.numpy(), from_cache(cache), dk.numpy(), dv.numpy(), np.array(parents))
+    np.testing.assert_allclose(got.numpy(), ref, rtol=1e-5, atol=1e-5)
 
 
 def test_tree_validation():
