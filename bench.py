@@ -367,7 +367,8 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
     return out
 
 
-TREE_CASES = ((4, (1, 4, 8, 16, 32, 64)), (8, (16, 64)))  # (requests, draft-node counts)
+# (requests, draft-node counts, KV format of the prefix cache)
+TREE_CASES = ((4, (1, 4, 8, 16, 32, 64), "affine_block"), (8, (16, 64), "affine_block"), (4, (16, 64), "fp8_block"))
 
 
 def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
@@ -382,17 +383,18 @@ def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
     g = torch.Generator(device=dev)
     g.manual_seed(13)
     gp = torch.Generator().manual_seed(17)
-    for nb, node_counts in TREE_CASES:
+    for nb, node_counts, kv_format in TREE_CASES:
         caches = []
         for _ in range(ROTATE):
             k = torch.randn((nb, H, S, D), generator=g, device=dev, dtype=torch.float16)
             v = torch.randn((nb, H, S, D), generator=g, device=dev, dtype=torch.float16)
-            caches.append(fa.PagedKVCache.from_dense(k, v, block_size=PAGE))
+            caches.append(fa.PagedKVCache.from_dense(k, v, block_size=PAGE, kv_format=kv_format))
             del k, v
         q1 = [torch.randn((nb, H, D), generator=g, device=dev, dtype=torch.float16) for _ in range(ROTATE)]
         dec_ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(q1[i % ROTATE], caches[i % ROTATE]),
                            steps, warmup)
-        prefix = algorithmic_bytes([S] * nb, H, D, PAGE) - 2 * nb * H * D * 2
+        prefix = algorithmic_bytes([S] * nb, H, D, PAGE, param_bytes=4 if kv_format == "fp8_block" else 6) \
+            - 2 * nb * H * D * 2
         for n in node_counts:
             par = torch.full((nb, n), -1, dtype=torch.int64)
             for j in range(1, n):
@@ -404,7 +406,8 @@ def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
                            steps, warmup)
             _, st = fa.tree_verify_attention(ins[0][0], caches[0], ins[0][1], ins[0][2], par, return_stats=True)
             nbytes = prefix + 4 * nb * n * H * D * 2 + nb * n * 8
-            row = {"workload": f"tree verify B{nb} H{H} S{S} D{D}, {n} draft nodes", "nodes": n,
+            row = {"workload": f"tree verify B{nb} H{H} S{S} D{D} {kv_format}, {n} draft nodes", "nodes": n,
+                   "kv_format": kv_format,
                    "depth": st["tree_depth"], "us_per_call": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
                    "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                    "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),

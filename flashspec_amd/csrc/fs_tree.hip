@@ -74,6 +74,28 @@ __device__ __forceinline__ f16x4_t v_block_f16(uint32_t t0, uint32_t t1, uint32_
   return __builtin_bit_cast(f16x4_t, v) + nz;
 }
 
+// FP8 E4M3 stores (value format kVfFp8): the codes convert exactly to fp16 (3 mantissa bits,
+// exponents 2^-9 .. 2^8), two per v_cvt_scalef32_pk_f16_fp8 with scale 1 (checked against the
+// fp32 conversion on all 256 codes on gfx950), and there is no zero point.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f16x8_t k_step_fp8(uint32_t w0, uint32_t w1) {
+  const f16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+  const f16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+  const f16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+  const f16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+  return f16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Byte `bp` of four tokens' dwords -> fp16 values of tokens 0..3.
+template <int BP>
+__device__ __forceinline__ f16x4_t v_block_fp8(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  constexpr uint32_t sel = (uint32_t)BP | ((uint32_t)(4 + BP) << 8) | 0x0c0c0000u;
+  const f16x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(__builtin_amdgcn_perm(t1, t0, sel), 1.0f, false);
+  const f16x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(__builtin_amdgcn_perm(t3, t2, sel), 1.0f, false);
+  return f16x4_t{lo[0], lo[1], hi[0], hi[1]};
+}
+
 // J bytes of one token row (J = D / 16: 4, 8 or 16).  Plain (cached) loads, unlike the row
 // kernel's non-temporal ones: the node groups of one (request, head) read the same tiles, and
 // measured at 16 and 64 nodes cached loads are 1-4% faster.
@@ -328,10 +350,11 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
                            heads, D, qk_scale, lane);
 }
 
-template <int DP, typename QT, int QM, int NG>
+template <int DP, typename QT, int QM, int NG, int VF>
 __global__ void __launch_bounds__(kWave * tree_waves_cap_dp(DP))
 tree_prefix_mfma_kernel(const DecodeParams p) {
   constexpr bool TOK = QM == kQmToken;
+  constexpr bool ZP = VF == kVfInt8;  // zero points (INT8); FP8 codes are the values
   constexpr int C = DP / 64, J = DP / 16, KS = DP / 32;
   constexpr int ROW = DP + 4;  // padded LDS row (floats)
   __shared__ float s_acc[tree_waves_cap_dp(DP) * kNodeGroup * ROW];
@@ -377,9 +400,11 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
       if (ti.data >= 0) {
         my_off = (int64_t)ti.data * (kTile * D);
         my_ks = p.sc[0][ti.meta] * p.qk_scale;
-        my_kz = p.zp[0][ti.meta];
         my_vs = p.sc[1][ti.meta];
-        my_vz = p.zp[1][ti.meta];
+        if constexpr (ZP) {
+          my_kz = p.zp[0][ti.meta];
+          my_vz = p.zp[1][ti.meta];
+        }
         vmax = my_vs;
       }
     }
@@ -421,9 +446,9 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         t.ks[r] = p.sc[0][tok0 + 4 * g + r];
-        t.kz[r] = p.zp[0][tok0 + 4 * g + r];
         t.vs[r] = p.sc[1][tok0 + 4 * g + r];
-        t.vz[r] = p.zp[1][tok0 + 4 * g + r];
+        t.kz[r] = ZP ? p.zp[0][tok0 + 4 * g + r] : 0;
+        t.vz[r] = ZP ? p.zp[1][tok0 + 4 * g + r] : 0;
       }
     }
   };
@@ -474,7 +499,11 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const uint4 raw = t.k[s >> 1];
-      const f16x8_t kf = (s & 1) ? k_step_f16(raw.z, raw.w) : k_step_f16(raw.x, raw.y);
+      f16x8_t kf;
+      if constexpr (ZP)
+        kf = (s & 1) ? k_step_f16(raw.z, raw.w) : k_step_f16(raw.x, raw.y);
+      else
+        kf = (s & 1) ? k_step_fp8(raw.z, raw.w) : k_step_fp8(raw.x, raw.y);
 #pragma unroll
       for (int gi = 0; gi < NG; ++gi) {
         sacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q[gi].hi[s], sacc[gi], 0, 0, 0);
@@ -487,7 +516,8 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool ok = backed && token0 + r < len;
-        sc[gi][r] = ok ? fmaf(-kzo[r], q[gi].sum, sacc[gi][r]) * (ksc[r] * qmul[gi]) : kNegBig;
+        const float raw_s = ZP ? fmaf(-kzo[r], q[gi].sum, sacc[gi][r]) : sacc[gi][r];
+        sc[gi][r] = ok ? raw_s * (ksc[r] * qmul[gi]) : kNegBig;
       }
     }
     // -(1024 + z) straight from the integer (exact in fp16 for zero points in [0, 255]); no
@@ -544,23 +574,44 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     for (int jb = 0; jb < J; ++jb) {
       const int dw = jb >> 2;
       f16x4_t va, vb;
-      switch (jb & 3) {
-        case 0:
-          va = v_block_f16<0>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
-          vb = v_block_f16<0>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
-          break;
-        case 1:
-          va = v_block_f16<1>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
-          vb = v_block_f16<1>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
-          break;
-        case 2:
-          va = v_block_f16<2>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
-          vb = v_block_f16<2>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
-          break;
-        default:
-          va = v_block_f16<3>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
-          vb = v_block_f16<3>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
-          break;
+      if constexpr (ZP) {
+        switch (jb & 3) {
+          case 0:
+            va = v_block_f16<0>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+            vb = v_block_f16<0>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+            break;
+          case 1:
+            va = v_block_f16<1>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+            vb = v_block_f16<1>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+            break;
+          case 2:
+            va = v_block_f16<2>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+            vb = v_block_f16<2>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+            break;
+          default:
+            va = v_block_f16<3>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw], za);
+            vb = v_block_f16<3>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw], zb);
+            break;
+        }
+      } else {
+        switch (jb & 3) {
+          case 0:
+            va = v_block_fp8<0>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw]);
+            vb = v_block_fp8<0>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw]);
+            break;
+          case 1:
+            va = v_block_fp8<1>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw]);
+            vb = v_block_fp8<1>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw]);
+            break;
+          case 2:
+            va = v_block_fp8<2>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw]);
+            vb = v_block_fp8<2>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw]);
+            break;
+          default:
+            va = v_block_fp8<3>(ta.v[0].w[dw], ta.v[1].w[dw], ta.v[2].w[dw], ta.v[3].w[dw]);
+            vb = v_block_fp8<3>(tb.v[0].w[dw], tb.v[1].w[dw], tb.v[2].w[dw], tb.v[3].w[dw]);
+            break;
+        }
       }
       const f16x8_t vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
@@ -684,14 +735,22 @@ int tree_nodes_per_wave(int head_dim, int nodes, bool q_fp32, bool tok, int64_t 
   return groups16 > cu_count ? 2 * kNodeGroup : kNodeGroup;
 }
 
-template <int DP, typename QT, int NG>
-static void launch_mq_ng(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
+template <int DP, typename QT, int NG, int VF>
+static void launch_mq_vf(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
   if (tok) {
     if constexpr (NG == 1 || DP <= 64)
-      hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken, NG>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken, NG, VF>), grid, block, 0, st, p);
   } else {
-    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock, NG>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock, NG, VF>), grid, block, 0, st, p);
   }
+}
+
+template <int DP, typename QT, int NG>
+static void launch_mq_ng(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
+  if (p.vfmt == kVfFp8)
+    launch_mq_vf<DP, QT, NG, kVfFp8>(p, tok, grid, block, st);
+  else
+    launch_mq_vf<DP, QT, NG, kVfInt8>(p, tok, grid, block, st);
 }
 
 template <int DP, typename QT>
@@ -797,13 +856,13 @@ static int tree_verify(const void* q, int q_dtype, const int8_t* k_values, const
   if (prefix_kernel < 0 || prefix_kernel > 4)
     return set_error(FS_ERR_INVALID, "prefix_kernel must be 0 (auto), 1 (row kernel), 2 (multi-query kernel), "
                                      "3 or 4 (multi-query kernel with 16- or 32-node workgroups)");
-  const bool int8_affine = vfmt == kVfInt8 && !per_channel;
-  const bool mq_ok = int8_affine && tree_mfma_path(head_dim, page_size, quant_block);
+  const bool mq_format = !per_channel;
+  const bool mq_ok = mq_format && tree_mfma_path(head_dim, page_size, quant_block);
   if (prefix_kernel >= 2 && !mq_ok)
-    return set_error(FS_ERR_INVALID, int8_affine ? "the multi-query tree kernel needs head_dim 64/128/256, pages of 16k "
-                                                   "tokens and quant blocks of 16k tokens (or 1)"
-                                                 : "the multi-query tree kernel reads INT8 caches with per-block or "
-                                                   "per-token parameters; use the row kernel (prefix_kernel 1)");
+    return set_error(FS_ERR_INVALID, mq_format ? "the multi-query tree kernel needs head_dim 64/128/256, pages of 16k "
+                                                 "tokens and quant blocks of 16k tokens (or 1)"
+                                               : "the multi-query tree kernel reads per-block or per-token parameters; "
+                                                 "use the row kernel (prefix_kernel 1) for per-channel stores");
   const bool mq = mq_ok && prefix_kernel != 1;
   DecodeParams p;
   bool tiled = false;

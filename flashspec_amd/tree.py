@@ -114,12 +114,10 @@ def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
     rows = batch * nodes * heads
     max_seq_len = int(cache.max_seq_len)
     fp8, per_channel = is_fp8(kq), is_per_channel(kq)
-    mfma_ok = not fp8 and not per_channel and bool(lib.fs_tree_mfma_path(head_dim, int(cache.block_size),
-                                                                          int(kq.block_size)))
+    mfma_ok = not per_channel and bool(lib.fs_tree_mfma_path(head_dim, int(cache.block_size), int(kq.block_size)))
     if kernel == "mfma" and not mfma_ok:
-        raise ValueError("kernel='mfma' needs an INT8 cache with per-block or per-token parameters, head_dim "
-                         "64/128/256, pages of a multiple of 16 tokens and quant blocks of 1 or a multiple of 16 "
-                         "tokens")
+        raise ValueError("kernel='mfma' needs per-block or per-token parameters (INT8 or FP8), head_dim 64/128/256, "
+                         "pages of a multiple of 16 tokens and quant blocks of 1 or a multiple of 16 tokens")
     use_mfma = mfma_ok and kernel != "rows"
     if use_mfma:
         cu = device_cu_count(dev)

@@ -149,11 +149,11 @@ int fs_tree_verify_i8(const void* q, int q_dtype,
 
 /*
  * fs_tree_verify_i8 over an FP8 E4M3 store (fs_quantize_pages_fp8 layout: codes and fp32 scales,
- * no zero points) and over a per-channel INT8 store (fs_quantize_pages_i8_channel layout: scale /
- * zero [num_pages, heads, page_size/quant_block, head_dim]).  Both run the row-kernel prefix
- * (prefix_kernel 0 or 1; 2-4 are rejected: the multi-query kernel reads the INT8 block and
- * token formats) and the same tail.  Arguments as for fs_tree_verify_i8.  No counterpart in the
- * reference.
+ * no zero points; every prefix kernel, the multi-query one converting the codes exactly to its
+ * fp16 operands) and over a per-channel INT8 store (fs_quantize_pages_i8_channel layout: scale /
+ * zero [num_pages, heads, page_size/quant_block, head_dim]; the row-kernel prefix only,
+ * prefix_kernel 0 or 1, 2-4 being rejected).  Arguments as for fs_tree_verify_i8.  No
+ * counterpart in the reference.
  */
 int fs_tree_verify_fp8(const void* q, int q_dtype,
                        const uint8_t* k_values, const float* k_scale,

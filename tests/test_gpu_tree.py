@@ -101,16 +101,40 @@ def test_tree_verify_formats(page, kv_format, q_dtype):
     got, ref, stats = _run(B, H, S, D, N, parents, [260, 100], page=page, kv_format=kv_format, q_dtype=q_dtype)
     # FP8 and per-channel stores run the row-kernel prefix (the multi-query kernel reads INT8
     # block / token parameters)
-    assert stats["mfma_prefix"] == float(kv_format in ("affine_block", "symmetric_token") and page % 16 == 0)
+    assert stats["mfma_prefix"] == float(kv_format != "affine_channel" and page % 16 == 0)
     assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), q_dtype, kv_format)
 
 
-@pytest.mark.parametrize("kv_format", ["fp8_block", "affine_channel"])
-def test_tree_mfma_rejects_other_formats(kv_format):
-    announce(f"tree mfma rejects {kv_format}")
+@pytest.mark.parametrize("D,N", [(128, 12), (64, 40)])
+def test_tree_mfma_fp8_per_token(D, N):
+    """FP8 codes with one scale per token (token mode of the multi-query kernel, no zero points)."""
+
+    announce(f"tree mfma fp8 per token D{D} N{N}")
+    B, H, S, page = 2, 4, 333, 16
+    k, v = randn((B, H, S, D), 81).to(DEV), randn((B, H, S, D), 82).to(DEV)
+    nbps = -(-S // page)
+    pk = fa.PagedKVCache._physical_pages(k, page, None)
+    pv = fa.PagedKVCache._physical_pages(v, page, None)
+    lens = torch.tensor([S, 150], dtype=torch.int64, device=DEV)
+    cache = fa.PagedKVCache(k_quant=fa.quantize_fp8_per_block(pk, 1), v_quant=fa.quantize_fp8_per_block(pv, 1),
+                            block_table=torch.arange(B * nbps, dtype=torch.int64, device=DEV).reshape(B, nbps),
+                            lengths=lens, block_size=page, max_seq_len=S)
+    parents = _random_parents(B, N, 11)
+    q = randn((B, N, H, D), 83).to(DEV)
+    dk, dv = randn((B, N, H, D), 84).to(DEV), randn((B, N, H, D), 85).to(DEV)
+    got, stats = fa.tree_verify_attention(q, cache, dk, dv, torch.tensor(parents), return_stats=True, kernel="mfma")
+    torch.cuda.synchronize(DEV)
+    assert stats["mfma_prefix"] == 1.0
+    ref = ot.tree_verify_attention(np_of(q.cpu().float()), from_cache(cache), np_of(dk.cpu().float()),
+                                   np_of(dv.cpu().float()), parents)
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float16, "fp8 per token")
+
+
+def test_tree_mfma_rejects_per_channel():
+    announce("tree mfma rejects affine_channel")
     B, H, S, D, N = 1, 2, 64, 64, 3
     with pytest.raises(ValueError):
-        _run(B, H, S, D, N, [[-1, 0, 0]], [64], kv_format=kv_format, kernel="mfma")
+        _run(B, H, S, D, N, [[-1, 0, 0]], [64], kv_format="affine_channel", kernel="mfma")
 
 
 def test_tree_verify_split_rows(monkeypatch):
@@ -173,6 +197,9 @@ MFMA_CASES = [
     (1, 16, 4096, 64, 16, 16, "affine_block", torch.float32, [4096]),
     (1, 2, 200, 64, 70, 16, "affine_block", torch.float16, [200]),          # > 64 nodes: tail walks memory
     (2, 4, 1500, 128, 33, 16, "affine_block", torch.bfloat16, [1500, 900]),
+    (2, 4, 600, 128, 16, 16, "fp8_block", torch.float16, [600, 250]),         # FP8 codes as fp16 operands
+    (1, 4, 300, 64, 20, 32, "fp8_block", torch.bfloat16, [300]),
+    (2, 2, 400, 256, 6, 16, "fp8_block", torch.float32, [400, 7]),
 ]
 
 
@@ -224,6 +251,7 @@ NG2_CASES = [
     (2, 4, 1500, 128, 33, "affine_block", torch.bfloat16, [1500, 900], "3"),  # split partials, tail kernel
     (1, 2, 200, 64, 70, "affine_block", torch.float32, [200], "1"),           # fused tail, > 64 nodes
     (2, 4, 700, 128, 48, "affine_block", torch.bfloat16, [700, 333], "1"),    # fused tail, 1.5 workgroups
+    (2, 4, 900, 128, 40, "fp8_block", torch.float16, [900, 512], None),       # FP8, two groups per wave
 ]
 
 
