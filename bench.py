@@ -263,7 +263,9 @@ SHAPES = [
     ("head_dim_192", 8, 32, 4096, 192, 16, 16, "float16", None),
     ("block_8", 8, 32, 4096, 128, 8, 8, "float16", None),
     ("page_16_quant_8", 8, 32, 4096, 128, 16, 8, "float16", None),
-    ("head_dim_40_generic", 8, 32, 4096, 40, 16, 16, "float16", None),
+    ("head_dim_40", 8, 32, 4096, 40, 16, 16, "float16", None),
+    ("head_dim_120", 8, 32, 4096, 120, 16, 16, "float16", None),
+    ("head_dim_36_generic", 8, 32, 4096, 36, 16, 16, "float16", None),
     ("batch_1_splitk", 1, 32, 16384, 128, 16, 16, "float16", None),
     ("c1_symmetric_per_token", 4, 32, 2048, 128, 16, 1, "float16", None),
     ("c2_symmetric_per_token", 8, 32, 4096, 128, 16, 1, "float16", None),

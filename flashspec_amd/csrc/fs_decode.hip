@@ -112,6 +112,11 @@ struct QSliceF {
 #pragma unroll
     for (int e = 0; e < 16; ++e) q[e] = to_f32(qp[e]);
   }
+  // the first 8 dims only (the lane holding a head_dim's last 8 dims); the rest zero
+  __device__ __forceinline__ void load8(const QT* qp) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) q[e] = e < 8 ? to_f32(qp[e]) : 0.f;
+  }
   __device__ __forceinline__ void clear() {
 #pragma unroll
     for (int e = 0; e < 16; ++e) q[e] = 0.f;
@@ -136,18 +141,25 @@ struct QSlice<__half> {
   static constexpr float kOffset = 1024.f;  // dot16 returns sum q*(1024+u)
   uint32_t qp[8];  // (q0,q2),(q1,q3),(q4,q6),(q5,q7),...
   float qsum_part;
+  template <int N = 16>
   __device__ __forceinline__ void load(const __half* q) {
     const uint16_t* h = (const uint16_t*)q;
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      qp[2 * k] = (uint32_t)h[4 * k] | ((uint32_t)h[4 * k + 2] << 16);
-      qp[2 * k + 1] = (uint32_t)h[4 * k + 1] | ((uint32_t)h[4 * k + 3] << 16);
+      if (4 * k < N) {
+        qp[2 * k] = (uint32_t)h[4 * k] | ((uint32_t)h[4 * k + 2] << 16);
+        qp[2 * k + 1] = (uint32_t)h[4 * k + 1] | ((uint32_t)h[4 * k + 3] << 16);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) s += __half2float(q[4 * k + c]);
+        for (int c = 0; c < 4; ++c) s += __half2float(q[4 * k + c]);
+      } else {
+        qp[2 * k] = qp[2 * k + 1] = 0u;
+      }
     }
     qsum_part = s;
   }
+  // the first 8 dims only (the lane holding a head_dim's last 8 dims); the rest zero
+  __device__ __forceinline__ void load8(const __half* q) { load<8>(q); }
   __device__ __forceinline__ void clear() {
 #pragma unroll
     for (int k = 0; k < 8; ++k) qp[k] = 0u;
@@ -428,7 +440,8 @@ template <int DP, typename QT, bool PAGED, int QM, int VF>
 __global__ void __launch_bounds__(kWave * max_tiled_waves(DP, QM))
 decode_rows_kernel(const DecodeParams p) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
-  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken, CHB = QM == kQmChannelBlocks;
+  constexpr bool T8 = QM == kQmBlockTail8 || QM == kQmTokenTail8;  // head_dim an odd multiple of 8
+  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken || QM == kQmTokenTail8, CHB = QM == kQmChannelBlocks;
   constexpr bool CH = QM == kQmChannel || CHB;
   __shared__ float s_acc[kMaxWaves * DP];
   __shared__ float s_ml[2 * kMaxWaves];
@@ -524,11 +537,17 @@ decode_rows_kernel(const DecodeParams p) {
   const int j = lane % LPT;  // dim slice [16j, 16j+16)
   const int g = lane / LPT;  // token row within a load
   const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
-  const int lane_off = g * D + (active ? 16 * j : 0);
+  // T8: the lane whose dims [16j, 16j + 16) pass the row end (D = 16j + 8) loads the row's last
+  // 16 bytes, [D - 16, D), and keeps their upper half as its dims 16j .. 16j + 7
+  const bool straddle = T8 && active && 16 * j + 16 > D;
+  const int col = active ? (straddle ? D - 16 : 16 * j) : 0;
+  const int lane_off = g * D + col;
   const int rstride = RPL * D;
   using QS = typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>, QSlice<QT>>::type;
   QS q;
-  if (active)
+  if (straddle)
+    q.load8((const QT*)p.q + (size_t)row * D + 16 * j);
+  else if (active)
     q.load((const QT*)p.q + (size_t)row * D + 16 * j);
   else
     q.clear();
@@ -568,9 +587,18 @@ decode_rows_kernel(const DecodeParams p) {
     if constexpr (SUB)
       load_tile_sub<DP>(t, kbase, vbase, base_of(k), base1_of(k), D, g, active ? 16 * j : 0);
     else if constexpr (TOK)
-      load_tile_tok<DP, VF == kVfInt8>(t, p, kbase, vbase, base_of(k), avail_of(k), D, g, active ? 16 * j : 0);
+      load_tile_tok<DP, VF == kVfInt8>(t, p, kbase, vbase, base_of(k), avail_of(k), D, g, col);
     else
       load_tile<DP>(t, kbase, vbase, base_of(k), D, lane_off, rstride);
+    if constexpr (T8) {
+      if (straddle) {
+#pragma unroll
+        for (int r = 0; r < LPTILE; ++r) {
+          t.k[r] = make_uint4(t.k[r].z, t.k[r].w, 0u, 0u);
+          t.v[r] = make_uint4(t.v[r].z, t.v[r].w, 0u, 0u);
+        }
+      }
+    }
   };
   auto consume = [&](const TileRegs<DP>& t, int k) {
     RowMeta<LPTILE> rm;
@@ -853,7 +881,12 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
 // one parameter set per token (quant block 1) on contiguous rows or pages of 16k tokens.
 // Per-channel stores take the tiled path with quant blocks of a multiple of 16 tokens.
 static bool tiled_path(int head_dim, int page_size, int quant_block, bool per_channel = false) {
-  if (head_dim < 16 || head_dim > 256 || head_dim % 16 != 0 || page_size <= 0) return false;
+  if (head_dim < 16 || head_dim > 256 || head_dim % 8 != 0 || page_size <= 0) return false;
+  if (head_dim % 16 != 0) {  // an odd multiple of 8: block and per-token parameters only
+    if (head_dim < 24 || per_channel) return false;
+    if (quant_block == 1) return page_size == 1 || page_size % kTile == 0;
+    return quant_block % kTile == 0 && page_size % quant_block == 0;
+  }
   if (per_channel)  // a wave holds at least one whole quant block: at most 64 tiles
     return quant_block > 0 && quant_block % kTile == 0 && quant_block <= kTile * kMaxTilesPerWave &&
            page_size % quant_block == 0;
@@ -902,10 +935,14 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
       launch_tiled<QT, PAGED, kQmChannelBlocks>(p, grid, block, st);
     else if (p.per_channel)
       launch_tiled<QT, PAGED, kQmChannel>(p, grid, block, st);
+    else if (p.quant_block == 1 && p.head_dim % 16 != 0)
+      launch_tiled<QT, PAGED, kQmTokenTail8>(p, grid, block, st);
     else if (p.quant_block == 1)
       launch_tiled<QT, PAGED, kQmToken>(p, grid, block, st);
     else if (p.quant_block % kTile != 0)
       launch_tiled<QT, PAGED, kQmSub>(p, grid, block, st);
+    else if (p.head_dim % 16 != 0)
+      launch_tiled<QT, PAGED, kQmBlockTail8>(p, grid, block, st);
     else
       launch_tiled<QT, PAGED, kQmBlock>(p, grid, block, st);
   } else {

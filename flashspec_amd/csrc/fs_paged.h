@@ -18,6 +18,10 @@ enum QuantMode : int {
   kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
   kQmChannel = 3,  // per quant block (a multiple of 16 tokens) one entry per channel
   kQmChannelBlocks = 4,  // kQmChannel with quant blocks of >= 2 tiles: waves take whole blocks
+  // kQmBlock / kQmToken for a head_dim that is an odd multiple of 8 (>= 24): the lane whose 16
+  // dims straddle the row end loads the row's last 16 bytes and keeps their upper half
+  kQmBlockTail8 = 5,
+  kQmTokenTail8 = 6,
 };
 
 // Value format of the K/V store: affine INT8 (values int8 = u - 128, scale, zero point) or FP8

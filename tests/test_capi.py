@@ -62,7 +62,11 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.fs_decode_tiled_path(128, 16, 16) == 1 and lib.fs_decode_tiled_path(128, 32, 16) == 1
     assert lib.fs_decode_tiled_path(48, 16, 16) == 1 and lib.fs_decode_tiled_path(96, 32, 32) == 1
     assert lib.fs_decode_tiled_path(128, 16, 8) == 1 and lib.fs_decode_tiled_path(128, 24, 24) == 1
-    assert lib.fs_decode_tiled_path(128, 4, 4) == 0 and lib.fs_decode_tiled_path(72, 16, 16) == 0
+    assert lib.fs_decode_tiled_path(128, 4, 4) == 0 and lib.fs_decode_tiled_path(68, 16, 16) == 0
+    # head_dim an odd multiple of 8 (>= 24): block and per-token parameters on the tiled path
+    assert lib.fs_decode_tiled_path(72, 16, 16) == 1 and lib.fs_decode_tiled_path(24, 16, 1) == 1
+    assert lib.fs_decode_tiled_path(8, 16, 16) == 0 and lib.fs_decode_tiled_path(72, 8, 8) == 0
+    assert lib.fs_decode_tiled_path_channel(72, 16, 16) == 0
     assert lib.fs_decode_tiled_path(128, 48, 32) == 0 and lib.fs_decode_tiled_path(512, 16, 16) == 0
     # per-channel stores with 64-token blocks: waves take whole blocks, so a split holds whole
     # blocks of 4 tiles and a wave at most 64 tiles

@@ -150,6 +150,7 @@ def _sym_fused_case(B, H, S, D, seed, q_dtype):
     (2, 2, 77, 64, torch.bfloat16, [77, 5]),
     (1, 2, 300, 256, torch.float16, None),
     (2, 3, 50, 96, torch.float32, [50, 17]),
+    (2, 3, 120, 104, torch.float16, [120, 64]),     # head_dim 104: the straddling lane in token mode
 ])
 def test_fused_symmetric_per_token_matches_oracle(B, H, S, D, q_dtype, lengths):
     announce(f"fused symmetric per-token B{B} H{H} S{S} D{D} {q_dtype} lengths={lengths}")
@@ -345,7 +346,11 @@ def _fused_case(B, H, S, D, bs, seed, q_dtype=torch.float16, lengths=None):
     (2, 3, 200, 64, 8, torch.float16, [200, 99]),         # 8-token quant blocks (sub-tiles), 64-dim layout
     (2, 4, 301, 128, 8, torch.float16, [301, 150]),       # 8-token quant blocks, 128-dim layout
     (1, 2, 90, 256, 24, torch.bfloat16, [90]),            # 24-token quant blocks, 256-dim layout
-    (1, 2, 100, 40, 16, torch.float16, [100]),            # generic path: head_dim 40
+    (1, 2, 100, 40, 16, torch.float16, [100]),            # head_dim 40: an odd multiple of 8 (straddling lane)
+    (2, 3, 333, 120, 16, torch.bfloat16, [333, 200]),     # head_dim 120 on the 128-dim layout
+    (1, 2, 260, 248, 32, torch.float32, None),            # head_dim 248 on the 256-dim layout
+    (2, 2, 1500, 88, 16, torch.float16, [1500, 700]),     # head_dim 88, split-K
+    (2, 2, 90, 36, 16, torch.float16, [90, 31]),          # generic path: head_dim 36
 ])
 def test_fused_attention_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     announce(f"fused B{B} H{H} S{S} D{D} bs{bs} {q_dtype} lengths={lengths}")
@@ -399,7 +404,9 @@ def _paged_case(B, H, S, D, page, seed, layout="contiguous", lengths=None, q_dty
     (2, 3, 50, 48, 16, "shuffled", [50, 3]),              # head_dim 48 on the 64-dim layout
     (2, 3, 300, 96, 32, "shuffled", [300, 45]),           # head_dim 96, page = quant block 32
     (2, 2, 200, 112, 64, "interleaved", [200, 64]),       # head_dim 112, page 64
-    (2, 2, 50, 24, 16, "contiguous", [50, 9]),            # generic path: head_dim 24
+    (2, 2, 50, 24, 16, "contiguous", [50, 9]),            # head_dim 24: the straddling lane loads bytes 8..23
+    (2, 3, 300, 72, 32, "shuffled", [300, 45]),           # head_dim 72, two tiles per page
+    (2, 2, 60, 20, 16, "interleaved", [60, 13]),          # generic path: head_dim 20
     (3, 4, 200, 128, 8, "shuffled", [200, 17, 9]),        # 8-token pages: two pages per tile
     (2, 2, 100, 64, 8, "interleaved", [100, 8]),          # 8-token pages, 64-dim layout
     (2, 3, 150, 96, 24, "shuffled", [150, 50]),           # 24-token pages
