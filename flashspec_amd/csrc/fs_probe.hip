@@ -1,19 +1,22 @@
 // Measurement helper: a plain streaming read of one device buffer.  Its rate on the same GPU is
 // the practical HBM read ceiling that the decode kernels' reads are compared against (the
 // published 8 TB/s is a peak no read pattern reaches).  No counterpart in the reference.
-#include "fs_common.h"
+#include "fs_paged.h"
 
 namespace fs {
 
-// Grid-stride 16-byte loads, one per lane per step.  The XOR of every word read reaches memory
-// only when it equals `magic`, which keeps the loads from being dropped while writing nothing
-// in practice (and, if it ever matches, one word of the caller's `sink`).
+// Grid-stride non-temporal 16-byte loads, one per lane per step: the fastest plain read
+// measured on MI355X (256 MiB, 2048 workgroups of 256 lanes: 7.08 TB/s against 6.4 TB/s with
+// cached loads; 2 loads in flight per lane or 512/1024-lane workgroups were no faster).  The
+// XOR of every word read reaches memory only when it equals `magic`, which keeps the loads from
+// being dropped while writing nothing in practice (and, if it ever matches, one word of the
+// caller's `sink`).
 __global__ void __launch_bounds__(256) stream_read_kernel(const uint4* __restrict__ src, int64_t n16,
                                                           unsigned* sink, unsigned magic) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   unsigned acc = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
-    const uint4 v = src[i];
+    const uint4 v = stream_load(src + i);
     acc ^= v.x ^ v.y ^ v.z ^ v.w;
   }
   if (acc == magic) sink[0] = acc;

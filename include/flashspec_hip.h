@@ -361,7 +361,7 @@ int fs_append_tokens_i8(const void* k_new, const void* v_new, int src_dtype,
 
 /* Measurement helper with no counterpart in the reference: one plain streaming read of
  * `bytes` (a positive multiple of 16, `src` 16-byte aligned) by `blocks` workgroups of 256
- * lanes, 16-byte loads in a grid-stride loop.  Its rate is the practical HBM read ceiling that
+ * lanes, non-temporal 16-byte loads in a grid-stride loop (the decode kernels' load form).  Its rate is the practical HBM read ceiling that
  * bench.py sets beside the decode kernel's; `sink` (4 bytes of device memory) is written only
  * if the XOR of everything read matches a fixed word. */
 int fs_stream_read(const void* src, int64_t bytes, unsigned* sink, int blocks, void* stream);
