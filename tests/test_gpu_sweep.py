@@ -1,4 +1,4 @@
-"""Seeded randomized parity sweep of paged decode against the CPU oracle.
+"""Seeded randomized parity sweeps of paged and fused decode and of tree verification against the CPU oracle.
 
 Each case draws batch, heads, head_dim, page size, KV format, query dtype, page layout and
 ragged lengths (empty and one-token rows included) from its own seed, so the hand-picked
@@ -37,7 +37,7 @@ def _require_gpu(monkeypatch):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     assert _lib.available(), _lib.LOAD_ERROR
-    for key in ("FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_WARPS"):
+    for key in ("FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_WARPS", "FLASHSPEC_TREE_NODES_PER_WG"):
         monkeypatch.delenv(key, raising=False)
 
 
@@ -108,3 +108,46 @@ def test_fused_decode_random_sweep(monkeypatch, seed):
     if empty:
         assert (got[empty] == 0).all(), "empty rows must be zero"
     assert_attention_close(got[keep], ref[keep], c["q_dtype"], f"fused sweep seed {seed}")
+
+
+def _draw_tree(seed: int) -> dict:
+    r = np.random.default_rng(7000 + seed)
+    B, H = int(r.integers(1, 4)), int(r.integers(1, 5))
+    S = int(r.integers(1, 500))
+    lengths = [S] + [int(r.integers(0, S + 1)) for _ in range(B - 1)]
+    N = int(r.choice([1, 3, 16, 17, 31, 33, 48, 64, 70]))
+    parents = np.full((B, N), -1, dtype=np.int64)
+    for n in range(1, N):
+        parents[:, n] = r.integers(-1, n, size=B)
+    return dict(B=B, H=H, S=S, D=int(r.choice((64, 96, 128, 256))), N=N, page=int(r.choice((16, 32, 64))),
+                fmt=str(r.choice(FORMATS)), q_dtype=QDTYPES[int(r.integers(0, 3))], lengths=lengths,
+                parents=parents, kernel=str(r.choice(("auto", "rows"))), per_wg=[None, "32"][int(r.integers(0, 2))],
+                splits=[None, "1", "3"][int(r.integers(0, 3))])
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_tree_verify_random_sweep(monkeypatch, seed):
+    from oracle import tree as ot
+
+    c = _draw_tree(seed)
+    print(f"[gpu case] tree sweep seed={seed} { {k: v for k, v in c.items() if k != 'parents'} }", flush=True)
+    sys.stdout.flush()
+    if c["splits"] is not None:
+        monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", c["splits"])
+        monkeypatch.setenv("FLASHSPEC_BLOCK_N", "16")
+    if c["per_wg"] is not None:
+        monkeypatch.setenv("FLASHSPEC_TREE_NODES_PER_WG", c["per_wg"])
+    B, H, S, D, N = c["B"], c["H"], c["S"], c["D"], c["N"]
+    q = randn((B, N, H, D), 13 * seed + 1, c["q_dtype"])
+    k, v = randn((B, H, S, D), 13 * seed + 2), randn((B, H, S, D), 13 * seed + 3)
+    dk = randn((B, N, H, D), 13 * seed + 4, torch.float32).to(c["q_dtype"])
+    dv = randn((B, N, H, D), 13 * seed + 5, torch.float32).to(c["q_dtype"])
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=c["page"],
+                                       lengths=torch.tensor(c["lengths"]).to(DEV), block_table_pattern="shuffled",
+                                       layout_seed=seed, kv_format=c["fmt"])
+    got = fa.tree_verify_attention(q.to(DEV), cache, dk.to(DEV), dv.to(DEV), torch.tensor(c["parents"]),
+                                   kernel=c["kernel"])
+    torch.cuda.synchronize(DEV)
+    ref = ot.tree_verify_attention(np_of(q.float()), from_cache(cache), np_of(dk.float()), np_of(dv.float()),
+                                   c["parents"])
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), c["q_dtype"], f"tree sweep {seed}")
