@@ -50,7 +50,7 @@ def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
-    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--layout", default="contiguous", choices=["contiguous", "shuffled", "interleaved"])
     ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "readbw", "serving", "shapes", "tree"],
@@ -116,9 +116,31 @@ def stream_read_ceiling(torch, dev, steps: int = 60) -> dict:
             "GBps": round(STREAM_READ_BYTES / (ms * 1e-3) / 1e9, 1)}
 
 
-def time_loop(torch, fn, steps: int, warmup: int) -> float:
-    """Mean ms per call over `steps` calls bracketed by synchronize + events."""
+# Untimed calls of the step itself, for at least this long, before the counted warm-up: the
+# GPU's clocks take tens of milliseconds of sustained load to settle.  Measured at the metric
+# shape on one box, the first timed loop read 49.2-49.9 us after 30 warm-up steps (1.4 ms)
+# and 46.8-47.0 us after 1000 or 3000.
+SETTLE_S = 0.1
 
+
+def settle(torch, fn, seconds: float = SETTLE_S) -> int:
+    """Calls fn(i) in batches of 20 until `seconds` of wall time have passed; returns the count."""
+
+    torch.cuda.synchronize()
+    t0, n = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn(n)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
+def time_loop(torch, fn, steps: int, warmup: int) -> float:
+    """Mean ms per call over `steps` calls bracketed by synchronize + events, after `settle`
+    and `warmup` untimed calls."""
+
+    settle(torch, fn)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -196,6 +218,8 @@ def serving_step_bench(torch, fa, dev, steps: int, warmup: int) -> dict:
     qs = [torch.randn((SERVE_B, H, D), generator=gd, device=dev, dtype=torch.float16) for _ in range(n_in)]
     ks = [torch.randn((SERVE_B, H, 1, D), generator=gd, device=dev, dtype=torch.float16) for _ in range(n_in)]
     vs = [torch.randn((SERVE_B, H, 1, D), generator=gd, device=dev, dtype=torch.float16) for _ in range(n_in)]
+    # settle the clocks with attention-only calls: a step appends, so it cannot repeat freely
+    settle(torch, lambda i: batch.attend(qs[i % n_in]))
     for i in range(warmup):
         batch.step(qs[i % n_in], ks[i % n_in], vs[i % n_in])
     torch.cuda.synchronize()
@@ -511,6 +535,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s_per_timed_loop": SETTLE_S,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(ms * 1e3, 2),
         "pct_of_peak": round(100.0 * value / PEAK_GBPS, 1),
