@@ -274,6 +274,7 @@ def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
 # "channel" = per-channel affine INT8 (quantize_int8_per_channel).
 SHAPES = [
     ("metric", 8, 32, 4096, 128, 16, 16, "float16", None),
+    ("c1_affine", 4, 32, 2048, 128, 16, 16, "float16", None),
     ("c3_s2048", 8, 32, 2048, 128, 16, 16, "float16", None),
     ("c4_descending_tail", 16, 32, 4096, 128, 16, 16, "float16", [4096 - 256 * i - 7 for i in range(16)]),
     ("head_dim_64", 8, 32, 4096, 64, 16, 16, "float16", None),

@@ -11,6 +11,7 @@ fp32 log-sum-exp combine.
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Any
 
 import torch
@@ -21,6 +22,8 @@ from .quant import (FP8_DTYPE, QuantizedTensor, build_compression_stats, estimat
 from .triton_utils import (
     dispatch_triton_or_fallback,
     launch_plan,
+    layout_checked,
+    remember_layout,
     resolve_block_n as _resolve_block_n,
     resolve_num_warps as _resolve_num_warps,
     validate_decode_query,
@@ -98,9 +101,17 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
                                         ) -> torch.Tensor | tuple[torch.Tensor, dict[str, float]]:
     """Launch the HIP fused kernel (replaces triton_fused.py:604-761); no dense K/V is built."""
 
-    _validate_triton_fused_inputs(q, k_quant, v_quant, lengths)
-    lib = _lib.require()
     dev = q.device
+    # the memo lives on k_quant; v_quant and lengths enter by identity (a weak reference, so a
+    # recycled id never matches) and data pointer
+    memo_key = (q.shape, q.dtype, dev, id(v_quant), k_quant.values.data_ptr(), v_quant.values.data_ptr(),
+                None if lengths is None else (lengths.shape, lengths.device, lengths.dtype))
+    memo = k_quant.__dict__.get("_fs_v_ref")
+    if not (layout_checked(k_quant, memo_key) and memo is not None and memo() is v_quant):
+        _validate_triton_fused_inputs(q, k_quant, v_quant, lengths)
+        remember_layout(k_quant, memo_key)
+        object.__setattr__(k_quant, "_fs_v_ref", weakref.ref(v_quant))
+    lib = _lib.require()
     q_c = q.contiguous()
     kv = [t.contiguous() for t in (k_quant.values, k_quant.scale, k_quant.zero_point,
                                     v_quant.values, v_quant.scale, v_quant.zero_point)]

@@ -22,6 +22,8 @@ from .quant import FP8_DTYPE, build_compression_stats, is_fp8, is_per_channel
 from .triton_utils import (
     dispatch_triton_or_fallback,
     launch_plan,
+    layout_checked,
+    remember_layout,
     resolve_block_n as _resolve_block_n,
     resolve_num_warps as _resolve_num_warps,
     validate_decode_query,
@@ -82,11 +84,15 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
                                       ) -> torch.Tensor | tuple[torch.Tensor, dict[str, float]]:
     """Launch the HIP paged kernel (replaces triton_paged.py:338-450); no dense K/V is built."""
 
-    _validate_triton_paged_inputs(q, cache)
-    lib = _lib.require()
-    dev = q.device
-    q_c = q.contiguous()
     kq, vq = cache.k_quant, cache.v_quant
+    dev = q.device
+    memo_key = (q.shape, q.dtype, dev, kq.values.data_ptr(), vq.values.data_ptr(), cache.block_table.data_ptr(),
+                cache.lengths.data_ptr())
+    if not layout_checked(cache, memo_key):
+        _validate_triton_paged_inputs(q, cache)
+        remember_layout(cache, memo_key)
+    lib = _lib.require()
+    q_c = q.contiguous()
     kv = [t.contiguous() for t in (kq.values, kq.scale, kq.zero_point, vq.values, vq.scale, vq.zero_point)]
     table = cache.block_table.contiguous()
     lengths = cache.lengths if cache.lengths.dtype == torch.int64 else cache.lengths.to(torch.int64)

@@ -591,3 +591,49 @@ def test_gpu_validation_errors_before_launch():
         fa.fused_dequant_attention_triton(q.to(DEV), kq, kq, lengths=torch.tensor([1, 2, 3], device=DEV))
     with pytest.raises(RuntimeError):
         fa.fused_dequant_attention_triton(q.to(DEV), kq, kq, lengths=torch.tensor([1, 2]))
+
+
+def test_repeat_launch_memo_still_validates_and_stays_correct():
+    """Repeated launches over one cache skip re-validation only for an identical signature:
+    a changed query, a different V store or lengths of another shape are checked again."""
+
+    announce("repeat-launch layout memo: paged + fused, mismatches after a good call")
+    k = randn((2, 4, 100, 64), 31)
+    v = randn((2, 4, 100, 64), 32)
+    q = randn((2, 4, 64), 33)
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=16, block_table_pattern="shuffled",
+                                       layout_seed=3)
+    ref = oracle_paged_attention(q, cache)
+    for _ in range(3):
+        out = fa.paged_quant_attention_triton(q.to(DEV), cache)
+        sync()
+        assert_attention_close(out, ref, q.dtype, "paged repeat")
+    with pytest.raises(ValueError):
+        fa.paged_quant_attention_triton(randn((2, 3, 64), 34).to(DEV), cache)
+    with pytest.raises(ValueError):
+        fa.paged_quant_attention_triton(randn((2, 4, 64), 34).to(DEV).float().to(torch.float64), cache)
+    out = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    sync()
+    assert_attention_close(out, ref, q.dtype, "paged after rejected calls")
+    # a second cache of another length through the same process-wide plan memo
+    cache2 = fa.PagedKVCache.from_dense(k[:, :, :37].to(DEV), v[:, :, :37].to(DEV), block_size=16)
+    out2 = fa.paged_quant_attention_triton(q.to(DEV), cache2)
+    sync()
+    assert_attention_close(out2, oracle_paged_attention(q, cache2), q.dtype, "second cache")
+
+    kq = fa.quantize_int8_per_block(k.to(DEV), 16)
+    vq = fa.quantize_int8_per_block(v.to(DEV), 16)
+    fref = oracle_fused_attention(q, kq, vq)
+    for _ in range(2):
+        out = fa.fused_dequant_attention_triton(q.to(DEV), kq, vq)
+        sync()
+        assert_attention_close(out, fref, q.dtype, "fused repeat")
+    v_short = fa.quantize_int8_per_block(v[:, :, :50].to(DEV), 16)
+    with pytest.raises(ValueError):
+        fa.fused_dequant_attention_triton(q.to(DEV), kq, v_short)
+    with pytest.raises(ValueError):
+        fa.fused_dequant_attention_triton(q.to(DEV), kq, vq, torch.tensor([100, 100, 100], device=DEV))
+    lengths = torch.tensor([100, 41], device=DEV)
+    out = fa.fused_dequant_attention_triton(q.to(DEV), kq, vq, lengths)
+    sync()
+    assert_attention_close(out, oracle_fused_attention(q, kq, vq, lengths.cpu()), q.dtype, "fused with lengths")
