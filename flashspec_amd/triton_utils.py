@@ -117,6 +117,19 @@ MAX_TILED_WAVES = 16
 MIN_SPLIT_TILES = 8
 MIN_TILES_PER_WAVE = 4
 MAX_TILES_PER_WAVE = 64
+# Light tiles (fp16 query, INT8 values with one scale / zero point per 16-token page, head_dim
+# 128: the fp16 dot2 score path with every lane busy) run 4-wave workgroups when the grid puts
+# one workgroup on 3/4 to all of the CUs and a split holds 128..256 tiles (32..64 per wave, so
+# no extra split).  Measured on MI355X (one box each, settled clocks, 3 rotated input sets), paged /
+# fused us with 4 against 16 waves: B8 H32 S4096 D128 43.4 / 42.1 vs 45.5 / 43.1, S2048
+# 25.1 / 24.3 vs 26.4 / 24.8, B4 S8192 46.4 / 45.0 vs 49.0 / 46.3, B2 S8192 29.3 / 27.3 vs
+# 30.1 / 27.8, B1 S16384 29.7 / 29.2 vs 30.4 / 29.3.  Heavier tiles (bf16 / fp32 query, FP8,
+# per-token or per-channel parameters, 64- or 256-dim layouts, head_dim 96 in the 128-dim layout:
+# 41.0 vs 37.5 us, pages of two quant blocks: 45.2 vs 44.5 us) and grids of more than one
+# workgroup per CU (ragged B16: 56.5 vs 49.7 us) keep more waves, and so do half-empty grids
+# (B4 S2048 in one split: 21.8 us with 4 waves, 18.2 with 8, 19.3 with 16).
+LIGHT_WAVES = 4
+LIGHT_MIN_SPLIT_TILES = 128
 GENERIC_WAVES_PER_CU = 16
 GENERIC_MIN_SPLIT_TILES = 8
 GENERIC_MAX_SPLIT_TILES = 64
@@ -165,13 +178,14 @@ def forced_tiled_waves() -> int | None:
 
 def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: bool = True,
                 waves: int | None = None, max_waves: int = MAX_TILED_WAVES,
-                tile_group: int = 1) -> tuple[int, int, int]:
+                tile_group: int = 1, light: bool = False) -> tuple[int, int, int]:
     """Return ``(split_tiles, max_splits, waves_per_block)`` for one decode launch.
 
     ``rows`` rows of up to ``seq_len`` tokens; ``waves`` fixes the workgroup size
     (tiled path) or the waves grouped per workgroup (generic path).  ``tile_group`` > 1
     (per-channel stores on the tiled path, quant_block / 16): waves take whole groups of that
-    many tiles, so splits hold whole groups and a wave at most 64 tiles.
+    many tiles, so splits hold whole groups and a wave at most 64 tiles.  ``light``: the
+    tiles take the fp16 dot2 score path (see LIGHT_WAVES).
     """
 
     tiles = max(1, math.ceil(seq_len / TILE_TOKENS))
@@ -191,6 +205,9 @@ def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: 
             waves = 1
             while waves < max_waves and 2 * waves * per_wave <= split_groups * grp:
                 waves *= 2
+            if light and grp == 1 and cu_count * 3 // 4 <= rows * n <= cu_count and \
+                    LIGHT_MIN_SPLIT_TILES <= split_groups <= LIGHT_WAVES * MAX_TILES_PER_WAVE:
+                waves = LIGHT_WAVES
         cap = MAX_TILES_PER_WAVE // grp * waves
         if split_groups > cap:
             split_groups = math.ceil(groups / math.ceil(groups / cap))
@@ -251,8 +268,11 @@ _PLAN_KNOBS = ("FLASHSPEC_NUM_WARPS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_SPLITS
 
 
 def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, device,
-                per_channel: bool = False):
+                per_channel: bool = False, light: bool = False):
     """(tiled, waves_per_block, split_tiles, max_splits, block_n) for one decode launch.
+
+    ``light``: fp16 query over INT8 values (the caller's part of the LIGHT_WAVES condition;
+    the store layout part is checked here).
 
     The plan is a pure function of the shape, the device and the three env knobs, which are
     read on every call; it is computed once per distinct combination (a few microseconds of
@@ -262,7 +282,7 @@ def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_bl
     env = os.environ
     knobs = tuple(env.get(k) for k in _PLAN_KNOBS)
     return _launch_plan_cached(int(seq_len), int(rows), int(head_dim), int(page_size), int(quant_block),
-                               dev.type, dev.index, bool(per_channel), knobs)
+                               dev.type, dev.index, bool(per_channel), bool(light), knobs)
 
 
 def torch_device(device):
@@ -273,7 +293,7 @@ def torch_device(device):
 
 @functools.lru_cache(maxsize=512)
 def _launch_plan_cached(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, dev_type: str,
-                        dev_index, per_channel: bool, knobs: tuple):
+                        dev_index, per_channel: bool, light: bool, knobs: tuple):
     """`knobs` only keys the cache: the helpers below read the same values from the environment."""
 
     import torch
@@ -293,6 +313,8 @@ def _launch_plan_cached(seq_len: int, rows: int, head_dim: int, page_size: int, 
         waves = min(waves, max_waves)
     block_n = resolve_block_n()
     group = quant_block // TILE_TOKENS if tiled and per_channel else 1
+    light = light and tiled and not per_channel and quant_block == TILE_TOKENS and page_size == TILE_TOKENS and \
+        head_dim == 128
     split_tiles, max_splits, waves = plan_splits(seq_len, rows, block_n, device_cu_count(device), tiled=tiled,
-                                                 waves=waves, max_waves=max_waves, tile_group=group)
+                                                 waves=waves, max_waves=max_waves, tile_group=group, light=light)
     return tiled, waves, split_tiles, max_splits, block_n

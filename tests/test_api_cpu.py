@@ -137,6 +137,25 @@ def test_split_plan_covers_every_tile(clean_env):
     plan = triton_utils.plan_splits
     # metric shape: 256 rows on 256 CUs -> one 16-wave workgroup per row, no second launch
     assert plan(4096, 256, 128, 256) == (256, 1, 16)
+    # light tiles (fp16 query over INT8 blocks, 128-dim layout): 4-wave workgroups when one
+    # workgroup lands on 3/4 to all of the CUs and every wave keeps 32..64 tiles
+    assert plan(4096, 256, 128, 256, light=True) == (256, 1, 4)
+    assert plan(2048, 256, 128, 256, light=True) == (128, 1, 4)
+    assert plan(8192, 128, 128, 256, light=True) == (256, 2, 4)
+    assert plan(4096, 128, 128, 256, light=True) == (128, 2, 4)
+    assert plan(16384, 32, 128, 256, light=True) == (128, 8, 4)
+    assert plan(4096, 512, 128, 256, light=True) == (256, 1, 16)   # two workgroups per CU
+    assert plan(8192, 256, 128, 256, light=True) == (512, 1, 16)   # 4 waves would need a second split
+    assert plan(1024, 256, 128, 256, light=True) == (64, 1, 16)    # short rows
+    assert plan(2048, 128, 128, 256, light=True) == (64, 2, 16)    # 64-tile splits
+    assert plan(4096, 96, 128, 256, light=True) == (86, 3, 16)
+    assert plan(4096, 160, 128, 256, light=True) == (128, 2, 16)   # 320 workgroups: more than one per CU
+    clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1")  # 128 of 256 CUs busy: not full enough for 4 waves
+    assert plan(2048, 128, 128, 256, light=True) == (128, 1, 16)
+    clean_env.delenv("FLASHSPEC_NUM_SPLITS")
+    clean_env.setenv("FLASHSPEC_NUM_WARPS", "16")
+    assert plan(4096, 256, 128, 256, waves=triton_utils.forced_tiled_waves(), light=True) == (256, 1, 16)
+    clean_env.delenv("FLASHSPEC_NUM_WARPS")
     # few rows: split rows to fill the GPU; workgroup size follows the split length
     assert plan(2048, 128, 128, 256) == (64, 2, 16)
     assert plan(1500, 8, 128, 256) == (8, 12, 2)   # the reference's split-K test shape splits
