@@ -117,10 +117,11 @@ def stream_read_ceiling(torch, dev, steps: int = 60) -> dict:
 
 
 # Untimed calls of the step itself, for at least this long, before the counted warm-up: the
-# GPU's clocks take tens of milliseconds of sustained load to settle.  Measured at the metric
-# shape on one box, the first timed loop read 49.2-49.9 us after 30 warm-up steps (1.4 ms)
-# and 46.8-47.0 us after 1000 or 3000.
-SETTLE_S = 0.1
+# GPU's clocks take tens to hundreds of milliseconds of sustained load to settle.  Measured at
+# the metric shape on one box, the first timed loop read 49.2-49.9 us after 30 warm-up steps
+# (1.4 ms) and 46.8-47.0 us after 1000 or 3000; with 0.1 s of settle and 5 warm-up steps, the
+# first shape of `--mode shapes` still read 46.4 us where the full line read 43.1 us.
+SETTLE_S = 0.25
 
 
 def settle(torch, fn, seconds: float = SETTLE_S) -> int:
