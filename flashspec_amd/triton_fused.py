@@ -104,8 +104,10 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     dev = q.device
     # the memo lives on k_quant; v_quant and lengths enter by identity (a weak reference, so a
     # recycled id never matches) and data pointer
-    memo_key = (q.shape, q.dtype, dev, id(v_quant), k_quant.values.data_ptr(), v_quant.values.data_ptr(),
-                None if lengths is None else (lengths.shape, lengths.device, lengths.dtype))
+    kv_, vv_ = k_quant.values, v_quant.values
+    memo_key = (q.shape, q.dtype, dev, id(v_quant), kv_.data_ptr(), kv_.numel(), k_quant.scale.numel(),
+                k_quant.zero_point.numel(), vv_.data_ptr(), vv_.numel(), v_quant.scale.numel(),
+                v_quant.zero_point.numel(), None if lengths is None else (lengths.shape, lengths.device, lengths.dtype))
     memo = k_quant.__dict__.get("_fs_v_ref")
     if not (layout_checked(k_quant, memo_key) and memo is not None and memo() is v_quant):
         _validate_triton_fused_inputs(q, k_quant, v_quant, lengths)

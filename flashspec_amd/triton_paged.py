@@ -86,8 +86,10 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
 
     kq, vq = cache.k_quant, cache.v_quant
     dev = q.device
-    memo_key = (q.shape, q.dtype, dev, kq.values.data_ptr(), vq.values.data_ptr(), cache.block_table.data_ptr(),
-                cache.lengths.data_ptr())
+    table, lens = cache.block_table, cache.lengths
+    memo_key = (q.shape, q.dtype, dev, table.data_ptr(), table.numel(), lens.data_ptr(), lens.numel(),
+                kq.values.data_ptr(), kq.values.numel(), kq.scale.numel(), kq.zero_point.numel(),
+                vq.values.data_ptr(), vq.values.numel(), vq.scale.numel(), vq.zero_point.numel())
     if not layout_checked(cache, memo_key):
         _validate_triton_paged_inputs(q, cache)
         remember_layout(cache, memo_key)

@@ -57,8 +57,9 @@ def dispatch_triton_or_fallback(args, kwargs, *, run_triton, load_fallback, extr
 # The K/V containers (QuantizedTensor, PagedKVCache) are frozen dataclasses: their tensors
 # never change identity.  After a full validation, the container remembers the query
 # signature (shape, dtype, device) and companions it was checked with, plus the data
-# pointers of its value stores, so repeated launches over the same cache skip the checks
-# (about 10 us of host time per call).  Any difference re-runs the full validation.
+# pointers and element counts of its tensors, so repeated launches over the same cache skip
+# the checks (about 10 us of host time per call).  Any difference, including a tensor resized
+# in place, re-runs the full validation.
 _MEMO_ATTR = "_fs_layout_checked"
 
 
