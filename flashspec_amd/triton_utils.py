@@ -131,6 +131,13 @@ MAX_TILES_PER_WAVE = 64
 # (B4 S2048 in one split: 21.8 us with 4 waves, 18.2 with 8, 19.3 with 16).
 LIGHT_WAVES = 4
 LIGHT_MIN_SPLIT_TILES = 128
+# Rows that fill at least half of the CUs split in two only when each half keeps 128 tiles;
+# otherwise they run unsplit with at most 8 waves per workgroup.  Measured on MI355X, B4 H32
+# S2048 D128 (128 rows of 128 tiles), paged / fused us: unsplit x 8 waves 18.2 / 17.6, unsplit x
+# 16 19.3 / 18.0, 2 splits x 16 (the plan before) 19.1 / 18.4; B4 S4096 (256 tiles) keeps its
+# split: 2 x 4 waves 29.1 / 27.9 against unsplit x 8 29.9 / 29.3.
+HALVE_MIN_SPLIT_TILES = 128
+HALF_EMPTY_WAVES = 8
 GENERIC_WAVES_PER_CU = 16
 GENERIC_MIN_SPLIT_TILES = 8
 GENERIC_MAX_SPLIT_TILES = 64
@@ -194,11 +201,16 @@ def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: 
     if tiled:
         grp = max(1, tile_group)
         groups = math.ceil(tiles / grp)
+        half_empty = False
         if forced is not None:
             n = forced
         else:
             n = max(1, math.ceil(cu_count / max(1, rows)))
             n = min(n, max(1, math.ceil(tiles / MIN_SPLIT_TILES)))
+            if n == 2 and tiles < 2 * HALVE_MIN_SPLIT_TILES:
+                # half the CUs or more already hold a row: a two-way split saves less than its
+                # merge launch costs unless each half keeps HALVE_MIN_SPLIT_TILES tiles
+                n, half_empty = 1, True
         n = min(n, groups)
         split_groups = math.ceil(groups / n)
         if waves is None:
@@ -206,6 +218,8 @@ def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: 
             waves = 1
             while waves < max_waves and 2 * waves * per_wave <= split_groups * grp:
                 waves *= 2
+            if half_empty and grp == 1:
+                waves = min(waves, HALF_EMPTY_WAVES)
             if light and grp == 1 and cu_count * 3 // 4 <= rows * n <= cu_count and \
                     LIGHT_MIN_SPLIT_TILES <= split_groups <= LIGHT_WAVES * MAX_TILES_PER_WAVE:
                 waves = LIGHT_WAVES
