@@ -102,8 +102,9 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     """Launch the HIP fused kernel (replaces triton_fused.py:604-761); no dense K/V is built."""
 
     dev = q.device
-    # the memo lives on k_quant; v_quant and lengths enter by identity (a weak reference, so a
-    # recycled id never matches) and data pointer
+    # the memo lives on k_quant; v_quant enters by identity (checked through a weak reference, so
+    # a recycled id never matches), data pointer and element counts, lengths by shape, device
+    # and dtype
     kv_, vv_ = k_quant.values, v_quant.values
     memo_key = (q.shape, q.dtype, dev, id(v_quant), kv_.data_ptr(), kv_.numel(), k_quant.scale.numel(),
                 k_quant.zero_point.numel(), vv_.data_ptr(), vv_.numel(), v_quant.scale.numel(),
