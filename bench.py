@@ -31,6 +31,16 @@ METRIC = "decode-attn µs/step + achieved HBM GB/s (% of peak), paged INT8 B8 H3
 PEAK_GBPS = 8000.0  # MI355X HBM3E
 B, H, S, D, PAGE = 8, 32, 4096, 128, 16
 ROTATE = 3
+# Rotated input sets must together exceed the 256 MiB MALL (last-level cache) twice over, so a
+# timed step cannot be served from what an earlier step left there.
+MALL_BYTES = 256 << 20
+
+
+def rotation_sets(set_bytes: int) -> int:
+    """Input sets to rotate for a workload of `set_bytes` per step: at least ROTATE, and enough
+    that they hold at least 2 x MALL_BYTES together."""
+
+    return max(ROTATE, math.ceil(2 * MALL_BYTES / max(1, set_bytes)))
 PMC_SUMMARY = ROOT / "profiles" / "paged_decode_b8h32s4096d128_pmc.json"
 
 
@@ -52,6 +62,7 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--only", default="", help="--mode shapes: comma-separated shape names to run")
     ap.add_argument("--layout", default="contiguous", choices=["contiguous", "shuffled", "interleaved"])
     ap.add_argument("--mode", default="full", choices=["full", "paged", "copy", "readbw", "serving", "shapes", "tree"],
                     help="full: the JSON line; paged: only the timed paged steps (for rocprofv3); "
@@ -166,33 +177,100 @@ def kernel_durations_us(torch, fn, calls: int) -> list[float]:
     return [a.elapsed_time(b) * 1e3 for a, b in evs]
 
 
-def cpu_baseline(seconds_budget: float = 20.0) -> dict:
-    """Time the numpy oracle (reference algorithm, one thread) on a 2-request sample."""
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    import numpy as np
 
-    from oracle import attention as oa
-    from oracle import paged as op
+def _median_run(fn, threads: int, repeats: int) -> tuple[float, int]:
+    """Median seconds of `repeats` timed calls after one warm-up call, on `threads` torch threads."""
 
-    sample_b = 2
-    rng = np.random.default_rng(0)
-    k = rng.standard_normal((sample_b, H, S, D), dtype=np.float32).astype(np.float16)
-    v = rng.standard_normal((sample_b, H, S, D), dtype=np.float32).astype(np.float16)
-    q = rng.standard_normal((sample_b, H, D), dtype=np.float32).astype(np.float16)
-    cache = op.from_dense(k.astype(np.float32), v.astype(np.float32), PAGE)
+    import torch
+
+    torch.set_num_threads(threads)
+    fn()
     times = []
-    t_end = time.perf_counter() + seconds_budget
-    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+    for _ in range(repeats):
         t0 = time.perf_counter()
-        oa.paged_quant_attention(q.astype(np.float32), cache)
+        fn()
         times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
-    nbytes = algorithmic_bytes([S] * sample_b, H, D, PAGE)
+    return statistics.median(times), repeats
+
+
+def cpu_baseline(torch, fa, dev) -> dict:
+    """The reference's CPU path timed on this host: its PyTorch op sequence (dequantize K/V to dense
+    float32, einsum, length mask, softmax, einsum, cast; reference attention.py:124-223), which is
+    this package's portable path (`flashspec_amd.attention`), on the same synthetic workload as the
+    GPU line.  All cores (`torch.set_num_threads(len(os.sched_getaffinity(0)))`) and one thread;
+    `perf_counter`, one warm-up call, median of the repeats.
+
+    `value`: the metric workload (paged B8 H32 S4096 D128, whole-store dequantize and gather as
+    the reference's `paged_quant_attention` does) on all cores.  Also: C1 (fused B4 S2048, the
+    primary CPU comparator) on all cores and on one thread, and the metric workload on one thread
+    over a one-request sample (one request's pool; the reference path's cost is linear in it).
+    The int8 stores are made by this library's GPU quantizer, which is bit-identical to the CPU
+    path (tested), then copied to host memory; only the attention calls are timed."""
+
+    threads = len(os.sched_getaffinity(0))
+    saved = torch.get_num_threads()
+    g = torch.Generator().manual_seed(0)
+
+    def paged_inputs(b):
+        q = torch.randn((b, H, D), generator=g).to(torch.float16)
+        k = torch.randn((b, H, S, D), generator=g).to(torch.float16)
+        v = torch.randn((b, H, S, D), generator=g).to(torch.float16)
+        c = fa.PagedKVCache.from_dense(k.to(dev), v.to(dev), block_size=PAGE)
+        cpu = fa.PagedKVCache(
+            k_quant=fa.QuantizedTensor(*(t.cpu() for t in (c.k_quant.values, c.k_quant.scale, c.k_quant.zero_point)),
+                                       c.k_quant.block_size, c.k_quant.original_shape),
+            v_quant=fa.QuantizedTensor(*(t.cpu() for t in (c.v_quant.values, c.v_quant.scale, c.v_quant.zero_point)),
+                                       c.v_quant.block_size, c.v_quant.original_shape),
+            block_table=c.block_table.cpu(), lengths=c.lengths.cpu(), block_size=PAGE, max_seq_len=S)
+        return q, cpu
+
+    try:
+        c1_b, c1_s = 4, 2048
+        q1 = torch.randn((c1_b, H, D), generator=g).to(torch.float16)
+        k1 = torch.randn((c1_b, H, c1_s, D), generator=g).to(torch.float16)
+        v1 = torch.randn((c1_b, H, c1_s, D), generator=g).to(torch.float16)
+        kq, vq = (fa.quantize_int8_per_block(x.to(dev), PAGE) for x in (k1, v1))
+        kq, vq = (fa.QuantizedTensor(x.values.cpu(), x.scale.cpu(), x.zero_point.cpu(), x.block_size,
+                                     x.original_shape) for x in (kq, vq))
+        del k1, v1
+        c1_bytes = algorithmic_bytes([c1_s] * c1_b, H, D, PAGE)
+        c1_all, n1 = _median_run(lambda: fa.fused_dequant_attention(q1, kq, vq), threads, 5)
+        c1_one, _ = _median_run(lambda: fa.fused_dequant_attention(q1, kq, vq), 1, 5)
+        del kq, vq
+        qm, cm = paged_inputs(B)
+        m_all, nm = _median_run(lambda: fa.paged_quant_attention(qm, cm), threads, 5)
+        del qm, cm
+        qs, cs = paged_inputs(1)
+        m_one, ns = _median_run(lambda: fa.paged_quant_attention(qs, cs), 1, 3)
+        del qs, cs
+    finally:
+        torch.set_num_threads(saved)
+    m_bytes = algorithmic_bytes([S] * B, H, D, PAGE)
+    s_bytes = algorithmic_bytes([S], H, D, PAGE)
     return {
-        "value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"numpy oracle paged attention (dequantize whole store, gather, einsum, softmax, einsum) "
-                  f"on {sample_b} of the 8 requests (H32 S4096 D128), median of {len(times)} runs, "
-                  f"{sec * 1e3:.0f} ms per run",
+        "value": round(m_bytes / m_all / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"the reference's torch-CPU paged path (flashspec_amd.attention.paged_quant_attention: "
+                  f"whole-store dequantize, gather, einsum, mask, softmax, einsum) on the full metric workload "
+                  f"B{B} H{H} S{S} D{D}, {threads} threads, median of {nm} after 1 warm-up: "
+                  f"{m_all * 1e3:.1f} ms per step",
+        "us_per_step": round(m_all * 1e6, 1),
+        "cpu_model": cpu_model(), "torch": torch.__version__, "threads": threads,
+        "c1_fused": {"workload": f"fused B{c1_b} H{H} S{c1_s} D{D} (C1), reference torch-CPU fused path",
+                     "all_cores_ms": round(c1_all * 1e3, 2), "all_cores_gbps": round(c1_bytes / c1_all / 1e9, 3),
+                     "one_thread_ms": round(c1_one * 1e3, 2), "one_thread_gbps": round(c1_bytes / c1_one / 1e9, 3),
+                     "repeats": n1},
+        "metric_one_thread": {"sample": f"1 of the {B} requests (its own page pool), B1 H{H} S{S} D{D}",
+                              "ms": round(m_one * 1e3, 1), "gbps": round(s_bytes / m_one / 1e9, 3),
+                              "repeats": ns},
     }
 
 
@@ -329,18 +407,25 @@ def paged_from_blocks(torch, fa, k, v, page: int, qb: int, lengths):
                            max_seq_len=s)
 
 
-def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
-    """Paged and contiguous decode over the SHAPES table, 3 rotated input sets each; prints one
+def shapes_bench(torch, fa, dev, steps: int, warmup: int, only=None) -> list[dict]:
+    """Paged and contiguous decode over the SHAPES table (or the shapes named in `only`), with
+    `rotation_sets` input sets each (at least 3, and at least 2 x the MALL together); prints one
     JSON object per shape."""
 
     out = []
     for name, b, h, s, d, page, qb, qdt, lens, *rest in SHAPES:
+        if only and name not in only:
+            continue
         fmt = rest[0] if rest else "int8"
         g = torch.Generator(device=dev)
         g.manual_seed(11)
         qdtype = getattr(torch, qdt)
+        lengths = lens or [s] * b
+        nbytes = algorithmic_bytes(lengths, h, d, page, q_bytes=torch.finfo(qdtype).bits // 8, quant_block=qb,
+                                   param_bytes={"fp8": 4, "channel": 6 * d}.get(fmt, 6))
+        n_sets = rotation_sets(nbytes)
         sets = []
-        for _ in range(ROTATE):
+        for _ in range(n_sets):
             q = torch.randn((b, h, d), generator=g, device=dev, dtype=torch.float16).to(qdtype)
             k = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
             v = torch.randn((b, h, s, d), generator=g, device=dev, dtype=torch.float16)
@@ -374,18 +459,16 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
                 vq = fa.quantize_int8_per_block(v, qb)
             del k, v
             sets.append((q, cache, kq, vq, lt))
-        lengths = lens or [s] * b
-        nbytes = algorithmic_bytes(lengths, h, d, page, q_bytes=torch.finfo(qdtype).bits // 8, quant_block=qb,
-                                   param_bytes={"fp8": 4, "channel": 6 * d}.get(fmt, 6))
-        ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(sets[i % ROTATE][0], sets[i % ROTATE][1]),
+        ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(sets[i % n_sets][0], sets[i % n_sets][1]),
                        steps, warmup)
         _, st = fa.paged_quant_attention_triton(sets[0][0], sets[0][1], return_stats=True)
         row = {"shape": name, "format": fmt, "batch": b, "heads": h, "seq_len": s, "head_dim": d, "page": page,
                "quant_block": qb, "q_dtype": qdt, "paged_us": round(ms * 1e3, 2), "paged_pct_of_peak": round(
                    100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
-               "tiled_path": bool(st["tiled_path"]), "num_splits": st["num_splits"], "waves": st["num_warps"]}
+               "tiled_path": bool(st["tiled_path"]), "num_splits": st["num_splits"], "waves": st["num_warps"],
+               "rotated_sets": n_sets, "rotated_bytes": n_sets * nbytes}
         fms = time_loop(torch, lambda i: fa.fused_dequant_attention_triton(
-            sets[i % ROTATE][0], sets[i % ROTATE][2], sets[i % ROTATE][3], lengths=sets[i % ROTATE][4]), steps, warmup)
+            sets[i % n_sets][0], sets[i % n_sets][2], sets[i % n_sets][3], lengths=sets[i % n_sets][4]), steps, warmup)
         row["fused_us"] = round(fms * 1e3, 2)
         row["paged_vs_fused"] = round(ms / fms, 3)
         out.append(row)
@@ -401,7 +484,7 @@ TREE_CASES = ((4, (1, 4, 8, 16, 32, 64), "affine_block"), (8, (16, 64), "affine_
 
 def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
     """tree_verify_attention over B4 and B8 H32 S4096 D128 paged prefixes (16-token pages, fp16
-    q and drafts) for random draft trees of 1-64 nodes, 3 rotated input sets.  Algorithmic
+    q and drafts) for random draft trees of 1-64 nodes, `rotation_sets` input sets.  Algorithmic
     bytes read the shared prefix once per (request, head) plus the drafts, q, output and parents;
     ``vs_decode`` = time / the time of one single-query paged decode over the same prefix.  The
     tree topology is a host tensor, as a drafter produces it (checked, then copied through
@@ -412,25 +495,26 @@ def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
     g.manual_seed(13)
     gp = torch.Generator().manual_seed(17)
     for nb, node_counts, kv_format in TREE_CASES:
+        prefix = algorithmic_bytes([S] * nb, H, D, PAGE, param_bytes=4 if kv_format == "fp8_block" else 6) \
+            - 2 * nb * H * D * 2
+        n_sets = rotation_sets(prefix)
         caches = []
-        for _ in range(ROTATE):
+        for _ in range(n_sets):
             k = torch.randn((nb, H, S, D), generator=g, device=dev, dtype=torch.float16)
             v = torch.randn((nb, H, S, D), generator=g, device=dev, dtype=torch.float16)
             caches.append(fa.PagedKVCache.from_dense(k, v, block_size=PAGE, kv_format=kv_format))
             del k, v
-        q1 = [torch.randn((nb, H, D), generator=g, device=dev, dtype=torch.float16) for _ in range(ROTATE)]
-        dec_ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(q1[i % ROTATE], caches[i % ROTATE]),
+        q1 = [torch.randn((nb, H, D), generator=g, device=dev, dtype=torch.float16) for _ in range(n_sets)]
+        dec_ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(q1[i % n_sets], caches[i % n_sets]),
                            steps, warmup)
-        prefix = algorithmic_bytes([S] * nb, H, D, PAGE, param_bytes=4 if kv_format == "fp8_block" else 6) \
-            - 2 * nb * H * D * 2
         for n in node_counts:
             par = torch.full((nb, n), -1, dtype=torch.int64)
             for j in range(1, n):
                 par[:, j] = torch.randint(-1, j, (nb,), generator=gp)
             ins = [tuple(torch.randn((nb, n, H, D), generator=g, device=dev, dtype=torch.float16) for _ in range(3))
-                   for _ in range(ROTATE)]
-            ms = time_loop(torch, lambda i: fa.tree_verify_attention(ins[i % ROTATE][0], caches[i % ROTATE],
-                                                                     ins[i % ROTATE][1], ins[i % ROTATE][2], par),
+                   for _ in range(n_sets)]
+            ms = time_loop(torch, lambda i: fa.tree_verify_attention(ins[i % n_sets][0], caches[i % n_sets],
+                                                                     ins[i % n_sets][1], ins[i % n_sets][2], par),
                            steps, warmup)
             _, st = fa.tree_verify_attention(ins[0][0], caches[0], ins[0][1], ins[0][2], par, return_stats=True)
             nbytes = prefix + 4 * nb * n * H * D * 2 + nb * n * 8
@@ -441,7 +525,7 @@ def tree_bench(torch, fa, dev, steps: int, warmup: int) -> list[dict]:
                    "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
                    "single_query_decode_us": round(dec_ms * 1e3, 2), "vs_decode": round(ms / dec_ms, 3),
                    "num_splits": st["num_splits"], "waves": st["num_warps"], "mfma_prefix": st["mfma_prefix"],
-                   "nodes_per_workgroup": st["nodes_per_workgroup"]}
+                   "nodes_per_workgroup": st["nodes_per_workgroup"], "rotated_sets": n_sets}
             out.append(row)
             print(json.dumps({"mode": "tree", **row}), flush=True)
             del ins
@@ -485,7 +569,8 @@ def main() -> int:
         print(json.dumps({"mode": "readbw", **stream_read_ceiling(torch, dev, args.steps)}), flush=True)
         return 0
     if args.mode == "shapes":
-        shapes_bench(torch, fa, dev, min(args.steps, 100), min(args.warmup, 10))
+        shapes_bench(torch, fa, dev, min(args.steps, 100), min(args.warmup, 10),
+                     only={x for x in args.only.split(",") if x} or None)
         return 0
     if args.mode == "tree":
         tree_bench(torch, fa, dev, min(args.steps, 100), min(args.warmup, 10))
@@ -594,7 +679,7 @@ def main() -> int:
     except Exception as exc:  # reported, never hides the metric line
         result["serving_step"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_baseline(torch, fa, dev)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -71,6 +71,44 @@ __device__ __forceinline__ float wave_min(float x) {
   return x;
 }
 
+// ---- gfx950 lane swaps (VALU; no LDS traffic) ----------------------------------------------------
+// For registers x and y of every lane (layouts checked lane by lane on gfx950):
+//   swap32: .a = x of lanes 0-31 in lanes 0-31, y of lanes 0-31 in lanes 32-63;
+//           .b = x of lanes 32-63 in lanes 0-31, y of lanes 32-63 in lanes 32-63.
+//   swap16 (rows of 16 lanes r0..r3): .a = (x.r0, y.r0, x.r2, y.r2); .b = (x.r1, y.r1, x.r3, y.r3).
+// So swap(x, y).a + swap(x, y).b is the sum over the partner rows of x in the lower rows and of y
+// in the upper ones (one half of a reduce-scatter), and swap(x, x) gives every lane the same sum.
+struct LanePair {
+  float a, b;
+};
+__device__ __forceinline__ LanePair swap32(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y),
+                                                  false, false);
+  return {__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1])};
+}
+__device__ __forceinline__ LanePair swap16(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y),
+                                                  false, false);
+  return {__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1])};
+}
+constexpr int kDppRowRor8 = 0x128;  // lane i of a row reads lane (i + 8) % 16
+// lane i reads lane i ^ 4 (ds_swizzle bit-mask mode: and 0x1f, or 0, xor 4; no memory access)
+__device__ __forceinline__ float swizzle_xor4(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x101f));
+}
+
+// Maximum over the whole wave, every lane getting the same bits.
+__device__ __forceinline__ float wave_max_valu(float x) {
+  x = fmaxf(x, dpp_f32<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp_f32<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp_f32<kDppRowHalfMirror>(x));
+  x = fmaxf(x, dpp_f32<kDppRowMirror>(x));
+  const LanePair r16 = swap16(x, x);
+  x = fmaxf(r16.a, r16.b);
+  const LanePair r32 = swap32(x, x);
+  return fmaxf(r32.a, r32.b);
+}
+
 __device__ __forceinline__ int readlane_i32(int x, int lane) { return __builtin_amdgcn_readlane(x, lane); }
 __device__ __forceinline__ float readlane_f32(float x, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));

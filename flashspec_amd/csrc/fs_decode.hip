@@ -426,6 +426,104 @@ __device__ __forceinline__ void consume_tile_channel(LaneState& st, const TileRe
   for (int e = 0; e < 16; ++e) st.acc[e] = fmaf(cp.vs[e], fmaf(-cp.vz[e], P, T[e]), st.acc[e]);
 }
 
+// ---- end of a wave: its token-row groups summed without LDS traffic --------------------------------
+// A wave's lanes (g, j) = (lane / LPT, lane % LPT) hold partial sums for dims [16j, 16j + 16) over
+// token-row group g.  reduce_scatter_groups sums over g and leaves lane (g, j) with dims
+// 16j + NV*g + t, t < NV = LPT / 4: swap32 halves the 16 values over lane bit 5, swap16 over bit 4,
+// the row rotation by 8 over bit 3 (LPT <= 8) and the xor-4 swizzle over bit 2 (LPT = 4).
+template <int LPT>
+__device__ __forceinline__ void reduce_scatter_groups(const float (&acc)[16], float (&out)[LPT / 4], int lane) {
+  static_assert(LPT == 4 || LPT == 8 || LPT == 16, "lanes per token row");
+  float v8[8];  // dim i + 8 * bit5
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const LanePair r = swap32(acc[i], acc[i + 8]);
+    v8[i] = r.a + r.b;
+  }
+  float v4[4];  // dim i + 4 * bit4 + 8 * bit5
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const LanePair r = swap16(v8[i], v8[i + 4]);
+    v4[i] = r.a + r.b;
+  }
+  if constexpr (LPT == 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = v4[i];
+  } else {
+    const bool b3 = (lane & 8) != 0;
+    float v2[2];  // dim i + 2 * bit3 + 4 * bit4 + 8 * bit5
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float send = b3 ? v4[i] : v4[i + 2];
+      const float keep = b3 ? v4[i + 2] : v4[i];
+      v2[i] = keep + dpp_f32<kDppRowRor8>(send);
+    }
+    if constexpr (LPT == 8) {
+      out[0] = v2[0];
+      out[1] = v2[1];
+    } else {
+      const bool b2 = (lane & 4) != 0;
+      const float send = b2 ? v2[0] : v2[1];
+      const float keep = b2 ? v2[1] : v2[0];
+      out[0] = keep + swizzle_xor4(send);  // dim lane >> 2
+    }
+  }
+}
+
+// Sum over the token-row groups, the same bits in every lane.
+template <int LPT>
+__device__ __forceinline__ float allreduce_groups(float x) {
+  const LanePair r32 = swap32(x, x);
+  x = r32.a + r32.b;
+  const LanePair r16 = swap16(x, x);
+  x = r16.a + r16.b;
+  if constexpr (LPT <= 8) x += dpp_f32<kDppRowRor8>(x);
+  if constexpr (LPT <= 4) x += swizzle_xor4(x);
+  return x;
+}
+
+// The NW wave states of one workgroup (LDS: acc [NW][DP], (m, l) [NW]) merged into the row's output,
+// or into the split partials (m, l, acc) when the row has several splits.
+template <int NW, int DP, typename QT>
+__device__ __forceinline__ void merge_waves(const DecodeParams& p, const float* s_acc, const float* s_ml, int row,
+                                            int split, int nsplit, int D) {
+  float mv[NW], lv[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float2 ml = *(const float2*)(s_ml + 2 * w);
+    mv[w] = ml.x;
+    lv[w] = ml.y;
+  }
+  float M = mv[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, mv[w]);
+  float ew[NW];
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    ew[w] = fast_exp2(mv[w] - M);
+    L = fmaf(lv[w], ew[w], L);
+  }
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float x[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) x[w] = s_acc[w * DP + d];
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) a = fmaf(x[w], ew[w], a);
+    if (nsplit == 1 && !p.force_partials) {
+      ((QT*)p.out)[(size_t)row * D + d] = from_f32<QT>(L > 0.f ? a / L : 0.f);
+    } else {
+      const size_t ws = (size_t)row * p.max_splits + split;
+      p.part_acc[ws * D + d] = a;
+      if (d == 0) {
+        p.part_ml[2 * ws] = M;
+        p.part_ml[2 * ws + 1] = L;
+      }
+    }
+  }
+}
+
 // Waves per workgroup the tiled kernel may run with: 16, or 8 for head_dim 256 so
 // that its 128-float registers per lane fit without spilling.
 // Per-channel parameters add ~50 registers per lane: 8 waves there too.
@@ -443,12 +541,10 @@ decode_rows_kernel(const DecodeParams p) {
   constexpr bool T8 = QM == kQmBlockTail8 || QM == kQmTokenTail8;  // head_dim an odd multiple of 8
   constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken || QM == kQmTokenTail8, CHB = QM == kQmChannelBlocks;
   constexpr bool CH = QM == kQmChannel || CHB;
-  __shared__ float s_acc[kMaxWaves * DP];
-  __shared__ float s_ml[2 * kMaxWaves];
+  constexpr int WMAX = max_tiled_waves(DP, QM);
+  __shared__ __attribute__((aligned(16))) float s_acc[WMAX * DP];
+  __shared__ __attribute__((aligned(16))) float s_ml[2 * WMAX];
 
-#ifdef FS_TRACE_WG
-  const uint64_t trace_t0 = __builtin_amdgcn_s_memrealtime();
-#endif
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform by construction; readfirstlane lets the compiler keep everything derived
   // from it (tile counts, tile offsets, load base addresses) in scalar registers
@@ -660,68 +756,47 @@ decode_rows_kernel(const DecodeParams p) {
   for (int k = 0; k < nk; k += 2) {
     load(tb2, k + 1);
     consume(ta, k);
-#ifdef FS_TRACE_WG
-    if (k == 0 && w == 0 && lane == 0)
-      ((uint64_t*)p.part_ml)[(size_t)blockIdx.x * 20 + 1] = __builtin_amdgcn_s_memrealtime();
-#endif
     if (k + 1 >= nk) break;
     load(ta, k + 2);
     consume(tb2, k + 1);
   }
 
-#ifdef FS_TRACE_WG
-  // per-workgroup record: [start, wave0 first-data, 16 x wave end, merged end]
-  uint64_t* trace = (uint64_t*)p.part_ml + (size_t)blockIdx.x * 20;
-  if (lane == 0) trace[2 + w] = __builtin_amdgcn_s_memrealtime();
-  if (threadIdx.x == 0) trace[0] = trace_t0;
-#endif
 #pragma unroll
   for (int e = 0; e < 16; ++e) st.acc[e] -= st.zacc;
-  // merge the token-row groups of the wave (lanes sharing a dim slice)
-  float m = st.m, l = st.l;
+  // One running maximum per wave (lanes of a token-row group already share theirs), then the
+  // groups' sums, scattered so that each lane holds NV = LPT / 4 dims of the wave's result.
+  constexpr int NV = LPT / 4;
+  const float mw = wave_max_valu(st.m);
+  const float alpha = fast_exp2(st.m - mw);  // 0 for lanes that saw no valid token (st.m = kNegBig)
 #pragma unroll
-  for (int off = LPT; off < kWave; off <<= 1) {
-    const float m2 = __shfl_xor(m, off, kWave);
-    const float l2 = __shfl_xor(l, off, kWave);
-    const float mm = fmaxf(m, m2);
-    const float a1 = fast_exp2(m - mm), a2 = fast_exp2(m2 - mm);
-    l = l * a1 + l2 * a2;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) st.acc[e] = st.acc[e] * a1 + __shfl_xor(st.acc[e], off, kWave) * a2;
-    m = mm;
-  }
-  // merge the W waves through LDS
-  if (g == 0) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s_acc[w * DP + 16 * j + e] = st.acc[e];
-  }
-  if (lane == 0) {
-    s_ml[2 * w] = m;
-    s_ml[2 * w + 1] = l;
-  }
+  for (int e = 0; e < 16; ++e) st.acc[e] *= alpha;
+  const float lw = allreduce_groups<LPT>(st.l * alpha);
+  float part[NV];
+  reduce_scatter_groups<LPT>(st.acc, part, lane);
+  float* dst = s_acc + w * DP + 16 * j + NV * g;
+  if constexpr (NV == 4)
+    *(float4*)dst = make_float4(part[0], part[1], part[2], part[3]);
+  else if constexpr (NV == 2)
+    *(float2*)dst = make_float2(part[0], part[1]);
+  else
+    dst[0] = part[0];
+  if (lane == 0) *(float2*)(s_ml + 2 * w) = make_float2(mw, lw);
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float M = kNegBig;
-    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, s_ml[2 * ww]);
-    float L = 0.f, a = 0.f;
-    for (int ww = 0; ww < W; ++ww) {
-      const float e = fast_exp2(s_ml[2 * ww] - M);
-      L = fmaf(s_ml[2 * ww + 1], e, L);
-      a = fmaf(s_acc[ww * DP + d], e, a);
-    }
-    if (nsplit == 1 && !p.force_partials) {
-      ((QT*)p.out)[(size_t)row * D + d] = from_f32<QT>(L > 0.f ? a / L : 0.f);
-#ifdef FS_TRACE_WG
-      if (d == 0) ((uint64_t*)p.part_ml)[(size_t)blockIdx.x * 20 + 19] = __builtin_amdgcn_s_memrealtime();
-#endif
-    } else {
-      const size_t ws = (size_t)row * p.max_splits + split;
-      p.part_acc[ws * D + d] = a;
-      if (d == 0) {
-        p.part_ml[2 * ws] = M;
-        p.part_ml[2 * ws + 1] = L;
+  // merge the W waves: weights exp2(m_w - M), in wave order (bit-reproducible); the wave count is
+  // a compile-time constant there, so each thread issues all its LDS reads together
+  switch (W) {
+    case 1: merge_waves<1, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D); break;
+    case 2: merge_waves<2, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D); break;
+    case 4: merge_waves<4, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D); break;
+    default:
+      if constexpr (WMAX >= 16) {
+        if (W == 16) {
+          merge_waves<16, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D);
+          break;
+        }
       }
-    }
+      merge_waves<8, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D);
+      break;
   }
 }
 

@@ -42,9 +42,15 @@ from .runtime import device_name, resolve_device, resolve_dtype, synchronize
 from .triton_utils import HAS_TRITON
 
 DTYPE_CHOICES = ["auto", "float16", "fp16", "bfloat16", "bf16", "float32", "fp32"]
+# Kernels a backend's step launches (rocprofv3 kernel names, e.g.
+# "void fs::decode_rows_kernel<128, __half, true, 0, 0>(fs::DecodeParams)"): the tiled decode kernel
+# (template <head_dim layout, q type, paged, quant mode, value format>), the generic one and the
+# split merge.
 KERNEL_REGEX = {
-    "triton_fused": "fused_dequant_attention|decode_rows_kernel<[0-9]+, [^,]+, false>|combine_splits",
-    "triton_paged": "paged_quant_attention|decode_rows_kernel<[0-9]+, [^,]+, true>|combine_splits",
+    "triton_fused": r"decode_rows_kernel<[0-9]+, [^,]+, false[,>]|decode_generic_kernel<[^,]+, false[,>]|"
+                    r"combine_splits",
+    "triton_paged": r"decode_rows_kernel<[0-9]+, [^,]+, true[,>]|decode_generic_kernel<[^,]+, true[,>]|"
+                    r"combine_splits",
 }
 # gfx950's FETCH_SIZE expression counts half of the bytes a plain device copy reads
 # (calibration in profiles/paged_decode_b8h32s4096d128_pmc.json); WRITE_SIZE is exact.
@@ -203,56 +209,84 @@ def latency_breakdown(args, stats: dict, latency_ms: float, method: str) -> list
     ]
 
 
+def _csv_rows(directory: str, suffix: str) -> list[dict]:
+    import csv
+
+    rows = []
+    for path in glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True):
+        with open(path, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
 def _profile(args, result: dict) -> None:
-    """Run this benchmark under rocprofv3 (child processes) and backfill measured_* fields."""
+    """Run this benchmark under rocprofv3 (child processes, the program itself after ``--``) in
+    three passes -- kernel trace, FETCH_SIZE, WRITE_SIZE -- and backfill the measured_* fields.
+
+    Per step: the matching kernels' median durations and median per-dispatch bytes, summed over
+    the distinct kernels a step launches (the decode, plus the split merge when rows split).
+    FETCH_SIZE is scaled by FETCH_SIZE_SCALE (gfx950 counts half of the bytes a copy reads)."""
+
+    import re
 
     regex = KERNEL_REGEX.get(args.backend)
+    pat = re.compile(regex) if regex else None
     bench = [sys.executable, "-m", "flashspec_amd.microbench", *cli_args(args, json_flag=False)]
+    env = dict(os.environ, TMPDIR=tempfile.gettempdir())
     with tempfile.TemporaryDirectory() as tmp:
-        passes = {"trace": ["--kernel-trace", "--stats"], "fetch": ["--pmc", "FETCH_SIZE"],
-                  "write": ["--pmc", "WRITE_SIZE"]}
-        dbs = {}
+        passes = {"trace": ["--kernel-trace"], "fetch": ["--pmc", "FETCH_SIZE"], "write": ["--pmc", "WRITE_SIZE"]}
+        found = {}
         for name, opts in passes.items():
-            cmd = [args.rocprof_bin, *opts]
+            cmd = [args.rocprof_bin, *opts, "--output-format", "csv"]
             if regex and name != "trace":
                 cmd += ["--kernel-include-regex", regex]
             cmd += ["-d", os.path.join(tmp, name), "-o", name, "--", *bench]
             try:
                 proc = subprocess.run(cmd, capture_output=True, text=True, timeout=args.profile_timeout,
-                                      cwd=str(Path(__file__).resolve().parents[1]))
+                                      cwd=str(Path(__file__).resolve().parents[1]), env=env)
             except (FileNotFoundError, subprocess.TimeoutExpired) as exc:
                 result["profiler_error"] = f"rocprofv3 {name} pass failed: {exc}"
                 return
-            found = glob.glob(os.path.join(tmp, name, "**", "*.db"), recursive=True)
-            if proc.returncode != 0 and not found:
-                result["profiler_error"] = f"rocprofv3 {name} exited {proc.returncode}: {proc.stderr[-600:]}"
+            suffix = "kernel_trace.csv" if name == "trace" else "counter_collection.csv"
+            rows = _csv_rows(os.path.join(tmp, name), suffix)
+            # rocprofv3 may exit non-zero after the program finished with whole results; only
+            # missing output counts as a failure
+            if not rows:
+                result["profiler_error"] = f"rocprofv3 {name} exited {proc.returncode} without {suffix}: " \
+                                           f"{proc.stderr[-600:]}"
                 return
-            dbs[name] = found[0]
-        import re
+            found[name] = rows
 
-        pat = re.compile(regex) if regex else None
+        durations: dict[str, list[float]] = {}
+        for r in found["trace"]:
+            if pat is None or pat.search(r["Kernel_Name"]):
+                durations.setdefault(r["Kernel_Name"], []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6)
 
-        def pick(db, sql):
-            rows = sqlite3.connect(db).execute(sql).fetchall()
-            return [r for r in rows if pat is None or pat.search(r[0])]
+        def per_dispatch(rows, counter):
+            by_kernel: dict[str, dict[str, float]] = {}
+            for r in rows:
+                if r["Counter_Name"] == counter and (pat is None or pat.search(r["Kernel_Name"])):
+                    d = by_kernel.setdefault(r["Kernel_Name"], {})
+                    d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+            return {k: statistics.median(v.values()) for k, v in by_kernel.items()}
 
-        kern = pick(dbs["trace"], "select name, duration from kernels")
-        fetch = pick(dbs["fetch"], "select kernel_name, value from counters_collection")
-        write = pick(dbs["write"], "select kernel_name, value from counters_collection")
-        if not kern or not fetch:
+        fetch = per_dispatch(found["fetch"], "FETCH_SIZE")
+        write = per_dispatch(found["write"], "WRITE_SIZE")
+        if not durations or not fetch:
             result["profiler_warning"] = "no matching kernels in the rocprofv3 output"
             return
-        dur_ms = statistics.median(r[1] for r in kern) / 1e6
-        fetched = statistics.median(r[1] for r in fetch) * 1024 * FETCH_SIZE_SCALE
-        written = statistics.median(r[1] for r in write) * 1024 if write else 0.0
+        dur_ms = sum(statistics.median(v) for v in durations.values())
+        fetched = sum(fetch.values()) * 1024 * FETCH_SIZE_SCALE
+        written = sum(write.values()) * 1024
         result.update({
             "bandwidth_fields_are_estimates": False,
             "measured_dram_bytes": fetched + written,
             "measured_achieved_bandwidth_gbps": (fetched + written) / (dur_ms * 1e-3) / 1e9,
             "measured_dram_throughput_pct": 100.0 * (fetched + written) / (dur_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
             "measured_kernel_duration_ms": dur_ms,
-            "measured_kernel_count": len(kern),
-            "measured_kernel_names": sorted({r[0] for r in kern}),
+            "measured_kernel_count": sum(len(v) for v in durations.values()),
+            "measured_kernel_names": sorted(durations),
             "profiler_metrics_source": "rocprofv3",
         })
 

@@ -323,24 +323,28 @@ class PagedKVAllocator:
 
     # -- helpers ------------------------------------------------------------------------------
     def _validate_kv(self, k: torch.Tensor, v: torch.Tensor, *, batch_expected: int | None) -> None:
-        if k.ndim != 4 or v.ndim != 4:
-            raise ValueError("KV must be [batch, heads, tokens, head_dim]")
+        """New tokens must be a pair of equal [batch, heads, tokens >= 1, head_dim] tensors on the pool's
+        device; every violation is a ValueError, as for the reference allocator (paged.py:201-213)."""
+
+        if (k.ndim, v.ndim) != (4, 4):
+            raise ValueError(f"new K/V must be 4-D [batch, heads, tokens, head_dim] (got {k.ndim}-D / {v.ndim}-D)")
         if k.shape != v.shape:
-            raise ValueError("K and V shapes must match")
-        if batch_expected is not None and k.shape[0] != batch_expected:
-            raise ValueError("KV batch dim must match request_ids")
-        if k.shape[1] != self.heads or k.shape[3] != self.head_dim:
-            raise ValueError("KV heads/head_dim must match the allocator")
-        if k.shape[2] <= 0:
-            raise ValueError("KV token dim must be non-empty")
-        if k.device != self.device or v.device != self.device:
-            raise ValueError("KV tensors must be on the allocator's device")
+            raise ValueError(f"new K and V differ in shape: {tuple(k.shape)} vs {tuple(v.shape)}")
+        expect = {0: batch_expected, 1: self.heads, 3: self.head_dim}
+        off = [f"dim {d} is {k.shape[d]}, expected {want}" for d, want in expect.items()
+               if want is not None and k.shape[d] != want]
+        if off:
+            raise ValueError("new K/V do not fit this pool (batch = requests, heads, head_dim): " + "; ".join(off))
+        if k.shape[2] < 1:
+            raise ValueError("new K/V hold no tokens")
+        if not (k.device == v.device == self.device):
+            raise ValueError(f"new K/V must live on {self.device} (got {k.device} / {v.device})")
 
     def _get_request(self, request_id: int) -> _RequestBlocks:
-        try:
-            return self._requests[int(request_id)]
-        except KeyError as exc:
-            raise KeyError(f"unknown request_id: {request_id}") from exc
+        request = self._requests.get(int(request_id))
+        if request is None:
+            raise KeyError(f"no live request with id {request_id}")
+        return request
 
     def _allocate_block(self) -> int:
         if not self._free_blocks:

@@ -272,7 +272,11 @@ class DecodeBatch:
         self._table_host = np.full((len(self._requests), cols), -1, dtype=np.int32)
         for i, r in enumerate(self._requests):
             self._table_host[i, : len(r.logical_blocks)] = r.logical_blocks
-        self._reserve(min(self.max_new_tokens, self.reserve_steps))
+        try:
+            self._reserve(min(self.max_new_tokens, self.reserve_steps))
+        except BaseException:
+            self._unreserve_all()
+            raise
         self.block_table = torch.empty((len(self._requests), cols), dtype=torch.int32, device=self.device)
         self._upload_table()
         lengths = torch.tensor(self.host_lengths, dtype=torch.int64)
@@ -296,6 +300,17 @@ class DecodeBatch:
                     self._taken.append(pg)
                     self._table_host[i, lp] = pg
         self._reserved_steps = max(self._reserved_steps, upto_step)
+
+    def _unreserve_all(self) -> None:
+        """Undo every reservation of this batch (a failed first reservation): the pages leave their
+        requests and go back to the front of the free list in the order they were taken."""
+
+        taken = set(self._taken)
+        for r in self._requests:
+            r.logical_blocks[:] = [pg for pg in r.logical_blocks if pg not in taken]
+        self.allocator._free_blocks[:0] = self._taken
+        self._taken = []
+        self._reserved_steps = 0
 
     def _upload_table(self) -> None:
         src = torch.from_numpy(self._table_host)

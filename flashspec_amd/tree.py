@@ -228,10 +228,7 @@ def _device_parents(parents: torch.Tensor, batch: int, nodes: int, dev: torch.de
     hit = _PARENTS_CACHE.get(key)
     if hit is not None:
         _PARENTS_CACHE.move_to_end(key)
-        tensor, made_on, ready = hit
-        if made_on != stream:
-            stream.wait_event(ready)
-        return tensor
+        return _reuse_on(hit, stream)
     validate_parents(parents, batch, nodes)
     tensor = host.pin_memory().to(dev, non_blocking=True)
     ready = torch.cuda.Event()
@@ -239,6 +236,22 @@ def _device_parents(parents: torch.Tensor, batch: int, nodes: int, dev: torch.de
     _PARENTS_CACHE[key] = (tensor, stream, ready)
     if len(_PARENTS_CACHE) > _PARENTS_CACHE_ENTRIES:
         _PARENTS_CACHE.popitem(last=False)
+    return tensor
+
+
+def _reuse_on(entry: tuple, stream) -> torch.Tensor:
+    """A cached device copy ``(tensor, made_on, ready)`` used on ``stream``.
+
+    On another stream than the one that made it, the stream first waits for the copy, and
+    ``record_stream`` tells the caching allocator that ``stream`` uses the memory: once the
+    entry is evicted, the block is then not handed out again until the kernels queued on
+    ``stream`` up to that point have finished reading it.
+    """
+
+    tensor, made_on, ready = entry
+    if made_on != stream:
+        stream.wait_event(ready)
+        tensor.record_stream(stream)
     return tensor
 
 

@@ -22,6 +22,7 @@ from oracle import quant as oq
 from tests._helpers import (
     assert_attention_close,
     assert_quant_equal,
+    cast_like_q,
     from_cache,
     from_qt,
     golden_cache,
@@ -540,19 +541,33 @@ def test_repeated_calls_are_bit_identical():
 
 
 def test_unallocated_pages_and_lengths_past_the_table_are_masked():
-    """-1 table entries and lengths beyond max_seq_len follow the Triton kernel's masking."""
+    """A -1 table entry inside a row's length: the HIP kernel masks that page's tokens (the
+    reference Triton kernel's semantics, triton_paged.py:219-232), whereas the reference PyTorch
+    path reads physical page 0 there (paged.py:441, ``block_table.clamp_min(0)``).  Both are run
+    on the same cache: rows without such an entry match the oracle; the affected row equals the
+    oracle's attention over the backed tokens only, and differs from the page-0 reading.  A length
+    past max_seq_len is clamped to it, as in both reference paths."""
 
     announce("table -1 entries / clamped lengths")
     q, cache = _paged_case(2, 4, 64, 128, 16, seed=41)
     table = cache.block_table.clone()
-    table[1, 2:] = -1  # row 1 keeps only 32 tokens of backing pages
-    lengths = torch.tensor([999, 32], device=DEV)  # row 0 clamps to max_seq_len
+    table[1, 1] = -1  # row 1: tokens [16, 32) have no backing page
+    lengths = torch.tensor([999, 64], device=DEV)  # row 0 clamps to max_seq_len
     masked = fa.PagedKVCache(cache.k_quant, cache.v_quant, table, lengths, 16, 64)
     got = fa.paged_quant_attention_triton(q.to(DEV), masked)
     sync()
-    trimmed = fa.PagedKVCache(cache.k_quant, cache.v_quant, cache.block_table, torch.tensor([64, 32], device=DEV),
-                              16, 64)
-    assert_attention_close(got, oracle_paged_attention(q, trimmed), torch.float16, "masked")
+    # the reference PyTorch path on the identical cache (page 0 read for the -1 entry)
+    same = oracle_paged_attention(q, masked)
+    assert_attention_close(got[:1], same[:1], torch.float16, "row without -1 entries")
+    # row 1 as documented: attention over tokens [0, 16) and [32, 64) only
+    dense = op.to_dense(from_cache(masked))
+    keep = np.r_[0:16, 32:64]
+    k1 = dense[0][1:2][:, :, keep]
+    v1 = dense[1][1:2][:, :, keep]
+    want = oa.reference_attention(np_of(q)[1:2].astype(np.float32), k1, v1)
+    assert_attention_close(got[1:], want, torch.float16, "row with a -1 entry")
+    diverge = np.abs(got[1:].float().cpu().numpy() - cast_like_q(same[1:], torch.float16)).max()
+    assert diverge > 1e-2, "the page-0 reading of the reference PyTorch path should differ on this row"
 
 
 def test_graph_replay_matches_eager():

@@ -131,3 +131,25 @@ def test_simulation_counts_arrivals_and_finishes():
     assert res["generated_tokens"] == 15
     assert res["live_requests"] == 3.0
     assert res["attention_backend"] == "portable"
+
+
+def test_decode_batch_failed_reservation_leaves_allocator_unchanged():
+    """Opening a batch whose first reservation runs out of pages raises and hands every page it
+    took back: free list (order included), request pages and stats are as before."""
+
+    alloc = fa.PagedKVAllocator(capacity_blocks=5, heads=2, head_dim=8, block_size=4)
+    for rid in range(3):
+        k, v = _pair(rid, (1, 2, 4, 8))  # one full page each
+        alloc.add_request(rid, k, v)
+    free_before = list(alloc._free_blocks)
+    pages_before = {rid: list(alloc._get_request(rid).logical_blocks) for rid in range(3)}
+    stats_before = alloc.stats()
+    with pytest.raises(RuntimeError, match="out of physical blocks"):
+        DecodeBatch(alloc, [0, 1, 2], max_new_tokens=4)
+    assert alloc._free_blocks == free_before
+    assert {rid: alloc._get_request(rid).logical_blocks for rid in range(3)} == pages_before
+    assert alloc.stats() == stats_before
+    # the pool still serves a batch that fits
+    batch = DecodeBatch(alloc, [0, 1], max_new_tokens=4)
+    batch.close()
+    assert alloc._free_blocks == free_before

@@ -72,3 +72,30 @@ def test_tree_shape_counts():
     shape = tree_shape(torch.tensor([[-1, 0, 0, 1, -1, 4], [-1, 0, 1, 2, 3, 4]]))
     assert shape == {"depth": 6, "leaves": 3, "max_branch": 2}
     assert tree_shape(torch.tensor([[-1, -1, -1]])) == {"depth": 1, "leaves": 3, "max_branch": 3}
+
+
+def test_parents_cache_hit_on_another_stream_records_that_stream():
+    """A cached parents copy reused on a second stream waits for the copy and is registered with
+    the caching allocator for that stream (record_stream); on its own stream neither happens."""
+
+    from flashspec_amd.tree import _reuse_on
+
+    class Stream:
+        def __init__(self, name):
+            self.name, self.waited = name, []
+
+        def wait_event(self, ev):
+            self.waited.append(ev)
+
+    class Tensor:
+        def __init__(self):
+            self.recorded = []
+
+        def record_stream(self, s):
+            self.recorded.append(s)
+
+    made_on, other, ready, t = Stream("made"), Stream("other"), object(), Tensor()
+    assert _reuse_on((t, made_on, ready), made_on) is t
+    assert t.recorded == [] and made_on.waited == []
+    assert _reuse_on((t, made_on, ready), other) is t
+    assert other.waited == [ready] and t.recorded == [other]
