@@ -64,8 +64,8 @@ def test_microbench_triton_paged_backend(layout):
                        "--repeats", "5")
     _check_hip_result(data, "triton_paged", 8, 2048)
     assert data["paged_layout"] == layout
-    # int8 K/V + fp32 scale + int16 zero per 16-token page and head
-    assert data["estimated_quant_kv_bytes"] == 2 * (8 * 32 * 2048 * 128 + 8 * 32 * 128 * 6)
+    # int8 K/V + fp32 scale + int16 zero per 16-token page and head, + int64 table and lengths
+    assert data["estimated_quant_kv_bytes"] == 2 * (8 * 32 * 2048 * 128 + 8 * 32 * 128 * 6) + 8 * 128 * 8 + 8 * 8
 
 
 def test_microbench_triton_fused_backend_c1():
@@ -104,7 +104,7 @@ def test_microbench_profile_rocprof_backfills_measured_fields():
     assert data["bandwidth_fields_are_estimates"] is False
     assert data["profiler_metrics_source"] == "rocprofv3"
     assert any("decode_rows_kernel" in n for n in data["measured_kernel_names"])
-    algorithmic = data["estimated_quant_kv_bytes"] + 2 * 8 * 32 * 128 * 2 + 8 * 128 * 8 + 8 * 8
+    algorithmic = data["estimated_quant_kv_bytes"] + 2 * 8 * 32 * 128 * 2  # + fp16 q and output
     ratio = data["measured_dram_bytes"] / algorithmic
     print(f"measured / algorithmic bytes = {ratio:.4f}, kernel {data['measured_kernel_duration_ms'] * 1e3:.2f} us",
           flush=True)
