@@ -37,6 +37,13 @@ _SIGNATURES = {
          c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float,
          c_int, c_int, c_int, c_void_p],
     ),
+    "fs_paged_decode_i8_noalloc": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
+         c_void_p, c_void_p, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int,
+         c_void_p],
+    ),
+    "fs_noalloc_scratch_bytes": (c_int64, []),
     "fs_tree_verify_i8": (
         c_int,
         [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,

@@ -110,6 +110,29 @@ int fs_paged_decode_i8(const void* q, int q_dtype,
                        int split_tiles, int max_splits, int waves_per_block, void* stream);
 
 /*
+ * fs_paged_decode_i8 without a workspace argument, for callers that cannot allocate device
+ * memory (code under graph capture, serving loops that forbid allocation).  No counterpart in
+ * the reference.  When rows split (max_splits > 1) the split-K partials go to a device array
+ * inside the library, one per GPU, of fs_noalloc_scratch_bytes() bytes (16 MiB), and this call
+ * also launches the split merge (no separate fs_combine_splits).  Plans whose partials,
+ * fs_decode_workspace_bytes(batch*heads, max_splits, head_dim), exceed that size are rejected
+ * with FS_ERR_INVALID.  Nothing needs clearing between calls: every split writes its partials
+ * before the merge reads them.  All calls on one GPU share its array: calls that overlap on one
+ * GPU (other streams, other host threads) race.
+ */
+int fs_paged_decode_i8_noalloc(const void* q, int q_dtype,
+                               const int8_t* k_values, const float* k_scale, const int16_t* k_zero,
+                               const int8_t* v_values, const float* v_scale, const int16_t* v_zero,
+                               const void* block_table, int table_index_bytes, int64_t table_cols,
+                               const int64_t* lengths, void* out,
+                               int batch, int heads, int head_dim, int64_t num_pages,
+                               int page_size, int quant_block, int max_seq_len, float sm_scale,
+                               int split_tiles, int max_splits, int waves_per_block, void* stream);
+
+/* Bytes of the device array behind fs_paged_decode_i8_noalloc (per GPU). */
+int64_t fs_noalloc_scratch_bytes(void);
+
+/*
  * Speculative-decoding tree verification over a paged INT8 prefix.  Request b has `nodes`
  * draft nodes in topological order; node n attends to the prefix tokens [0, lengths[b]) of
  * the paged cache and to the draft tokens on its path to the root (n, parents[b, n],

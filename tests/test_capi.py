@@ -99,3 +99,18 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert rc == _lib.FS_ERR_INVALID and "differ" in lib.fs_last_error().decode()
     rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 2, 4, 7, 9, 2, 2, 64, 16, None)
     assert rc == _lib.FS_ERR_INVALID and "int32 or int64" in lib.fs_last_error().decode()
+
+
+def test_no_alloc_entry_point_rejects_plans_beyond_its_array():
+    """fs_paged_decode_i8_noalloc checks the partials' size against its per-GPU array before any
+    HIP call (no GPU needed)."""
+
+    lib = _lib.require()
+    assert lib.fs_noalloc_scratch_bytes() == 16 << 20
+    # 256 rows x 1024 splits x (128 + 2) floats = 136 MB of partials
+    rc = lib.fs_paged_decode_i8_noalloc(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 8, 32, 128, 64, 16, 16, 16384,
+                                        0.1, 1, 1024, 1, None)
+    assert rc == _lib.FS_ERR_INVALID and "at most" in lib.fs_last_error().decode()
+    rc = lib.fs_paged_decode_i8_noalloc(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 0, 32, 128, 64, 16, 16, 16384,
+                                        0.1, 1, 2, 1, None)
+    assert rc == _lib.FS_ERR_INVALID
