@@ -210,6 +210,41 @@ def test_config2_symmetric_per_token_split_k(monkeypatch):
         assert_attention_close(got[b:b + 1], ref, torch.float16, f"request {b}")
 
 
+def test_config2_affine_per_block_split_k(monkeypatch):
+    """Config C2 in the reference's own format: B8 H32 S4096 D128, affine per-block INT8 (16-token
+    blocks, quantized by the HIP quantizer and checked bit-exact against the oracle quantizer on the
+    sampled requests), num_splits=4 with the fp32 LSE merge (reference triton_fused.py:697-744 and
+    its split test tests/test_flashspec.py:107-125); rows of two requests against the oracle."""
+
+    announce("config 2 affine per-block split-K B8 H32 S4096 D128")
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", "4")
+    B, H, S, D = 8, 32, 4096, 128
+    g = torch.Generator(device=DEV)
+    g.manual_seed(6)
+    q = torch.randn((B, H, D), generator=g, device=DEV, dtype=torch.float16)
+    k = torch.randn((B, H, S, D), generator=g, device=DEV, dtype=torch.float16)
+    v = torch.randn((B, H, S, D), generator=g, device=DEV, dtype=torch.float16)
+    kq, vq = fa.quantize_int8_per_block(k, 16), fa.quantize_int8_per_block(v, 16)
+    got, stats = fa.fused_dequant_attention_triton(q, kq, vq, return_stats=True)
+    sync()
+    assert stats["num_splits"] == 4.0 and stats["materializes_dense_kv"] == 0.0
+    for b in (1, 6):
+        rk = oq.quantize_int8_per_block(np_of(k[b:b + 1].float()), 16)
+        rv = oq.quantize_int8_per_block(np_of(v[b:b + 1].float()), 16)
+        for name, ours, ref in (("K", kq, rk), ("V", vq, rv)):
+            assert np.array_equal(ours.values[b:b + 1].cpu().numpy(), ref.values), f"{name} values request {b}"
+            assert np.array_equal(ours.scale[b:b + 1].cpu().numpy().view(np.uint32),
+                                  np.asarray(ref.scale, np.float32).view(np.uint32)), f"{name} scales request {b}"
+            assert np.array_equal(ours.zero_point[b:b + 1].cpu().numpy(), ref.zero_point), f"{name} zeros {b}"
+        ref = oa.fused_dequant_attention(np_of(q[b:b + 1].float()), rk, rv, None)
+        assert_attention_close(got[b:b + 1], ref, torch.float16, f"request {b}")
+    # the split plan agrees with one split on the whole batch
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", "1")
+    one = fa.fused_dequant_attention_triton(q, kq, vq)
+    sync()
+    assert (got.float() - one.float()).abs().max().item() <= 2e-3
+
+
 # ---- paged cache construction, append, allocator ----------------------------------------------
 
 @pytest.mark.parametrize("layout", ["contiguous", "shuffled", "interleaved"])
