@@ -333,7 +333,11 @@ def serving_step_bench(torch, fa, dev, steps: int, warmup: int) -> dict:
 
 def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
     """quantize_int8_per_block of one fp16 K tensor of the metric workload ([8, 32, 4096, 128],
-    16-token blocks), input resident in HBM; bytes = fp16 read + int8 write + scale/zero write."""
+    16-token blocks), input resident in HBM; bytes = fp16 read + int8 write + scale/zero write.
+    Beside it, the practical ceiling of that traffic on the same GPU: a streaming 2:1 copy of
+    the same tensor (`fs_stream_copy_half`)."""
+
+    from flashspec_amd import _lib
 
     g = torch.Generator(device=dev)
     g.manual_seed(5)
@@ -341,21 +345,43 @@ def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
     ms = time_loop(torch, lambda i: fa.quantize_int8_per_block(xs[i % 2], PAGE), calls, 3)
     groups = B * H * (S // PAGE)
     nbytes = B * H * S * D * (2 + 1) + groups * 6
-    del xs
+    # the same traffic with no arithmetic: fs_stream_copy_half reads the fp16 tensor and writes
+    # half as many bytes, best of a few grid sizes
+    lib = _lib.require()
+    dst = torch.empty(B * H * S * D, dtype=torch.int8, device=dev)
+    src_bytes = xs[0].numel() * 2
+    stream = _lib.stream_ptr(dev)
+    best = None
+    for blocks in (2048, 4096, 8192):
+        cms = time_loop(torch, lambda i: _lib.check(lib.fs_stream_copy_half(
+            xs[i % 2].data_ptr(), src_bytes, dst.data_ptr(), blocks, stream)), calls, 3)
+        if best is None or cms < best[0]:
+            best = (cms, blocks)
+    copy_bytes = src_bytes + src_bytes // 2
+    copy_gbps = copy_bytes / (best[0] * 1e-3) / 1e9
+    del xs, dst
+    gbps = nbytes / (ms * 1e-3) / 1e9
     return {"workload": f"quantize_int8_per_block fp16 [{B}, {H}, {S}, {D}], block {PAGE}",
             "us_per_call": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
-            "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1)}
+            "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 1),
+            "copy_ceiling": {"kernel": "stream_copy_half_kernel", "bytes": copy_bytes, "us": round(best[0] * 1e3, 2),
+                             "gbps": round(copy_gbps, 1), "workgroups": best[1]},
+            "frac_of_copy_ceiling": round(gbps / copy_gbps, 4)}
 
 
 # Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths
-# [, format]); quant block 1 = symmetric absmax INT8 with one scale per token
+# [, format [, page layout]]); quant block 1 = symmetric absmax INT8 with one scale per token
 # (quantize_int8_symmetric_per_token), or one FP8 scale per token with format "fp8"; format
-# "channel" = per-channel affine INT8 (quantize_int8_per_channel).
+# "channel" = per-channel affine INT8 (quantize_int8_per_channel); page layout = from_dense's
+# block_table_pattern (contiguous by default).
 SHAPES = [
     ("metric", 8, 32, 4096, 128, 16, 16, "float16", None),
     ("c1_affine", 4, 32, 2048, 128, 16, 16, "float16", None),
     ("c3_s2048", 8, 32, 2048, 128, 16, 16, "float16", None),
     ("c4_descending_tail", 16, 32, 4096, 128, 16, 16, "float16", [4096 - 256 * i - 7 for i in range(16)]),
+    ("c4_shuffled", 16, 32, 4096, 128, 16, 16, "float16", [4096 - 256 * i for i in range(16)], "int8", "shuffled"),
+    ("c4_interleaved", 16, 32, 4096, 128, 16, 16, "float16", [4096 - 256 * i for i in range(16)], "int8",
+     "interleaved"),
     ("head_dim_64", 8, 32, 4096, 64, 16, 16, "float16", None),
     ("head_dim_256", 8, 32, 4096, 256, 16, 16, "float16", None),
     ("page_32_quant_16", 8, 32, 4096, 128, 32, 16, "float16", None),
@@ -417,6 +443,7 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int, only=None) -> list[dic
         if only and name not in only:
             continue
         fmt = rest[0] if rest else "int8"
+        layout = rest[1] if len(rest) > 1 else "contiguous"
         g = torch.Generator(device=dev)
         g.manual_seed(11)
         qdtype = getattr(torch, qdt)
@@ -452,7 +479,7 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int, only=None) -> list[dic
                 kq, vq = fa.quantize_int8_symmetric_per_token(k), fa.quantize_int8_symmetric_per_token(v)
             else:
                 if qb == page:
-                    cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt)
+                    cache = fa.PagedKVCache.from_dense(k, v, block_size=page, lengths=lt, block_table_pattern=layout)
                 else:
                     cache = paged_from_blocks(torch, fa, k, v, page, qb, lt)
                 kq = fa.quantize_int8_per_block(k, qb)
@@ -462,7 +489,7 @@ def shapes_bench(torch, fa, dev, steps: int, warmup: int, only=None) -> list[dic
         ms = time_loop(torch, lambda i: fa.paged_quant_attention_triton(sets[i % n_sets][0], sets[i % n_sets][1]),
                        steps, warmup)
         _, st = fa.paged_quant_attention_triton(sets[0][0], sets[0][1], return_stats=True)
-        row = {"shape": name, "format": fmt, "batch": b, "heads": h, "seq_len": s, "head_dim": d, "page": page,
+        row = {"shape": name, "format": fmt, "layout": layout, "batch": b, "heads": h, "seq_len": s, "head_dim": d, "page": page,
                "quant_block": qb, "q_dtype": qdt, "paged_us": round(ms * 1e3, 2), "paged_pct_of_peak": round(
                    100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 1),
                "tiled_path": bool(st["tiled_path"]), "num_splits": st["num_splits"], "waves": st["num_warps"],
