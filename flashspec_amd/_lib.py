@@ -37,6 +37,18 @@ _SIGNATURES = {
          c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float,
          c_int, c_int, c_int, c_void_p],
     ),
+    "fs_decode_merge_area_bytes": (c_int64, [c_int64, c_int64, c_int64]),
+    "fs_fused_decode_merged": (
+        c_int,
+        [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+    ),
+    "fs_paged_decode_merged": (
+        c_int,
+        [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+         c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int, c_int, c_int, c_float,
+         c_int, c_int, c_int, c_void_p],
+    ),
     "fs_paged_decode_i8_noalloc": (
         c_int,
         [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
@@ -85,6 +97,7 @@ _SIGNATURES = {
     ),
     "fs_decode_tiled_path_channel": (c_int, [c_int, c_int, c_int]),
     "fs_stream_read": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p]),
+    "fs_stream_copy_half": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_void_p]),
     "fs_quantize_fp8": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fs_quantize_pages_fp8": (
         c_int,

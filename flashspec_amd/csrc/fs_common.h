@@ -109,6 +109,18 @@ __device__ __forceinline__ float wave_max_valu(float x) {
   return fmaxf(r32.a, r32.b);
 }
 
+// Minimum over the whole wave, every lane getting the same bits.
+__device__ __forceinline__ float wave_min_valu(float x) {
+  x = fminf(x, dpp_f32<kDppQuadXor1>(x));
+  x = fminf(x, dpp_f32<kDppQuadXor2>(x));
+  x = fminf(x, dpp_f32<kDppRowHalfMirror>(x));
+  x = fminf(x, dpp_f32<kDppRowMirror>(x));
+  const LanePair r16 = swap16(x, x);
+  x = fminf(r16.a, r16.b);
+  const LanePair r32 = swap32(x, x);
+  return fminf(r32.a, r32.b);
+}
+
 __device__ __forceinline__ int readlane_i32(int x, int lane) { return __builtin_amdgcn_readlane(x, lane); }
 __device__ __forceinline__ float readlane_f32(float x, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));

@@ -484,9 +484,152 @@ __device__ __forceinline__ float allreduce_groups(float x) {
 
 // The NW wave states of one workgroup (LDS: acc [NW][DP], (m, l) [NW]) merged into the row's output,
 // or into the split partials (m, l, acc) when the row has several splits.
+// ---- in-kernel split merge ------------------------------------------------------------------------
+// A row's split workgroups each publish their state (acc[D], m, l) as 64-bit words tagged 1 in the
+// upper half, with relaxed agent-scope atomic stores, then count themselves in with a relaxed
+// atomic add, with the first other splits' words already requested.  The last to arrive reads every
+// other split's words, waiting on each word's own tag rather than on a fence (a word is visible
+// whole or not at all, whatever the order in which the stores land), merges the splits in split
+// order, writes the row, and stores zeros over every word it used and over the count, so the area
+// is all zero again when the kernel ends.  Nobody waits for
+// a workgroup that has not yet arrived; the waits end within the latency of stores already issued
+// (bounded by kMergeSpins regardless, after which the row is written as NaN).
+constexpr int kMergeSpins = 1 << 14;
+
+__device__ __forceinline__ void publish(unsigned long long* w, float x) {
+  __hip_atomic_store(w, (1ull << 32) | __float_as_uint(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void clear_word(unsigned long long* w) {
+  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long load_word(const unsigned long long* w) {
+  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The value of word w, given a first load v of it: reloads until the tag is set.
+__device__ __forceinline__ float settle_word(unsigned long long v, const unsigned long long* w, bool& ok) {
+  for (int n = 0; (v >> 32) != 1ull && n < kMergeSpins; ++n) {
+    __builtin_amdgcn_s_sleep(1);
+    v = load_word(w);
+  }
+  ok = ok && (v >> 32) == 1ull;
+  return __uint_as_float((unsigned)v);
+}
+
+// Thread tid holds dims tid + k * blockDim.x (k < DPT) of its split's un-normalized state a[k], with
+// the split's max M (log2 units) and denominator L.
+template <int DPT, typename QT>
+__device__ __forceinline__ void merge_splits_here(const DecodeParams& p, int* s_last, int row, int split, int nsplit,
+                                                  int D, float M, float L, const float (&a)[DPT]) {
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const size_t rs = (size_t)D + 2;
+  unsigned long long* slots = p.merge_slots + (size_t)row * p.max_splits * rs;
+  unsigned long long* own = slots + (size_t)split * rs;
+#pragma unroll
+  for (int k = 0; k < DPT; ++k) {
+    const int d = tid + k * nthr;
+    if (d < D) publish(own + d, a[k]);
+  }
+  if (tid == 0) {
+    publish(own + D, M);
+    publish(own + D + 1, L);
+  }
+  // the first group of the other splits' words is loaded before the count comes back: the last
+  // arrival then usually finds them landed (its partners published before they counted themselves
+  // in); the others drop them.  Only threads that hold dims (tid < D) take part in the merge.
+  const bool holds = tid < D;
+  constexpr int G = 4;
+  unsigned long long v[G][DPT + 2];
+  auto load_group = [&](int s0) {
+#pragma unroll
+    for (int c = 0; c < G; ++c) {
+      const int s = s0 + c;
+      const unsigned long long* ws = slots + (size_t)s * rs;
+      const bool other = holds && s < nsplit && s != split;
+      v[c][0] = other ? load_word(ws + D) : 0ull;
+      v[c][1] = other ? load_word(ws + D + 1) : 0ull;
+#pragma unroll
+      for (int k = 0; k < DPT; ++k) {
+        const int d = tid + k * nthr;
+        v[c][2 + k] = other && d < D ? load_word(ws + d) : 0ull;
+      }
+    }
+  };
+  load_group(0);
+  __syncthreads();  // every word of this split is on its way before it counts itself in
+  if (tid == 0)
+    *s_last = __hip_atomic_fetch_add(p.merge_count + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (unsigned)(nsplit - 1);
+  __syncthreads();
+  if (!*s_last) return;  // the whole workgroup
+  if (holds) {
+    bool ok = true;
+    float Mr = kNegBig, Lr = 0.f, ar[DPT];
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) ar[k] = 0.f;
+    // splits in groups of G, merged in split order; words not yet landed are loaded again
+    for (int s0 = 0; s0 < nsplit; s0 += G) {
+      if (s0 > 0) load_group(s0);
+#pragma unroll
+      for (int c = 0; c < G; ++c) {
+        const int s = s0 + c;
+        if (s >= nsplit) break;
+        float m = M, l = L, x[DPT];
+#pragma unroll
+        for (int k = 0; k < DPT; ++k) x[k] = a[k];
+        if (s != split) {
+          const unsigned long long* ws = slots + (size_t)s * rs;
+          m = settle_word(v[c][0], ws + D, ok);
+          l = settle_word(v[c][1], ws + D + 1, ok);
+#pragma unroll
+          for (int k = 0; k < DPT; ++k) {
+            const int d = tid + k * nthr;
+            x[k] = d < D ? settle_word(v[c][2 + k], ws + d, ok) : 0.f;
+          }
+        }
+        const float mn = fmaxf(Mr, m);
+        const float e1 = fast_exp2(Mr - mn), e2 = fast_exp2(m - mn);
+        Lr = Lr * e1 + l * e2;
+#pragma unroll
+        for (int k = 0; k < DPT; ++k) ar[k] = ar[k] * e1 + x[k] * e2;
+        Mr = mn;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int d = tid + k * nthr;
+      if (d < D) {
+        const float o = Lr > 0.f ? ar[k] / Lr : 0.f;
+        ((QT*)p.out)[(size_t)row * D + d] = from_f32<QT>(ok ? o : __builtin_nanf(""));
+      }
+    }
+  }
+  // leave the area zero: every word of the row's splits, then the count.  Each thread clears the
+  // dim words it read itself; thread 0 clears the (m, l) words, which every thread holding dims
+  // reads, so all of them must have read them first.
+  __syncthreads();
+  if (holds) {
+    for (int s = 0; s < nsplit; ++s) {
+      unsigned long long* ws = slots + (size_t)s * rs;
+#pragma unroll
+      for (int k = 0; k < DPT; ++k) {
+        const int d = tid + k * nthr;
+        if (d < D) clear_word(ws + d);
+      }
+      if (tid == 0) {
+        clear_word(ws + D);
+        clear_word(ws + D + 1);
+      }
+    }
+  }
+  if (tid == 0) __hip_atomic_store(p.merge_count + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int NW, int DP, typename QT>
-__device__ __forceinline__ void merge_waves(const DecodeParams& p, const float* s_acc, const float* s_ml, int row,
-                                            int split, int nsplit, int D) {
+__device__ __forceinline__ void merge_waves(const DecodeParams& p, const float* s_acc, const float* s_ml, int* s_last,
+                                            int row, int split, int nsplit, int D) {
   float mv[NW], lv[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
@@ -503,6 +646,21 @@ __device__ __forceinline__ void merge_waves(const DecodeParams& p, const float* 
   for (int w = 0; w < NW; ++w) {
     ew[w] = fast_exp2(mv[w] - M);
     L = fmaf(lv[w], ew[w], L);
+  }
+  if (nsplit > 1 && p.merge_count != nullptr && !p.force_partials) {
+    constexpr int DPT = (DP + NW * kWave - 1) / (NW * kWave);  // dims per thread
+    float a[DPT];
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int d = threadIdx.x + k * blockDim.x;
+      a[k] = 0.f;
+      if (d < D) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) a[k] = fmaf(s_acc[w * DP + d], ew[w], a[k]);
+      }
+    }
+    merge_splits_here<DPT, QT>(p, s_last, row, split, nsplit, D, M, L, a);
+    return;
   }
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float x[NW];
@@ -544,6 +702,7 @@ decode_rows_kernel(const DecodeParams p) {
   constexpr int WMAX = max_tiled_waves(DP, QM);
   __shared__ __attribute__((aligned(16))) float s_acc[WMAX * DP];
   __shared__ __attribute__((aligned(16))) float s_ml[2 * WMAX];
+  __shared__ int s_last;
 
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform by construction; readfirstlane lets the compiler keep everything derived
@@ -785,17 +944,17 @@ decode_rows_kernel(const DecodeParams p) {
   // merge the W waves: weights exp2(m_w - M), in wave order (bit-reproducible); the wave count is
   // a compile-time constant there, so each thread issues all its LDS reads together
   switch (W) {
-    case 1: merge_waves<1, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D); break;
-    case 2: merge_waves<2, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D); break;
-    case 4: merge_waves<4, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D); break;
+    case 1: merge_waves<1, DP, QT>(p, s_acc, s_ml, &s_last, row, split, nsplit, D); break;
+    case 2: merge_waves<2, DP, QT>(p, s_acc, s_ml, &s_last, row, split, nsplit, D); break;
+    case 4: merge_waves<4, DP, QT>(p, s_acc, s_ml, &s_last, row, split, nsplit, D); break;
     default:
       if constexpr (WMAX >= 16) {
         if (W == 16) {
-          merge_waves<16, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D);
+          merge_waves<16, DP, QT>(p, s_acc, s_ml, &s_last, row, split, nsplit, D);
           break;
         }
       }
-      merge_waves<8, DP, QT>(p, s_acc, s_ml, row, split, nsplit, D);
+      merge_waves<8, DP, QT>(p, s_acc, s_ml, &s_last, row, split, nsplit, D);
       break;
   }
 }
@@ -1053,6 +1212,21 @@ static void bind_workspace(DecodeParams& p, void* workspace) {
   p.part_ml = workspace ? (float*)workspace + (size_t)p.rows * p.max_splits * p.head_dim : nullptr;
 }
 
+// Merge area layout: arrival counts [rows] (padded to 256 bytes), then tagged partial states
+// [rows, max_splits, head_dim + 2] as 64-bit words.
+static int bind_merge_area(DecodeParams& p, void* area, int64_t area_bytes) {
+  if (p.max_splits <= 1) return FS_OK;  // one split: rows are written directly
+  if (area == nullptr) return set_error(FS_ERR_INVALID, "merge area required when rows split");
+  if ((uintptr_t)area % 256 != 0) return set_error(FS_ERR_INVALID, "merge area must be 256-byte aligned");
+  const int64_t need = merge_area_bytes(p.rows, p.max_splits, p.head_dim);
+  if (area_bytes < need)
+    return set_error(FS_ERR_INVALID, "merge area too small (" + std::to_string(area_bytes) + " < " +
+                                         std::to_string(need) + " bytes)");
+  p.merge_count = (unsigned*)area;
+  p.merge_slots = (unsigned long long*)((char*)area + ((int64_t)p.rows * 4 + 255) / 256 * 256);
+  return FS_OK;
+}
+
 static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, int64_t workspace_bytes,
                         bool row_kernel = true) {
   if (p.rows <= 0 || p.heads <= 0) return set_error(FS_ERR_INVALID, "batch and heads must be positive");
@@ -1088,7 +1262,10 @@ static int check_common(const DecodeParams& p, bool tiled, int waves_per_block, 
   if (!p.q || !p.kv[0] || !p.kv[1] || !p.sc[0] || !p.sc[1] || !p.out ||
       (p.vfmt == kVfInt8 && (!p.zp[0] || !p.zp[1])))
     return set_error(FS_ERR_INVALID, "null tensor pointer");
-  if (p.max_splits > 1 || p.force_partials) {
+  if (p.merge_count != nullptr) {
+    if (!tiled) return set_error(FS_ERR_INVALID, "the in-kernel split merge needs the tiled decode path");
+    if (p.force_partials) return set_error(FS_ERR_INVALID, "the in-kernel split merge writes rows, not partials");
+  } else if (p.max_splits > 1 || p.force_partials) {
     const int64_t need = fs_decode_workspace_bytes(p.rows, p.max_splits, p.head_dim);
     if (workspace_bytes < need || p.part_acc == nullptr)
       return set_error(FS_ERR_INVALID, "split-K workspace too small (" + std::to_string(workspace_bytes) +
@@ -1118,7 +1295,7 @@ static int fused_decode(const void* q, int q_dtype, const int8_t* k_values, cons
                         const int64_t* lengths, void* out, void* workspace, int64_t workspace_bytes, int batch,
                         int heads, int head_dim, int seq_len, int n_blocks, int block_size, float sm_scale,
                         int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream,
-                        int per_channel = 0) {
+                        int per_channel = 0, void* merge_area = nullptr, int64_t merge_bytes = -1) {
   DecodeParams p{};
   p.vfmt = vfmt;
   p.per_channel = per_channel;
@@ -1135,6 +1312,9 @@ static int fused_decode(const void* q, int q_dtype, const int8_t* k_values, cons
   p.qk_scale = sm_scale * kLog2e;
   if (batch <= 0) return set_error(FS_ERR_INVALID, "batch must be positive");
   bind_workspace(p, workspace);
+  if (merge_bytes >= 0) {
+    if (int rc = bind_merge_area(p, merge_area, merge_bytes)) return rc;
+  }
   const bool tiled = tiled_path(head_dim, block_size, block_size, per_channel != 0);
   if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes)) return rc;
   if (block_size <= 0 || n_blocks <= 0 || (int64_t)n_blocks * block_size < seq_len)
@@ -1173,7 +1353,7 @@ int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* 
                         void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads,
                         int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
                         float sm_scale, int split_tiles, int max_splits, int waves_per_block,
-                        bool row_kernel, int vfmt, int per_channel) {
+                        bool row_kernel, int vfmt, int per_channel, void* merge_area, int64_t merge_bytes) {
   p = DecodeParams{};
   p.vfmt = vfmt;
   p.per_channel = per_channel;
@@ -1193,6 +1373,9 @@ int fs::paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* 
   if (batch <= 0 || nq <= 0) return set_error(FS_ERR_INVALID, "batch and nodes must be positive");
   if ((int64_t)batch * nq * heads > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "too many query rows");
   bind_workspace(p, workspace);
+  if (merge_bytes >= 0) {
+    if (int rc = bind_merge_area(p, merge_area, merge_bytes)) return rc;
+  }
   tiled = tiled_path(head_dim, page_size, quant_block, per_channel != 0);
   if (int rc = check_common(p, tiled, waves_per_block, workspace_bytes, row_kernel)) return rc;
   if (!block_table || !lengths) return set_error(FS_ERR_INVALID, "block_table and lengths are required");
@@ -1212,13 +1395,13 @@ static int paged_decode(const void* q, int q_dtype, const int8_t* k_values, cons
                         void* out, void* workspace, int64_t workspace_bytes, int batch, int heads, int head_dim,
                         int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale,
                         int split_tiles, int max_splits, int waves_per_block, int vfmt, void* stream,
-                        int per_channel = 0) {
+                        int per_channel = 0, void* merge_area = nullptr, int64_t merge_bytes = -1) {
   DecodeParams p;
   bool tiled = false;
   if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
                             table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, 1, heads,
                             head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
-                            max_splits, waves_per_block, true, vfmt, per_channel))
+                            max_splits, waves_per_block, true, vfmt, per_channel, merge_area, merge_bytes))
     return rc;
   return launch_decode<true>(p, q_dtype, tiled, waves_per_block, (hipStream_t)stream);
 }
@@ -1271,6 +1454,50 @@ extern "C" int fs_paged_decode_fp8(const void* q, int q_dtype, const uint8_t* k_
                       nullptr, block_table, table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes,
                       batch, heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
                       max_splits, waves_per_block, kVfFp8, stream);
+}
+
+extern "C" int64_t fs_decode_merge_area_bytes(int64_t rows, int64_t max_splits, int64_t head_dim) {
+  return merge_area_bytes(rows, max_splits, head_dim);
+}
+
+// kv_format: 0 = affine INT8 per block or token, 1 = FP8 E4M3 (zero arrays unused), 2 = per-channel
+// affine INT8.
+static int kv_format_of(int kv_format, int& vfmt, int& per_channel) {
+  if (kv_format < 0 || kv_format > 2) return set_error(FS_ERR_INVALID, "kv_format must be 0, 1 or 2");
+  vfmt = kv_format == 1 ? kVfFp8 : kVfInt8;
+  per_channel = kv_format == 2 ? 1 : 0;
+  return FS_OK;
+}
+
+extern "C" int fs_fused_decode_merged(const void* q, int q_dtype, int kv_format, const void* k_values,
+                                      const float* k_scale, const int16_t* k_zero, const void* v_values,
+                                      const float* v_scale, const int16_t* v_zero, const int64_t* lengths, void* out,
+                                      void* merge_area, int64_t merge_area_bytes, int batch, int heads, int head_dim,
+                                      int seq_len, int n_blocks, int block_size, float sm_scale, int split_tiles,
+                                      int max_splits, int waves_per_block, void* stream) {
+  int vfmt = 0, per_channel = 0;
+  if (int rc = kv_format_of(kv_format, vfmt, per_channel)) return rc;
+  return fused_decode(q, q_dtype, (const int8_t*)k_values, k_scale, k_zero, (const int8_t*)v_values, v_scale, v_zero,
+                      lengths, out, nullptr, 0, batch, heads, head_dim, seq_len, n_blocks, block_size, sm_scale,
+                      split_tiles, max_splits, waves_per_block, vfmt, stream, per_channel, merge_area,
+                      merge_area_bytes < 0 ? 0 : merge_area_bytes);
+}
+
+extern "C" int fs_paged_decode_merged(const void* q, int q_dtype, int kv_format, const void* k_values,
+                                      const float* k_scale, const int16_t* k_zero, const void* v_values,
+                                      const float* v_scale, const int16_t* v_zero, const void* block_table,
+                                      int table_index_bytes, int64_t table_cols, const int64_t* lengths, void* out,
+                                      void* merge_area, int64_t merge_area_bytes, int batch, int heads, int head_dim,
+                                      int64_t num_pages, int page_size, int quant_block, int max_seq_len,
+                                      float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                                      void* stream) {
+  int vfmt = 0, per_channel = 0;
+  if (int rc = kv_format_of(kv_format, vfmt, per_channel)) return rc;
+  return paged_decode(q, q_dtype, (const int8_t*)k_values, k_scale, k_zero, (const int8_t*)v_values, v_scale, v_zero,
+                      block_table, table_index_bytes, table_cols, lengths, out, nullptr, 0, batch, heads, head_dim,
+                      num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles, max_splits,
+                      waves_per_block, vfmt, stream, per_channel, merge_area,
+                      merge_area_bytes < 0 ? 0 : merge_area_bytes);
 }
 
 extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype,

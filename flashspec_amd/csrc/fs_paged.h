@@ -63,7 +63,17 @@ struct DecodeParams {
   const void* draft_k;
   const void* draft_v;
   const int64_t* parents;
+  // In-kernel split merge (tiled kernel, merge_count != nullptr): a zero-filled area of per-row
+  // arrival counts [rows] and tagged partial states [rows, max_splits, D + 2] (64-bit words, tag 1 in
+  // the upper half); the last split of a row to arrive merges the row and zeroes what it used.
+  unsigned* merge_count;
+  unsigned long long* merge_slots;
 };
+
+// Bytes of a merge area: the counts padded to 256 bytes, then the slots.
+__host__ __device__ inline int64_t merge_area_bytes(int64_t rows, int64_t max_splits, int64_t head_dim) {
+  return (rows * 4 + 255) / 256 * 256 + rows * max_splits * (head_dim + 2) * 8;
+}
 
 __device__ __forceinline__ int queries_per_head(const DecodeParams& p) { return p.nq > 1 ? p.nq : 1; }
 
@@ -200,7 +210,7 @@ int paged_params(DecodeParams& p, bool& tiled, const void* q, const int8_t* k_va
                  void* out, void* workspace, int64_t workspace_bytes, int batch, int nq, int heads, int head_dim,
                  int64_t num_pages, int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
                  int max_splits, int waves_per_block, bool row_kernel = true, int vfmt = kVfInt8,
-                 int per_channel = 0);
+                 int per_channel = 0, void* merge_area = nullptr, int64_t merge_bytes = -1);
 
 // The paged decode row kernel on `p` (fs_decode.hip).
 int launch_paged_rows(const DecodeParams& p, int q_dtype, bool tiled, int waves_per_block, hipStream_t st);

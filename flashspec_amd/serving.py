@@ -282,6 +282,7 @@ class DecodeBatch:
         lengths = torch.tensor(self.host_lengths, dtype=torch.int64)
         self._lengths = [lengths.to(self.device), lengths.to(self.device).clone()]
         self._cur = 0
+        self._caches: dict = {}  # lengths buffer -> ((buffer, max_seq_len), PagedKVCache)
         self._open = True
 
     # -- bookkeeping ----------------------------------------------------------------------
@@ -320,9 +321,22 @@ class DecodeBatch:
             self.block_table.copy_(src)
 
     def cache(self) -> PagedKVCache:
-        return PagedKVCache(k_quant=self.allocator.k_quant, v_quant=self.allocator.v_quant,
-                            block_table=self.block_table, lengths=self.lengths, block_size=self.page,
-                            max_seq_len=max(1, max(self.host_lengths)))
+        """The batch as a PagedKVCache over the current lengths buffer.
+
+        ``max_seq_len`` is the longest request rounded up to a whole page (the kernels mask by the
+        device lengths, and the table covers every page the batch reserved), so the same two
+        objects -- one per lengths buffer -- serve up to ``page`` steps in a row and the launch
+        path's layout validation memo holds across those steps."""
+
+        cap = -(-max(1, max(self.host_lengths)) // self.page) * self.page
+        key = (self._cur, cap)
+        cached = self._caches.get(self._cur)
+        if cached is None or cached[0] != key:
+            cached = (key, PagedKVCache(k_quant=self.allocator.k_quant, v_quant=self.allocator.v_quant,
+                                        block_table=self.block_table, lengths=self.lengths, block_size=self.page,
+                                        max_seq_len=cap))
+            self._caches[self._cur] = cached
+        return cached[1]
 
     # -- decode ---------------------------------------------------------------------------
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:

@@ -21,8 +21,11 @@ from .quant import (FP8_DTYPE, QuantizedTensor, build_compression_stats, estimat
                     is_per_channel)
 from .triton_utils import (
     dispatch_triton_or_fallback,
+    MERGE_MAX_WAVES,
+    kv_format_code,
     launch_plan,
     layout_checked,
+    merge_area,
     remember_layout,
     resolve_block_n as _resolve_block_n,
     resolve_num_warps as _resolve_num_warps,
@@ -131,6 +134,15 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     tiled, waves, split_tiles, max_splits, block_n = launch_plan(seq_len, rows, head_dim, block_size, block_size,
                                                                  dev, per_channel=per_channel, light=light)
     stream = _lib.stream_ptr(dev)
+    if tiled and max_splits > 1 and waves <= MERGE_MAX_WAVES:
+        # split rows merge inside the decode launch (no workspace, no merge launch)
+        area, area_bytes = merge_area(dev, rows, max_splits, head_dim)
+        _lib.check(lib.fs_fused_decode_merged(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kv_format_code(per_channel, is_fp8(k_quant)),
+            *(t.data_ptr() for t in kv), _lib.ptr(lengths_c), out.data_ptr(), area.data_ptr(), area_bytes, batch,
+            heads, head_dim, seq_len, n_blocks, block_size, sm_scale, split_tiles, max_splits, waves, stream))
+        return _fused_result(out, return_stats, k_quant, v_quant, q_c, seq_len, max_splits, block_n, waves,
+                             split_tiles, tiled)
     workspace, ws_bytes = None, 0
     if max_splits > 1:
         ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
@@ -150,8 +162,16 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
         _lib.check(lib.fs_combine_splits(
             workspace.data_ptr(), _lib.ptr(lengths_c), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,
             head_dim, seq_len, split_tiles, max_splits, stream))
+    return _fused_result(out, return_stats, k_quant, v_quant, q_c, seq_len, max_splits, block_n, waves, split_tiles,
+                         tiled)
+
+
+def _fused_result(out, return_stats, k_quant, v_quant, q_c, seq_len, max_splits, block_n, waves, split_tiles, tiled):
+    """``out`` or ``(out, stats)`` with the reference's stats keys (triton_fused.py:746-761)."""
+
     if not return_stats:
         return out
+    batch, heads, head_dim = (int(s) for s in q_c.shape)
     dense_bytes = 2 * batch * heads * seq_len * head_dim * q_c.element_size()
     quant_bytes = estimate_quantized_bytes(k_quant) + estimate_quantized_bytes(v_quant)
     return out, build_compression_stats(

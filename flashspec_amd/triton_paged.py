@@ -6,7 +6,8 @@ and validation errors.  The launch goes to ``fs_paged_decode_i8``: a workgroup o
 cooperating waves resolves each block_table entry once per page into a base offset
 (instead of per-token-lane table loads), streams the int8 pages with coalesced
 16-byte loads and merges its waves in LDS; rows only split across workgroups when
-there are fewer rows than CUs (fp32 log-sum-exp merge in a second launch).
+there are fewer rows than CUs, and then the last split of each row to finish merges
+the row (fp32 log-sum-exp) inside the same launch (``fs_paged_decode_merged``).
 """
 
 from __future__ import annotations
@@ -21,8 +22,11 @@ from .paged import PagedKVCache
 from .quant import FP8_DTYPE, build_compression_stats, is_fp8, is_per_channel
 from .triton_utils import (
     dispatch_triton_or_fallback,
+    MERGE_MAX_WAVES,
+    kv_format_code,
     launch_plan,
     layout_checked,
+    merge_area,
     remember_layout,
     resolve_block_n as _resolve_block_n,
     resolve_num_warps as _resolve_num_warps,
@@ -111,6 +115,16 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
         max_seq_len, rows, head_dim, int(cache.block_size), int(kq.block_size), dev, per_channel=per_channel,
         light=light)
     stream = _lib.stream_ptr(dev)
+    if tiled and max_splits > 1 and waves <= MERGE_MAX_WAVES:
+        # split rows merge inside the decode launch (no workspace, no merge launch)
+        area, area_bytes = merge_area(dev, rows, max_splits, head_dim)
+        _lib.check(lib.fs_paged_decode_merged(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kv_format_code(per_channel, is_fp8(kq)),
+            *(t.data_ptr() for t in kv), table.data_ptr(), table.element_size(), int(table.shape[1]),
+            lengths.data_ptr(), out.data_ptr(), area.data_ptr(), area_bytes, batch, heads, head_dim, num_pages,
+            int(cache.block_size), int(kq.block_size), max_seq_len, sm_scale, split_tiles, max_splits, waves, stream))
+        return _paged_result(out, return_stats, cache, q_c, max_seq_len, max_splits, block_n, waves, split_tiles,
+                             tiled)
     workspace, ws_bytes = None, 0
     if max_splits > 1:
         ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
@@ -132,8 +146,15 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
         _lib.check(lib.fs_combine_splits(
             workspace.data_ptr(), lengths.data_ptr(), out.data_ptr(), _lib.dtype_code(out.dtype), batch, heads,
             head_dim, max_seq_len, split_tiles, max_splits, stream))
+    return _paged_result(out, return_stats, cache, q_c, max_seq_len, max_splits, block_n, waves, split_tiles, tiled)
+
+
+def _paged_result(out, return_stats, cache, q_c, max_seq_len, max_splits, block_n, waves, split_tiles, tiled):
+    """``out`` or ``(out, stats)`` with the reference's stats keys (triton_paged.py:439-449)."""
+
     if not return_stats:
         return out
+    batch, heads, head_dim = (int(s) for s in q_c.shape)
     dense_bytes = 2 * batch * heads * max_seq_len * head_dim * q_c.element_size()
     return out, build_compression_stats(
         dense_bytes, cache.estimated_bytes(), materializes_dense_kv=False,

@@ -73,6 +73,48 @@ def remember_layout(owner, key) -> None:
     object.__setattr__(owner, _MEMO_ATTR, key)
 
 
+# ---- merge areas of the in-kernel split merge -----------------------------------------------
+# Rows that split merge inside the decode launch: the last split of a row to finish merges it,
+# through a merge area that must be all zero before a launch and that every launch leaves all zero
+# again.  One zero-filled area per (device, stream) serves every eager call on that stream, grown
+# when a launch needs more.  Under stream capture each call zero-fills an area of its own inside
+# the capture (a fill kernel, recorded with the decode), so every replay starts from zero without
+# sharing memory with eager calls.
+_MERGE_AREAS: dict = {}
+_MERGE_AREA_MIN_BYTES = 1 << 16
+# Split launches of up to this many waves per workgroup merge in-kernel; 16-wave workgroups keep
+# the workspace + merge-launch path.  Measured on MI355X (paged, H32 D128, same box), in-kernel /
+# two launches / decode alone, us: B4 S2048 2 splits x 4 waves 16.46 / 18.15 / 14.55, B4 S4096
+# 2 x 4 26.13 / 27.86 / 24.56, B2 S8192 4 x 4 26.44 / 27.70 / 24.24, B1 S16384 8 x 4 28.08 / 28.81 /
+# 24.36; B2 S8192 8 x 16 35.32 / 33.71 / 29.23.
+MERGE_MAX_WAVES = 8
+
+
+def merge_area(device, rows: int, max_splits: int, head_dim: int):
+    """(tensor, bytes) of a zero-filled merge area for one decode launch on the current stream."""
+
+    import torch
+
+    lib = _lib.require()
+    need = int(lib.fs_decode_merge_area_bytes(rows, max_splits, head_dim))
+    if torch.cuda.is_current_stream_capturing():
+        area = torch.zeros(need, dtype=torch.uint8, device=device)
+        return area, need
+    stream = torch.cuda.current_stream(device)
+    key = (stream.device.index, stream.cuda_stream)
+    area = _MERGE_AREAS.get(key)
+    if area is None or area.numel() < need:
+        area = torch.zeros(max(need, _MERGE_AREA_MIN_BYTES), dtype=torch.uint8, device=device)
+        _MERGE_AREAS[key] = area
+    return area, int(area.numel())
+
+
+def kv_format_code(per_channel: bool, fp8: bool) -> int:
+    """kv_format of the merged decode entry points: 0 affine INT8, 1 FP8 E4M3, 2 per-channel INT8."""
+
+    return 2 if per_channel else (1 if fp8 else 0)
+
+
 _DEFAULT_BLOCK_N = 128
 
 

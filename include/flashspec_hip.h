@@ -110,6 +110,35 @@ int fs_paged_decode_i8(const void* q, int q_dtype,
                        int split_tiles, int max_splits, int waves_per_block, void* stream);
 
 /*
+ * Decode with the split merge inside the decode launch (tiled path only; replaces the split
+ * kernel plus _combine_splits_kernel pair, reference triton_fused.py:697-744, and gives
+ * triton_paged.py:428-434 split-K).  Arguments as fs_fused_decode_i8 / fs_paged_decode_i8 (or
+ * their _fp8 / _i8_channel forms, chosen by kv_format: 0 = affine INT8 per block or token,
+ * 1 = FP8 E4M3 with NULL zero arrays, 2 = per-channel affine INT8), with the workspace replaced
+ * by a merge area of at least fs_decode_merge_area_bytes(batch*heads, max_splits, head_dim)
+ * bytes, 256-byte aligned, all zero before its first use.  When rows split, the last split of
+ * each row to finish merges the row and writes it; every call leaves the area all zero again,
+ * so one area serves any number of later calls (graph replays included) on one stream.  Calls
+ * that overlap in time must use different areas.  With max_splits = 1 the area may be NULL.
+ */
+int64_t fs_decode_merge_area_bytes(int64_t rows, int64_t max_splits, int64_t head_dim);
+int fs_fused_decode_merged(const void* q, int q_dtype, int kv_format,
+                           const void* k_values, const float* k_scale, const int16_t* k_zero,
+                           const void* v_values, const float* v_scale, const int16_t* v_zero,
+                           const int64_t* lengths, void* out, void* merge_area, int64_t merge_area_bytes,
+                           int batch, int heads, int head_dim, int seq_len, int n_blocks,
+                           int block_size, float sm_scale, int split_tiles, int max_splits,
+                           int waves_per_block, void* stream);
+int fs_paged_decode_merged(const void* q, int q_dtype, int kv_format,
+                           const void* k_values, const float* k_scale, const int16_t* k_zero,
+                           const void* v_values, const float* v_scale, const int16_t* v_zero,
+                           const void* block_table, int table_index_bytes, int64_t table_cols,
+                           const int64_t* lengths, void* out, void* merge_area, int64_t merge_area_bytes,
+                           int batch, int heads, int head_dim, int64_t num_pages,
+                           int page_size, int quant_block, int max_seq_len, float sm_scale,
+                           int split_tiles, int max_splits, int waves_per_block, void* stream);
+
+/*
  * fs_paged_decode_i8 without a workspace argument, for callers that cannot allocate device
  * memory (code under graph capture, serving loops that forbid allocation).  No counterpart in
  * the reference.  When rows split (max_splits > 1) the split-K partials go to a device array
@@ -388,6 +417,14 @@ int fs_append_tokens_i8(const void* k_new, const void* v_new, int src_dtype,
  * bench.py sets beside the decode kernel's; `sink` (4 bytes of device memory) is written only
  * if the XOR of everything read matches a fixed word. */
 int fs_stream_read(const void* src, int64_t bytes, unsigned* sink, int blocks, void* stream);
+
+/*
+ * Measurement helper (no reference counterpart): streams src_bytes from src with 16-byte
+ * non-temporal loads and writes src_bytes / 2 to dst (two bytes of every four), in `blocks`
+ * workgroups of 256 lanes: the traffic of an fp16 -> int8 pass with no arithmetic, whose rate is
+ * the practical ceiling of the quantizers.
+ */
+int fs_stream_copy_half(const void* src, int64_t src_bytes, void* dst, int blocks, void* stream);
 
 #ifdef __cplusplus
 }
