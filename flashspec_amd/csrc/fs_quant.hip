@@ -180,28 +180,67 @@ __device__ __forceinline__ void store_chunks(const float (&x)[CH][8], float scal
   }
 }
 
+// One lane's share of a vectorized group as loaded: CH chunks of 8 source values (16 bytes each
+// for 16-bit types, 32 for fp32); chunks past the group's valid rows are zero.
 template <int CH, typename XT>
-__device__ __forceinline__ void quantize_group_vec(const XT* src, int valid_rows, int D, int8_t* dst,
-                                                   float* scale_out, int16_t* zero_out, int lane) {
-  float x[CH][8];
-  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+struct RawGroup {
+  static constexpr int kWords = sizeof(XT) == 4 ? 2 * CH : CH;
+  q_u32x4_t w[kWords];
+};
+
+template <int CH, typename XT>
+__device__ __forceinline__ void load_raw(RawGroup<CH, XT>& r, const XT* src, int valid_rows, int D, int lane) {
+  constexpr int per = RawGroup<CH, XT>::kWords / CH;  // 16-byte words per chunk
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int e = c * 512 + lane * 8;
-    if (e / D < valid_rows) {
-      load8(src + e, x[c]);
-    } else {
+    const bool ok = e / D < valid_rows;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[c][i] = 0.0f;
-    }
+    for (int i = 0; i < per; ++i)
+      r.w[c * per + i] = ok ? nt_load16((const char*)(src + e) + 16 * i) : q_u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ void unpack8(const q_u32x4_t* w, const float*, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = __uint_as_float(w[0][i]);
+    f[4 + i] = __uint_as_float(w[1][i]);
+  }
+}
+
+__device__ __forceinline__ void unpack8(const q_u32x4_t* w, const __half*, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __half2float(__ushort_as_half((unsigned short)(w[0][i] & 0xffffu)));
+    f[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w[0][i] >> 16)));
+  }
+}
+
+__device__ __forceinline__ void unpack8(const q_u32x4_t* w, const __hip_bfloat16*, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[0][i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[0][i] & 0xffff0000u);
+  }
+}
+
+// Quantizes a group held in registers (quantize_group's float32 op sequence).
+template <int CH>
+__device__ __forceinline__ void quantize_regs(const float (&x)[CH][8], int8_t* dst, float* scale_out,
+                                              int16_t* zero_out, int lane) {
+  float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       mn = fminf(mn, x[c][i]);
       mx = fmaxf(mx, x[c][i]);
     }
   }
-  mn = wave_min(mn);
-  mx = wave_max(mx);
+  // min / max are exact whatever the order; lane swaps and DPP keep them off the LDS
+  mn = wave_min_valu(mn);
+  mx = wave_max_valu(mx);
   const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
   const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
   const float rcp = 1.0f / scale;  // correctly rounded
@@ -217,40 +256,97 @@ __device__ __forceinline__ void quantize_group_vec(const XT* src, int valid_rows
   }
 }
 
+template <int CH, typename XT>
+__device__ __forceinline__ void unpack_group(const RawGroup<CH, XT>& r, float (&x)[CH][8]) {
+  constexpr int per = RawGroup<CH, XT>::kWords / CH;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) unpack8(&r.w[c * per], (const XT*)nullptr, x[c]);
+}
+
+template <int CH, typename XT>
+__device__ __forceinline__ void quantize_group_vec(const XT* src, int valid_rows, int D, int8_t* dst,
+                                                   float* scale_out, int16_t* zero_out, int lane) {
+  RawGroup<CH, XT> r;
+  load_raw(r, src, valid_rows, D, lane);
+  float x[CH][8];
+  unpack_group(r, x);
+  quantize_regs<CH>(x, dst, scale_out, zero_out, lane);
+}
+
+// Where group `grp` of a vectorized quantize pass reads and writes.
+template <typename XT>
+struct GroupRef {
+  const XT* src;
+  int valid_rows;
+  int8_t* dst;
+  float* scale;
+  int16_t* zero;
+};
+
+// Waves loop over groups grp = wave, wave + waves, ...: the next group's loads are issued before
+// the current group is quantized, so every wave keeps a group's bytes in flight while it computes.
+template <int CH, typename XT, typename Map>
+__device__ __forceinline__ void quantize_groups_pipelined(const Map& map, int64_t ngroups, int D) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x / kWave);
+  int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (grp >= ngroups) return;
+  GroupRef<XT> cur = map(grp);
+  RawGroup<CH, XT> raw;
+  load_raw(raw, cur.src, cur.valid_rows, D, lane);
+  for (;;) {
+    const int64_t nxt = grp + waves;
+    GroupRef<XT> ref_next{};
+    RawGroup<CH, XT> raw_next;
+    if (nxt < ngroups) {
+      ref_next = map(nxt);
+      load_raw(raw_next, ref_next.src, ref_next.valid_rows, D, lane);
+    }
+    float x[CH][8];
+    unpack_group(raw, x);
+    quantize_regs<CH>(x, cur.dst, cur.scale, cur.zero, lane);
+    if (nxt >= ngroups) break;
+    grp = nxt;
+    cur = ref_next;
+    raw = raw_next;
+  }
+}
+
 // Chunks of 512 values per group when the vectorized quantizer applies, else 0.
 __host__ __device__ constexpr int vec_chunks(int rows, int D) {
   return (D % 8 == 0 && (rows * D) % 512 == 0 && rows * D / 512 <= 8) ? rows * D / 512 : 0;
 }
 
-// x [outer, S, D] -> values [outer, nb, bs, D]; one wave per group (o, block), vectorized.
+// x [outer, S, D] -> values [outer, nb, bs, D]; groups (o, block), vectorized and pipelined.
 template <int CH, typename XT>
 __global__ void __launch_bounds__(256)
 quantize_blocks_vec_kernel(const XT* x, int64_t outer, int S, int D, int bs, int nb, int8_t* values, float* scale,
                            int16_t* zero) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-  if (grp >= outer * nb) return;
-  const int64_t o = grp / nb;
-  const int blk = (int)(grp - o * nb);
-  const XT* src = x + ((size_t)o * S + (size_t)blk * bs) * D;
-  quantize_group_vec<CH>(src, S - blk * bs, D, values + (size_t)grp * bs * D, scale + grp, zero + grp, lane);
+  auto map = [=](int64_t grp) {
+    const int64_t o = grp / nb;
+    const int blk = (int)(grp - o * nb);
+    return GroupRef<XT>{x + ((size_t)o * S + (size_t)blk * bs) * D, S - blk * bs, values + (size_t)grp * bs * D,
+                        scale + grp, zero + grp};
+  };
+  quantize_groups_pipelined<CH, XT>(map, outer * nb, D);
 }
 
-// dense [B, H, S, D] -> page store [P, H, page, D], vectorized (see quantize_pages_kernel).
+// dense [B, H, S, D] -> page store [P, H, page, D], vectorized and pipelined (see
+// quantize_pages_kernel).
 template <int CH, typename XT>
 __global__ void __launch_bounds__(256)
 quantize_pages_vec_kernel(const XT* x, int H, int S, int D, int page, int nbps, const int64_t* page_src, int64_t P,
                           int8_t* values, float* scale, int16_t* zero) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-  if (grp >= P * H) return;
-  const int64_t j = grp / H;
-  const int h = (int)(grp - j * H);
-  const int64_t o = page_src ? page_src[j] : j;
-  const int64_t b = o / nbps;
-  const int lb = (int)(o - b * nbps);
-  const XT* src = x + (((size_t)(b * H + h) * S) + (size_t)lb * page) * D;
-  quantize_group_vec<CH>(src, S - lb * page, D, values + (size_t)grp * page * D, scale + grp, zero + grp, lane);
+  auto map = [=](int64_t grp) {
+    const int64_t j = grp / H;
+    const int h = (int)(grp - j * H);
+    const int64_t o = page_src ? page_src[j] : j;
+    const int64_t b = o / nbps;
+    const int lb = (int)(o - b * nbps);
+    return GroupRef<XT>{x + (((size_t)(b * H + h) * S) + (size_t)lb * page) * D, S - lb * page,
+                        values + (size_t)grp * page * D, scale + grp, zero + grp};
+  };
+  quantize_groups_pipelined<CH, XT>(map, P * H, D);
 }
 
 // x [outer, S, D] -> values [outer, nb, bs, D]; group = (o, block); rows past S read as 0.
@@ -538,6 +634,14 @@ dequantize_fp8_kernel(const uint8_t* values, const float* scale, int64_t outer, 
 
 static dim3 wave_grid(int64_t groups) { return dim3((unsigned)((groups + 3) / 4)); }
 
+// The pipelined vectorized quantizers loop over groups: at most 2048 workgroups of 4 waves (8 per
+// CU on 256 CUs), each wave taking every (waves)-th group.
+constexpr int64_t kVecQuantMaxBlocks = 2048;
+static dim3 vec_grid(int64_t groups) {
+  const int64_t blocks = (groups + 3) / 4;
+  return dim3((unsigned)(blocks < kVecQuantMaxBlocks ? blocks : kVecQuantMaxBlocks));
+}
+
 static bool is_pow2_chunks(int ch) { return ch == 1 || ch == 2 || ch == 4 || ch == 8; }
 
 template <typename XT>
@@ -597,9 +701,9 @@ extern "C" int fs_quantize_i8(const void* x, int x_dtype, int64_t outer, int seq
   const int ch = vec_chunks(block_size, head_dim);
   if (is_pow2_chunks(ch) && ((uintptr_t)x % 16) == 0 && ((uintptr_t)values % 8) == 0) {
     switch (x_dtype) {
-      case FS_F32: return launch_vec_blocks<float>(ch, grid, st, (const float*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
-      case FS_F16: return launch_vec_blocks<__half>(ch, grid, st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
-      case FS_BF16: return launch_vec_blocks<__hip_bfloat16>(ch, grid, st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
+      case FS_F32: return launch_vec_blocks<float>(ch, vec_grid(groups), st, (const float*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
+      case FS_F16: return launch_vec_blocks<__half>(ch, vec_grid(groups), st, (const __half*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
+      case FS_BF16: return launch_vec_blocks<__hip_bfloat16>(ch, vec_grid(groups), st, (const __hip_bfloat16*)x, outer, seq_len, head_dim, block_size, nb, values, scale, zero);
       default: return set_error(FS_ERR_INVALID, "quantize: dtype code must be 0, 1 or 2");
     }
   }
@@ -649,9 +753,9 @@ extern "C" int fs_quantize_pages_i8(const void* x, int x_dtype, int batch, int h
   const int ch = vec_chunks(page_size, head_dim);
   if (is_pow2_chunks(ch) && ((uintptr_t)x % 16) == 0 && ((uintptr_t)values % 8) == 0) {
     switch (x_dtype) {
-      case FS_F32: return launch_vec_pages<float>(ch, grid, st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
-      case FS_F16: return launch_vec_pages<__half>(ch, grid, st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
-      case FS_BF16: return launch_vec_pages<__hip_bfloat16>(ch, grid, st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
+      case FS_F32: return launch_vec_pages<float>(ch, vec_grid(groups), st, (const float*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
+      case FS_F16: return launch_vec_pages<__half>(ch, vec_grid(groups), st, (const __half*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
+      case FS_BF16: return launch_vec_pages<__hip_bfloat16>(ch, vec_grid(groups), st, (const __hip_bfloat16*)x, heads, seq_len, head_dim, page_size, nbps, page_src, num_pages, values, scale, zero);
       default: return set_error(FS_ERR_INVALID, "quantize_pages: dtype code must be 0, 1 or 2");
     }
   }
