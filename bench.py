@@ -280,8 +280,8 @@ SERVE_B, SERVE_LO, SERVE_HI = 64, 128, 16384
 def serving_step_bench(torch, fa, dev, steps: int, warmup: int) -> dict:
     """Serving decode step at scale: 64 requests, lengths ~ U[128, 16384] (seeded CPU draw),
     fragmented shuffled page pool, one fp16 token appended per request per step and paged
-    attention over the updated cache (device-resident table and lengths, two launches + the
-    split merge when a request needs it)."""
+    attention over the updated cache: ``DecodeBatch.step``, device-resident table and lengths,
+    one launch with the append inside the decode kernel."""
 
     from flashspec_amd.serving import DecodeBatch, build_request_pool
 

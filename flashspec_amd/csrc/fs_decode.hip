@@ -253,6 +253,115 @@ __device__ __forceinline__ void load_tile_tok(TileRegs<DP>& t, const DecodeParam
   }
 }
 
+// One decode token appended inside the paged decode (kQmBlockAppend): value e of a lane's 16 new
+// K or V dims as loaded (QT's bytes in sizeof(QT) 16-byte words).
+template <typename QT>
+__device__ __forceinline__ float token_value(const uint4 (&w)[sizeof(QT)], int e) {
+  const uint4 q = w[e * (int)sizeof(QT) / 16];
+  const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+  if constexpr (sizeof(QT) == 4) {
+    return __uint_as_float(words[e % 4]);
+  } else {
+    const uint32_t h = (words[(e % 8) / 2] >> (16 * (e % 2))) & 0xffffu;
+    return to_f32(__builtin_bit_cast(QT, (uint16_t)h));
+  }
+}
+
+// The wave's loads of one appended token's tile -- a whole page (page = quant block = 16 tokens,
+// head_dim = DP) -- and of the new K / V rows (by the lanes holding the token's row of the tile).
+template <int DP, typename QT>
+struct AppendLoads {
+  static constexpr int LPTILE = TileRegs<DP>::LPTILE;
+  uint4 page[2][LPTILE];
+  uint4 tok[2][sizeof(QT)];
+  float old[4];  // the page's stored K scale, K zero, V scale, V zero
+  __device__ __forceinline__ void issue(const DecodeParams& p, int base, int meta, int row, int lane_off, int rstride,
+                                        int j, bool mine) {
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+      const int8_t* vals = p.kv[kv] + (size_t)base * (kTile * DP) + lane_off;
+#pragma unroll
+      for (int r = 0; r < LPTILE; ++r) page[kv][r] = *(const uint4*)(vals + (size_t)r * rstride);
+      const uint4* src = (const uint4*)((const QT*)(kv ? p.append_v : p.append_k) + (size_t)row * DP + 16 * j);
+#pragma unroll
+      for (int i = 0; i < (int)sizeof(QT); ++i) tok[kv][i] = mine ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+      old[2 * kv] = p.sc[kv][meta];
+      old[2 * kv + 1] = (float)p.zp[kv][meta];
+    }
+  }
+};
+
+// Row `off` of the loaded page replaced by the new token, K and then V requantized with the affine
+// per-block float32 op sequence of reference quant.py:141-158 (the page dequantized with its old
+// scale / zero point, stale rows included) -- the arithmetic of fs_append_tokens_i8, so pages and
+// parameters come out bit-identical to it -- and stored back: each lane stores exactly the 16-byte
+// pieces it loads again when the wave streams this tile later (same lane, same addresses, later in
+// program order).  prm = (K scale, K zero, V scale, V zero).
+template <int DP, typename QT>
+__device__ __forceinline__ void requant_appended_page(float (&prm)[4], const AppendLoads<DP, QT>& a,
+                                                      const DecodeParams& p, int base, int meta, int off, int lane_off,
+                                                      int rstride, int g) {
+#pragma clang fp contract(off)
+  constexpr int LPTILE = TileRegs<DP>::LPTILE, RPL = TileRegs<DP>::RPL;
+  const bool mine = g == off % RPL;  // this lane holds dims [16j, 16j + 16) of row `off`
+  const int r_off = off / RPL;
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    const float s_old = a.old[2 * kv], z_old = a.old[2 * kv + 1];
+    // value e of this lane's token row in load r: the new token, or the dequantized stored byte
+    auto value = [&](int r, int e) -> float {
+      if (r == r_off && mine) return token_value<QT>(a.tok[kv], e);
+      const uint32_t wv[4] = {a.page[kv][r].x, a.page[kv][r].y, a.page[kv][r].z, a.page[kv][r].w};
+      const int u = (int)((wv[e / 4] >> (8 * (e % 4))) & 0xffu) ^ 0x80;  // stored int8 + 128
+      return ((float)u - z_old) * s_old;
+    };
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int r = 0; r < LPTILE; ++r) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float x = value(r, e);
+        mn = fminf(mn, x);
+        mx = fmaxf(mx, x);
+      }
+    }
+    mn = wave_min_valu(mn);
+    mx = wave_max_valu(mx);
+    const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
+    const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
+    const float rcp = 1.0f / scale;  // correctly rounded
+    int8_t* vals = const_cast<int8_t*>(p.kv[kv]) + (size_t)base * (kTile * DP) + lane_off;
+    // rounding is monotonic: when the largest |x| * rcp is finite every product is (the test is
+    // wave-uniform, so one of the two forms runs)
+    auto requant = [&](auto use_rcp) {
+#pragma unroll
+      for (int r = 0; r < LPTILE; ++r) {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float x = value(r, e);
+          const float qd = decltype(use_rcp)::value ? div_by_scale(x, scale, rcp) : x / scale;
+          const float qv = fminf(fmaxf(__builtin_rintf(qd + zero), 0.0f), 255.0f);
+          w[e / 4] = __builtin_amdgcn_cvt_pk_u8_f32(qv, e % 4, w[e / 4]);  // exact: qv is an integer in [0, 255]
+        }
+        // stored as q - 128
+        *(uint4*)(vals + (size_t)r * rstride) =
+            make_uint4(w[0] ^ 0x80808080u, w[1] ^ 0x80808080u, w[2] ^ 0x80808080u, w[3] ^ 0x80808080u);
+      }
+    };
+    if (__builtin_isfinite(fmaxf(fabsf(mn), fabsf(mx)) * rcp))
+      requant(std::true_type{});
+    else
+      requant(std::false_type{});
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+      const_cast<float*>(p.sc[kv])[meta] = scale;
+      const_cast<int16_t*>(p.zp[kv])[meta] = (int16_t)zero;
+    }
+    prm[2 * kv] = scale;
+    prm[2 * kv + 1] = zero;
+  }
+}
+
 // Quantization parameters of the LPTILE token rows a lane holds in one tile.
 template <int N>
 struct RowMeta {
@@ -699,6 +808,8 @@ decode_rows_kernel(const DecodeParams p) {
   constexpr bool T8 = QM == kQmBlockTail8 || QM == kQmTokenTail8;  // head_dim an odd multiple of 8
   constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken || QM == kQmTokenTail8, CHB = QM == kQmChannelBlocks;
   constexpr bool CH = QM == kQmChannel || CHB;
+  constexpr bool APP = QM == kQmBlockAppend;  // one token appended to every request first
+  static_assert(!APP || (PAGED && VF == kVfInt8), "the fused append serves paged INT8 stores");
   constexpr int WMAX = max_tiled_waves(DP, QM);
   __shared__ __attribute__((aligned(16))) float s_acc[WMAX * DP];
   __shared__ __attribute__((aligned(16))) float s_ml[2 * WMAX];
@@ -764,7 +875,9 @@ decode_rows_kernel(const DecodeParams p) {
     }
   }
 
-  const int len = row_length(p.lengths, b, p.seq_len);
+  // APP: the row covers the appended token too (a token whose page is not backed lies in an
+  // unbacked tile and stays masked, which is what the separate append + decode would give)
+  const int len = APP ? row_length_after_append(p.lengths, b, p.seq_len) : row_length(p.lengths, b, p.seq_len);
   const int nsplit = row_splits(len, p.split_tiles);
   if (split >= nsplit) return;  // whole workgroup, before any barrier
   const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
@@ -785,6 +898,28 @@ decode_rows_kernel(const DecodeParams p) {
       my_kz1 = VF == kVfInt8 ? (float)p.zp[0][my_meta1] : 0.f;
       my_vs1 = p.sc[1][my_meta1];
       my_vz1 = VF == kVfInt8 ? (float)p.zp[1][my_meta1] : 0.f;
+    }
+  }
+
+  // APP: the token at position pos of request b goes into tile pos / 16 of the row.  The wave that
+  // streams that tile (k_app: its index in the wave's sequence, the wave's last tile, wave-uniform;
+  // -1 in every other wave) requantizes the page before it loads the tile.  The advanced length is
+  // written up front, once per request (head 0, split 0, wave 0): nothing in this launch reads
+  // lengths_out.
+  int k_app = -1, app_off = 0;
+  if constexpr (APP) {
+    const int64_t pos = p.lengths[b];
+    const bool in_range = pos >= 0 && pos < p.seq_len;
+    if (in_range) {
+      const int rel = (int)(pos / kTile) - split * p.split_tiles;
+      if (rel >= 0 && rel < p.split_tiles && rel % W == w && readlane_i32(my_base, rel / W) >= 0) {
+        k_app = rel / W;  // nk - 1: the row's last token is pos
+        app_off = (int)(pos % kTile);
+      }
+    }
+    if (h == 0 && split == 0 && w == 0 && lane == 0) {
+      const bool stored = in_range && tile_index<true>(p, b, 0, row, (int)(pos / kTile)).data >= 0;
+      p.lengths_out[b] = stored ? pos + 1 : pos;  // fs_append_tokens_i8's rule
     }
   }
 
@@ -857,6 +992,7 @@ decode_rows_kernel(const DecodeParams p) {
   };
   auto consume = [&](const TileRegs<DP>& t, int k) {
     RowMeta<LPTILE> rm;
+
     const bool v0 = readlane_i32(my_base, k) >= 0;
     if constexpr (CHB) {
       // this lane's 16 channels of the quant block, converted at its first tile: K scales
@@ -909,8 +1045,31 @@ decode_rows_kernel(const DecodeParams p) {
     }
     consume_tile<DP, VF>(st, t, q, qsum, rm, (first + W * k) * kTile, len, g);
   };
+  // APP: the owner requantizes its token's page before it loads any tile (registers: with a tile in
+  // flight the kernel would need 4 waves per SIMD instead of 6); its lane-held parameters for the
+  // tile then take the new values.
+  auto append = [&]() {
+    const int base = readlane_i32(my_base, k_app), meta = readlane_i32(my_meta, k_app);
+    AppendLoads<DP, QT> a;
+    a.issue(p, base, meta, row, lane_off, rstride, j, g == app_off % RPL);
+    return a;
+  };
+  auto finish_append = [&](const AppendLoads<DP, QT>& a) {
+    float prm[4];
+    requant_appended_page<DP, QT>(prm, a, p, readlane_i32(my_base, k_app), readlane_i32(my_meta, k_app), app_off,
+                                  lane_off, rstride, g);
+    if (lane == k_app) {
+      my_ks = prm[0] * p.qk_scale;  // as the lane-held parameters are formed from the store
+      my_kz = prm[1];
+      my_vs = prm[2];
+      my_vz = prm[3];
+    }
+  };
   // two register buffers: tile k+1 is in flight while tile k is consumed
   TileRegs<DP> ta, tb2;
+  if constexpr (APP) {
+    if (k_app >= 0) finish_append(append());
+  }
   load(ta, 0);
   for (int k = 0; k < nk; k += 2) {
     load(tb2, k + 1);
@@ -919,7 +1078,6 @@ decode_rows_kernel(const DecodeParams p) {
     load(ta, k + 2);
     consume(tb2, k + 1);
   }
-
 #pragma unroll
   for (int e = 0; e < 16; ++e) st.acc[e] -= st.zacc;
   // One running maximum per wave (lanes of a token-row group already share theirs), then the
@@ -1150,8 +1308,8 @@ static void launch_tiled_vf(const DecodeParams& p, dim3 grid, dim3 block, hipStr
 
 template <typename QT, bool PAGED, int QM>
 static void launch_tiled(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
-  if constexpr (QM == kQmChannel || QM == kQmChannelBlocks) {
-    launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);  // per-channel stores are INT8
+  if constexpr (QM == kQmChannel || QM == kQmChannelBlocks || QM == kQmBlockAppend) {
+    launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);  // per-channel / appending stores are INT8
   } else {
     if (p.vfmt == kVfFp8)
       launch_tiled_vf<QT, PAGED, QM, kVfFp8>(p, grid, block, st);
@@ -1165,6 +1323,12 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
   const dim3 block(kWave * waves_per_block);
   if (tiled) {
     const dim3 grid((unsigned)((int64_t)p.rows * p.max_splits));
+    if constexpr (PAGED) {
+      if (p.append_k != nullptr) {
+        launch_tiled<QT, PAGED, kQmBlockAppend>(p, grid, block, st);
+        return check_launch("paged_decode_append_kernel");
+      }
+    }
     if (p.per_channel && channel_whole_blocks(p))
       launch_tiled<QT, PAGED, kQmChannelBlocks>(p, grid, block, st);
     else if (p.per_channel)
@@ -1498,6 +1662,42 @@ extern "C" int fs_paged_decode_merged(const void* q, int q_dtype, int kv_format,
                       num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles, max_splits,
                       waves_per_block, vfmt, stream, per_channel, merge_area,
                       merge_area_bytes < 0 ? 0 : merge_area_bytes);
+}
+
+extern "C" int fs_paged_decode_append_i8(const void* q, int q_dtype, const void* k_new, const void* v_new,
+                                         int8_t* k_values, float* k_scale, int16_t* k_zero, int8_t* v_values,
+                                         float* v_scale, int16_t* v_zero, const void* block_table,
+                                         int table_index_bytes, int64_t table_cols, const int64_t* lengths_in,
+                                         int64_t* lengths_out, void* out, void* workspace, int64_t workspace_bytes,
+                                         void* merge_area, int64_t merge_area_bytes, int batch, int heads,
+                                         int head_dim, int64_t num_pages, int page_size, int max_seq_len,
+                                         float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                                         void* stream) {
+  if (page_size != kTile)
+    return set_error(FS_ERR_INVALID, "the fused append needs 16-token pages holding one quant block");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return set_error(FS_ERR_INVALID, "the fused append needs head_dim 64, 128 or 256");
+  if (!k_new || !v_new || !lengths_out) return set_error(FS_ERR_INVALID, "null new K/V or lengths_out pointer");
+  if ((const void*)lengths_out == (const void*)lengths_in)
+    return set_error(FS_ERR_INVALID, "lengths_out must be a buffer other than lengths_in");
+  DecodeParams p;
+  bool tiled = false;
+  if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
+                            table_index_bytes, table_cols, lengths_in, out, workspace, workspace_bytes, batch, 1,
+                            heads, head_dim, num_pages, page_size, page_size, max_seq_len, sm_scale, split_tiles,
+                            max_splits, waves_per_block, true, kVfInt8, 0, merge_area,
+                            merge_area != nullptr ? (merge_area_bytes < 0 ? 0 : merge_area_bytes) : -1))
+    return rc;
+  if (!tiled) return set_error(FS_ERR_INVALID, "the fused append needs the tiled decode path");
+  p.append_k = k_new;
+  p.append_v = v_new;
+  p.lengths_out = lengths_out;
+  hipStream_t st = (hipStream_t)stream;
+  if (int rc = launch_decode<true>(p, q_dtype, tiled, waves_per_block, st)) return rc;
+  if (p.max_splits > 1 && p.merge_count == nullptr)  // split partials: merged over the advanced lengths
+    return fs_combine_splits(workspace, lengths_out, out, q_dtype, batch, heads, head_dim, max_seq_len, split_tiles,
+                             max_splits, stream);
+  return FS_OK;
 }
 
 extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype,

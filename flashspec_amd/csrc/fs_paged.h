@@ -22,6 +22,9 @@ enum QuantMode : int {
   // dims straddle the row end loads the row's last 16 bytes and keeps their upper half
   kQmBlockTail8 = 5,
   kQmTokenTail8 = 6,
+  // kQmBlock (paged, 16-token pages holding one quant block, head_dim 64 / 128 / 256) with one
+  // decode token appended to every request inside the launch (fs_paged_decode_append_i8)
+  kQmBlockAppend = 7,
 };
 
 // Value format of the K/V store: affine INT8 (values int8 = u - 128, scale, zero point) or FP8
@@ -68,6 +71,13 @@ struct DecodeParams {
   // the upper half); the last split of a row to arrive merges the row and zeroes what it used.
   unsigned* merge_count;
   unsigned long long* merge_slots;
+  // One-token append fused into the paged decode (kQmBlockAppend): `lengths` holds each request's
+  // position before the append; the new K / V rows append_k / append_v [rows, head_dim] (q's
+  // dtype) go into the page at that position, which is requantized in place, and the advanced
+  // lengths go to lengths_out.
+  const void* append_k;
+  const void* append_v;
+  int64_t* lengths_out;
 };
 
 // Bytes of a merge area: the counts padded to 256 bytes, then the slots.
@@ -119,6 +129,13 @@ __device__ __forceinline__ int row_length(const int64_t* lengths, int b, int seq
   if (lengths == nullptr) return seq_len;
   const int64_t l = lengths[b];
   return (int)(l < 0 ? 0 : (l < (int64_t)seq_len ? l : (int64_t)seq_len));
+}
+
+// Row length once the fused append (kQmBlockAppend) has added the token at position lengths[b].
+__device__ __forceinline__ int row_length_after_append(const int64_t* lengths, int b, int seq_len) {
+  const int64_t pos = lengths[b];
+  const int64_t l = pos >= 0 ? pos + 1 : 0;
+  return (int)(l < (int64_t)seq_len ? l : (int64_t)seq_len);
 }
 
 __device__ __forceinline__ int row_splits(int len, int split_tiles) {

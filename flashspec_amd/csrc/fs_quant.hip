@@ -149,17 +149,6 @@ __device__ __forceinline__ void load8(const __hip_bfloat16* p, float* f) {
   }
 }
 
-// x / scale correctly rounded, from rcp = RN(1 / scale) and one FMA correction step
-// (Markstein's theorem: with rcp correctly rounded and q0 = RN(x * rcp) within one ulp,
-// r = x - q0 * scale is exact and RN(q0 + r * rcp) = RN(x / scale)).  A brute-force check
-// over every fp16 input and random fp32 inputs against IEEE division (tests/cdiv) finds no
-// difference except the sign of a zero quotient, which `+ zero` erases.  Valid while
-// x * rcp stays finite; the caller checks that once per group.
-__device__ __forceinline__ float div_by_scale(float x, float scale, float rcp) {
-  const float q0 = x * rcp;
-  const float r = __builtin_fmaf(-q0, scale, x);
-  return __builtin_fmaf(r, rcp, q0);
-}
 
 // Quantize CH chunks of 8 values held by this lane and store them as packed bytes.
 template <int CH, bool RCP>

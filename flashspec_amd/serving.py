@@ -6,12 +6,14 @@ reference's own design calls for: attention goes through
 ``paged_quant_attention_triton`` (the HIP kernel on GPU, the portable path on CPU)
 instead of the portable path only (serving.py:118,139 call ``paged_quant_attention``).
 On GPU the prompt writes run as batched HIP page-update launches, and the decode loop
-keeps the block table and lengths on the device (``DecodeBatch``): one append launch
-and one attention launch per step, no per-step table rebuild on the host.
+keeps the block table and lengths on the device (``DecodeBatch``): one attention launch
+and one append launch per step (the reference's order: attend, then append what the
+attention produced), no per-step table rebuild on the host.
 
 ``build_request_pool`` and ``DecodeBatch.step`` are the serving-at-scale pieces: a
 fragmented page pool of ragged requests, and one decode step that appends one token
-per request and then attends over the updated cache.
+per request and then attends over the updated cache -- one launch, with the append
+inside the decode kernel.
 
     python -m flashspec_amd.serving --requests 8 --prompt-lens 512,2048 --decode-steps 16 --json
 """
@@ -20,6 +22,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 from dataclasses import dataclass
 from time import perf_counter
 from typing import Dict, Sequence
@@ -235,7 +238,8 @@ class DecodeBatch:
     writes one token per request with a single ``fs_append_tokens_i8`` launch (K and V),
     which reads each request's position from the device lengths and writes the advanced
     lengths to a second buffer, so a decode step needs no host round trip.  ``attend`` runs
-    ``paged_quant_attention_triton`` over the current cache.
+    ``paged_quant_attention_triton`` over the current cache.  ``step`` does both in one
+    ``fs_paged_decode_append_i8`` launch where the shapes allow it.
 
     Page policy: pages are taken from the allocator's free list ``reserve_steps`` steps ahead,
     step-major and in request order, the order in which the reference allocator takes them one
@@ -401,10 +405,84 @@ class DecodeBatch:
         return paged_quant_attention_triton(q, self.cache(), return_stats=return_stats)
 
     def step(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor:
-        """One serving decode step: append one token per request, then attend over the updated cache."""
+        """One serving decode step: append one token per request, then attend over the updated cache.
 
+        On GPU, with 16-token pages, head_dim 64 / 128 / 256, q, k_new, v_new of one dtype, and a
+        decode grid of at most one workgroup per CU, both happen in one launch
+        (``fs_paged_decode_append_i8``: the append runs inside the decode kernel and gives the same
+        pages, lengths and output, bit for bit, as ``append`` followed by ``attend``).  Otherwise
+        the two run one after the other: there the wave that requantizes a request's page holds up
+        its workgroup's closing barrier, once per round of workgroups on a CU, which costs more
+        than the separate append launch.  Measured on MI355X (H32 D128, ragged lengths, shuffled
+        pool), one launch / two launches: B4 29.1 / 32.6 us, B16 69.3 / 68.8 us, B64 639 / 635 us."""
+
+        if self._fusable(q, k_new, v_new):
+            plan = self._fused_plan(q)
+            if plan is not None:
+                return self._step_fused(q, k_new, v_new, plan)
         self.append(k_new, v_new)
         return self.attend(q)
+
+    def _fusable(self, q, k_new, v_new) -> bool:
+        a = self.allocator
+        return (self._open and self.device.type == "cuda" and self.page == 16 and a.k_quant.block_size == 16
+                and a.head_dim in (64, 128, 256) and q.dtype == k_new.dtype == v_new.dtype
+                and tuple(q.shape) == (len(self._requests), a.heads, a.head_dim) and q.device == self.device
+                and self.steps_done < self.max_new_tokens)
+
+    def _fused_plan(self, q):
+        """(max_seq_len, launch plan) of a one-launch step whose grid fits one workgroup per CU, else None."""
+
+        from .triton_utils import device_cu_count, launch_plan
+
+        a = self.allocator
+        # every row covers its appended token: the longest request after the step, in whole pages
+        max_seq_len = -(-(max(self.host_lengths) + 1) // self.page) * self.page
+        rows = len(self._requests) * a.heads
+        plan = launch_plan(max_seq_len, rows, a.head_dim, self.page, self.page, self.device,
+                           light=q.dtype == torch.float16)
+        if rows * plan[3] > device_cu_count(self.device):
+            return None
+        return max_seq_len, plan
+
+    def _step_fused(self, q, k_new, v_new, fused_plan) -> torch.Tensor:
+        from .triton_utils import MERGE_MAX_WAVES, merge_area
+
+        n, a = len(self._requests), self.allocator
+        for t in (k_new, v_new):
+            if t.shape != (n, a.heads, 1, a.head_dim):
+                raise ValueError(f"expected new K/V of shape {(n, a.heads, 1, a.head_dim)}, got {tuple(t.shape)}")
+            if t.device != self.device:
+                raise ValueError("new K/V must be on the allocator's device")
+        if self.steps_done >= self._reserved_steps:
+            self._reserve(min(self.max_new_tokens, self.steps_done + self.reserve_steps))
+            self._upload_table()
+        lib = _lib.require()
+        q_c, k_c, v_c = q.contiguous(), k_new.contiguous(), v_new.contiguous()
+        ks, vs = a.k_quant, a.v_quant
+        max_seq_len, (tiled, waves, split_tiles, max_splits, _) = fused_plan
+        rows = n * a.heads
+        out = torch.empty_like(q_c)
+        area, area_bytes, workspace, ws_bytes = None, 0, None, 0
+        if max_splits > 1 and waves <= MERGE_MAX_WAVES:
+            area, area_bytes = merge_area(self.device, rows, max_splits, a.head_dim)
+        elif max_splits > 1:
+            ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, a.head_dim))
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=self.device)
+        nxt = 1 - self._cur
+        _lib.check(lib.fs_paged_decode_append_i8(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), k_c.data_ptr(), v_c.data_ptr(), ks.values.data_ptr(),
+            ks.scale.data_ptr(), ks.zero_point.data_ptr(), vs.values.data_ptr(), vs.scale.data_ptr(),
+            vs.zero_point.data_ptr(), self.block_table.data_ptr(), 4, int(self.block_table.shape[1]),
+            self._lengths[self._cur].data_ptr(), self._lengths[nxt].data_ptr(), out.data_ptr(), _lib.ptr(workspace),
+            ws_bytes, _lib.ptr(area), area_bytes, n, a.heads, a.head_dim, int(ks.values.shape[0]), self.page,
+            max_seq_len, 1.0 / math.sqrt(a.head_dim), split_tiles, max_splits, waves, _lib.stream_ptr(self.device)))
+        self._cur = nxt
+        self.steps_done += 1
+        for i, r in enumerate(self._requests):
+            self.host_lengths[i] += 1
+            r.length += 1
+        return out
 
     def close(self) -> None:
         """Return reserved pages that hold no token to the front of the free list, in taken order."""

@@ -136,7 +136,7 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     stream = _lib.stream_ptr(dev)
     if tiled and max_splits > 1 and waves <= MERGE_MAX_WAVES:
         # split rows merge inside the decode launch (no workspace, no merge launch)
-        area, area_bytes = merge_area(dev, rows, max_splits, head_dim)
+        area, area_bytes = merge_area(dev, rows, max_splits, head_dim, stream)
         _lib.check(lib.fs_fused_decode_merged(
             q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kv_format_code(per_channel, is_fp8(k_quant)),
             *(t.data_ptr() for t in kv), _lib.ptr(lengths_c), out.data_ptr(), area.data_ptr(), area_bytes, batch,

@@ -117,7 +117,7 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
     stream = _lib.stream_ptr(dev)
     if tiled and max_splits > 1 and waves <= MERGE_MAX_WAVES:
         # split rows merge inside the decode launch (no workspace, no merge launch)
-        area, area_bytes = merge_area(dev, rows, max_splits, head_dim)
+        area, area_bytes = merge_area(dev, rows, max_splits, head_dim, stream)
         _lib.check(lib.fs_paged_decode_merged(
             q_c.data_ptr(), _lib.dtype_code(q_c.dtype), kv_format_code(per_channel, is_fp8(kq)),
             *(t.data_ptr() for t in kv), table.data_ptr(), table.element_size(), int(table.shape[1]),

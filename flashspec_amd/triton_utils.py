@@ -90,18 +90,24 @@ _MERGE_AREA_MIN_BYTES = 1 << 16
 MERGE_MAX_WAVES = 8
 
 
-def merge_area(device, rows: int, max_splits: int, head_dim: int):
-    """(tensor, bytes) of a zero-filled merge area for one decode launch on the current stream."""
+@functools.lru_cache(maxsize=256)
+def _merge_area_bytes(rows: int, max_splits: int, head_dim: int) -> int:
+    return int(_lib.require().fs_decode_merge_area_bytes(rows, max_splits, head_dim))
+
+
+def merge_area(device, rows: int, max_splits: int, head_dim: int, stream: int | None = None):
+    """(tensor, bytes) of a zero-filled merge area for one decode launch on the current stream
+    (``stream``: its handle, when the caller has it already)."""
 
     import torch
 
-    lib = _lib.require()
-    need = int(lib.fs_decode_merge_area_bytes(rows, max_splits, head_dim))
+    need = _merge_area_bytes(rows, max_splits, head_dim)
     if torch.cuda.is_current_stream_capturing():
         area = torch.zeros(need, dtype=torch.uint8, device=device)
         return area, need
-    stream = torch.cuda.current_stream(device)
-    key = (stream.device.index, stream.cuda_stream)
+    dev = torch_device(device)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (index, stream if stream is not None else _lib.stream_ptr(dev))
     area = _MERGE_AREAS.get(key)
     if area is None or area.numel() < need:
         area = torch.zeros(max(need, _MERGE_AREA_MIN_BYTES), dtype=torch.uint8, device=device)
@@ -171,13 +177,17 @@ MAX_TILES_PER_WAVE = 64
 # 41.0 vs 37.5 us, pages of two quant blocks: 45.2 vs 44.5 us) and grids of more than one
 # workgroup per CU (ragged B16: 56.5 vs 49.7 us) keep more waves, and so do half-empty grids
 # (B4 S2048 in one split: 21.8 us with 4 waves, 18.2 with 8, 19.3 with 16).
+# Splits of 64..127 light tiles take 4 waves as well, with the in-kernel split merge: measured on
+# MI355X (paged H32 D128, one box, direct C-ABI loop), B4 S2048 (C1, 128 rows of 128 tiles) 2 splits
+# x 4 waves merged 16.48 us against 17.67 unsplit x 8 (the plan before) and 18.33 for 2 x 4 with the
+# merge launch; B2 S4096 4 x 4 merged 17.52 against 20.62 for 4 x 16 with the merge launch.
 LIGHT_WAVES = 4
-LIGHT_MIN_SPLIT_TILES = 128
-# Rows that fill at least half of the CUs split in two only when each half keeps 128 tiles;
-# otherwise they run unsplit with at most 8 waves per workgroup.  Measured on MI355X, B4 H32
-# S2048 D128 (128 rows of 128 tiles), paged / fused us: unsplit x 8 waves 18.2 / 17.6, unsplit x
-# 16 19.3 / 18.0, 2 splits x 16 (the plan before) 19.1 / 18.4; B4 S4096 (256 tiles) keeps its
-# split: 2 x 4 waves 29.1 / 27.9 against unsplit x 8 29.9 / 29.3.
+LIGHT_MIN_SPLIT_TILES = 64
+# Rows that fill at least half of the CUs split in two only when each half keeps 128 tiles (light
+# tiles: LIGHT_MIN_SPLIT_TILES); otherwise they run unsplit with at most 8 waves per workgroup.
+# Measured on MI355X before the in-kernel merge, B4 H32 S2048 D128 (fp16 query), paged / fused us:
+# unsplit x 8 waves 18.2 / 17.6, unsplit x 16 19.3 / 18.0, 2 splits x 16 19.1 / 18.4;
+# B4 S4096 (256 tiles) keeps its split: 2 x 4 waves 29.1 / 27.9 against unsplit x 8 29.9 / 29.3.
 HALVE_MIN_SPLIT_TILES = 128
 HALF_EMPTY_WAVES = 8
 GENERIC_WAVES_PER_CU = 16
@@ -249,9 +259,10 @@ def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: 
         else:
             n = max(1, math.ceil(cu_count / max(1, rows)))
             n = min(n, max(1, math.ceil(tiles / MIN_SPLIT_TILES)))
-            if n == 2 and tiles < 2 * HALVE_MIN_SPLIT_TILES:
+            halve_min = LIGHT_MIN_SPLIT_TILES if light and grp == 1 else HALVE_MIN_SPLIT_TILES
+            if n == 2 and tiles < 2 * halve_min:
                 # half the CUs or more already hold a row: a two-way split saves less than its
-                # merge launch costs unless each half keeps HALVE_MIN_SPLIT_TILES tiles
+                # merge costs unless each half keeps halve_min tiles
                 n, half_empty = 1, True
         n = min(n, groups)
         split_groups = math.ceil(groups / n)

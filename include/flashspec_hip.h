@@ -411,6 +411,29 @@ int fs_append_tokens_i8(const void* k_new, const void* v_new, int src_dtype,
                         const int64_t* lengths_in, int64_t* lengths_out,
                         int batch, int heads, int head_dim, int page_size, void* stream);
 
+/* One serving decode step in one launch: fs_append_tokens_i8 followed by paged decode attention
+ * over the advanced lengths, with the append done inside the decode kernel.  For every request b,
+ * the wave whose tile holds position pos = lengths_in[b] requantizes that page (the op sequence
+ * and results of fs_append_tokens_i8, bit for bit) and attends over it from registers; every row
+ * covers pos + 1 tokens.  lengths_out[b] = pos + 1, or pos when the page is not backed (table
+ * entry -1 or out of range) or pos >= max_seq_len -- such a token is dropped and stays masked.
+ * Needs 16-token pages holding one quant block, head_dim 64 / 128 / 256, and k_new / v_new
+ * ([batch, heads, 1, head_dim]) in q's dtype; max_seq_len must exceed every lengths_in[b] for
+ * the token to be kept.  Rows that split merge through `merge_area` when it is given
+ * (fs_paged_decode_merged's contract), else through `workspace` and a merge launch made here.
+ * Replaces the serving step's PagedKVAllocator.append_batch + paged attention pair
+ * (reference src/flashspec/paged.py:108-144 and serving.py:126-163). */
+int fs_paged_decode_append_i8(const void* q, int q_dtype, const void* k_new, const void* v_new,
+                              int8_t* k_values, float* k_scale, int16_t* k_zero,
+                              int8_t* v_values, float* v_scale, int16_t* v_zero,
+                              const void* block_table, int table_index_bytes, int64_t table_cols,
+                              const int64_t* lengths_in, int64_t* lengths_out, void* out,
+                              void* workspace, int64_t workspace_bytes,
+                              void* merge_area, int64_t merge_area_bytes,
+                              int batch, int heads, int head_dim, int64_t num_pages, int page_size,
+                              int max_seq_len, float sm_scale, int split_tiles, int max_splits,
+                              int waves_per_block, void* stream);
+
 /* Measurement helper with no counterpart in the reference: one plain streaming read of
  * `bytes` (a positive multiple of 16, `src` 16-byte aligned) by `blocks` workgroups of 256
  * lanes, non-temporal 16-byte loads in a grid-stride loop (the decode kernels' load form).  Its rate is the practical HBM read ceiling that

@@ -1,4 +1,4 @@
-// Division used by the vectorized INT8 quantizer (flashspec_amd/csrc/fs_quant.hip,
+// Division used by the vectorized INT8 quantizer (flashspec_amd/csrc/fs_common.h,
 // div_by_scale): q1 = fma(fma(-q0, b, a), y, q0) with y = RN(1/b), q0 = RN(a*y).
 // Compares q1 with IEEE a/b for every finite fp16 value a (and random fp32 values) over
 // quantizer-like scales (mx - mn) / 255, all-ones significands and random normals, and

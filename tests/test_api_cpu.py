@@ -146,7 +146,9 @@ def test_split_plan_covers_every_tile(clean_env):
     assert plan(16384, 32, 128, 256, light=True) == (128, 8, 4)
     assert plan(4096, 512, 128, 256, light=True) == (256, 1, 16)   # two workgroups per CU
     assert plan(8192, 256, 128, 256, light=True) == (512, 1, 16)   # 4 waves would need a second split
-    assert plan(1024, 256, 128, 256, light=True) == (64, 1, 16)    # short rows
+    assert plan(1024, 256, 128, 256, light=True) == (64, 1, 4)     # short rows: 16 tiles per wave
+    assert plan(4096, 64, 128, 256, light=True) == (64, 4, 4)      # 4 splits of 64 tiles, merged in-kernel
+    assert plan(512, 256, 128, 256, light=True) == (32, 1, 8)      # under 64 tiles: the general rule
     assert plan(4096, 96, 128, 256, light=True) == (86, 3, 16)
     assert plan(4096, 160, 128, 256, light=True) == (128, 2, 16)   # 320 workgroups: more than one per CU
     clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1")  # 128 of 256 CUs busy: not full enough for 4 waves
@@ -155,11 +157,12 @@ def test_split_plan_covers_every_tile(clean_env):
     clean_env.setenv("FLASHSPEC_NUM_WARPS", "16")
     assert plan(4096, 256, 128, 256, waves=triton_utils.forced_tiled_waves(), light=True) == (256, 1, 16)
     clean_env.delenv("FLASHSPEC_NUM_WARPS")
-    # half the CUs hold a row: split in two only when each half keeps 128 tiles, else run
-    # unsplit with 8 waves (C1: B4 H32 S2048)
+    # half the CUs hold a row: split in two only when each half keeps 128 tiles (64 for light
+    # tiles, whose 4-wave splits merge in-kernel), else run unsplit with 8 waves (C1: B4 H32 S2048)
     assert plan(2048, 128, 128, 256) == (128, 1, 8)
     assert plan(4096, 128, 128, 256) == (128, 2, 16)
-    assert plan(2048, 128, 128, 256, light=True) == (128, 1, 8)
+    assert plan(2048, 128, 128, 256, light=True) == (64, 2, 4)
+    assert plan(1024, 128, 128, 256, light=True) == (64, 1, 8)     # halves of 32 tiles: unsplit
     # few rows: split rows to fill the GPU; workgroup size follows the split length
     assert plan(2048, 64, 128, 256) == (32, 4, 8)
     assert plan(1500, 8, 128, 256) == (8, 12, 2)   # the reference's split-K test shape splits

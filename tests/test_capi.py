@@ -99,6 +99,16 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert rc == _lib.FS_ERR_INVALID and "differ" in lib.fs_last_error().decode()
     rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 2, 4, 7, 9, 2, 2, 64, 16, None)
     assert rc == _lib.FS_ERR_INVALID and "int32 or int64" in lib.fs_last_error().decode()
+    # fused append + decode: 16-token pages, head_dim 64 / 128 / 256, two lengths buffers
+
+    def fused(page, D, lens_in, lens_out):
+        return lib.fs_paged_decode_append_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, lens_in, lens_out, 1, None, 0,
+                                             None, 0, 2, 2, D, 8, page, 64, 0.1, 4, 1, 1, None)
+
+    assert fused(32, 128, 7, 9) == _lib.FS_ERR_INVALID and "16-token pages" in lib.fs_last_error().decode()
+    assert fused(16, 96, 7, 9) == _lib.FS_ERR_INVALID and "64, 128 or 256" in lib.fs_last_error().decode()
+    assert fused(16, 128, 7, 7) == _lib.FS_ERR_INVALID and "lengths_out" in lib.fs_last_error().decode()
+    assert fused(16, 128, 7, None) == _lib.FS_ERR_INVALID
 
 
 def test_no_alloc_entry_point_rejects_plans_beyond_its_array():

@@ -90,12 +90,20 @@ def test_decode_batch_bit_exact_against_oracle_allocator(src_dtype, D):
         assert alloc._requests[rid].logical_blocks == ora.requests[rid]["blocks"]
 
 
-def test_decode_batch_attention_bit_identical_to_allocator_cache():
+def test_decode_batch_attention_bit_identical_to_allocator_cache(monkeypatch):
+    """A small batch (32 rows): every step is one fs_paged_decode_append_i8 launch (append is never
+    called) and matches the allocator's int64-table cache bit for bit."""
+
     H, D = 8, 128
     announce("decode batch int32 device table vs allocator int64 table")
     alloc, rids = build_request_pool([300, 17, 1000, 64], heads=H, head_dim=D, headroom_tokens=32, seed=4,
                                      device=DEV)
     batch = DecodeBatch(alloc, rids, max_new_tokens=20, reserve_steps=4)
+
+    def no_separate_append(*_a, **_k):
+        raise AssertionError("a one-round grid should take the one-launch step")
+
+    monkeypatch.setattr(DecodeBatch, "append", no_separate_append)
     for step in range(20):
         q = randn((4, H, D), 40 + step).to(DEV)
         kn, vn = randn((4, H, 1, D), 60 + step).to(DEV), randn((4, H, 1, D), 80 + step).to(DEV)
@@ -134,14 +142,18 @@ def _expected_page(before, row, token, H, bs, D):
     return oq.quantize_int8_per_block(blk, bs)
 
 
-@pytest.mark.parametrize("forced_splits", [None, "4"])
-def test_serving_step_at_scale_b64_ragged_shuffled_pool(monkeypatch, forced_splits):
+@pytest.mark.parametrize("forced_splits,fused", [(None, False), ("4", False), (None, True), ("4", True)])
+def test_serving_step_at_scale_b64_ragged_shuffled_pool(monkeypatch, forced_splits, fused):
+    """fused: DecodeBatch.step (which takes two launches here: 2048 rows are several rounds of
+    workgroups); else append, then attend."""
+
     B, H, D, bs, steps = 64, 32, 128, 16, 3
     g = torch.Generator().manual_seed(2024)
     lengths = torch.randint(128, 16385, (B,), generator=g).tolist()
     lengths[5] = 16384 - 1  # a request that crosses into a new page on the second step
     lengths[9] = 128        # one exactly at a page boundary: the first append opens a page
-    announce(f"serving step B{B} H{H} D{D} ragged [128,16384] sum {sum(lengths)} splits {forced_splits}")
+    announce(f"serving step B{B} H{H} D{D} ragged [128,16384] sum {sum(lengths)} splits {forced_splits} "
+             f"fused {fused}")
     if forced_splits:
         monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", forced_splits)
     alloc, rids = build_request_pool(lengths, heads=H, head_dim=D, headroom_tokens=16, seed=7, device=DEV)
@@ -158,9 +170,13 @@ def test_serving_step_at_scale_b64_ragged_shuffled_pool(monkeypatch, forced_spli
             before[i] = (pos, page)
         pre = {i: (_page_copy(alloc.k_quant, p), _page_copy(alloc.v_quant, p)) for i, (_, p) in before.items()
                if p is not None}
-        out, stats = None, None
-        batch.append(kn.to(DEV), vn.to(DEV))
-        out, stats = batch.attend(q, return_stats=True)
+        if fused:
+            out = batch.step(q, kn.to(DEV), vn.to(DEV))
+            plain, stats = batch.attend(q, return_stats=True)
+            assert torch.equal(out, plain), f"step {step}: fused step vs decode over the appended cache"
+        else:
+            batch.append(kn.to(DEV), vn.to(DEV))
+            out, stats = batch.attend(q, return_stats=True)
         torch.cuda.synchronize(DEV)
         announce(f"step {step}: num_splits {stats['num_splits']}")
         if forced_splits:
@@ -193,3 +209,110 @@ def test_simulation_uses_device_batch_and_keeps_allocator_consistent():
     assert res["finishes"] == 8 and res["arrivals"] == 12
     assert res["generated_tokens"] == 48
     assert res["used_tokens"] > 0 and 0.0 < res["block_utilization"] <= 1.0
+
+
+def _append_then_decode_reference(cache, kn, vn, lens_in, plan):
+    """fs_append_tokens_i8 followed by the paged decode over the advanced lengths (two launches)."""
+
+    lib = _lib.require()
+    ks, vs = cache.k_quant, cache.v_quant
+    B, H, _, D = kn.shape
+    lens_out = torch.empty_like(lens_in)
+    table = cache.block_table
+    _lib.check(lib.fs_append_tokens_i8(
+        kn.data_ptr(), vn.data_ptr(), _lib.dtype_code(kn.dtype), ks.values.data_ptr(), ks.scale.data_ptr(),
+        ks.zero_point.data_ptr(), vs.values.data_ptr(), vs.scale.data_ptr(), vs.zero_point.data_ptr(),
+        int(ks.values.shape[0]), table.data_ptr(), table.element_size(), int(table.shape[1]), lens_in.data_ptr(),
+        lens_out.data_ptr(), B, H, D, cache.block_size, _lib.stream_ptr(DEV)))
+    after = fa.PagedKVCache(k_quant=ks, v_quant=vs, block_table=table, lengths=lens_out, block_size=cache.block_size,
+                            max_seq_len=plan["max_seq_len"])
+    return lens_out, after
+
+
+def _fused_append_decode(cache, q, kn, vn, lens_in, plan):
+    lib = _lib.require()
+    from flashspec_amd.triton_utils import MERGE_MAX_WAVES, launch_plan, merge_area
+
+    ks, vs = cache.k_quant, cache.v_quant
+    B, H, D = q.shape
+    tiled, waves, split_tiles, max_splits, _ = launch_plan(plan["max_seq_len"], B * H, D, cache.block_size,
+                                                           cache.block_size, DEV, light=q.dtype == torch.float16)
+    assert tiled
+    area, area_bytes, ws, ws_bytes = None, 0, None, 0
+    if max_splits > 1 and waves <= MERGE_MAX_WAVES:
+        area, area_bytes = merge_area(DEV, B * H, max_splits, D)
+    elif max_splits > 1:
+        ws_bytes = int(lib.fs_decode_workspace_bytes(B * H, max_splits, D))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(q)
+    lens_out = torch.full_like(lens_in, -7)
+    table = cache.block_table
+    _lib.check(lib.fs_paged_decode_append_i8(
+        q.data_ptr(), _lib.dtype_code(q.dtype), kn.data_ptr(), vn.data_ptr(), ks.values.data_ptr(),
+        ks.scale.data_ptr(), ks.zero_point.data_ptr(), vs.values.data_ptr(), vs.scale.data_ptr(),
+        vs.zero_point.data_ptr(), table.data_ptr(), table.element_size(), int(table.shape[1]), lens_in.data_ptr(),
+        lens_out.data_ptr(), out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(area), area_bytes, B, H, D,
+        int(ks.values.shape[0]), cache.block_size, plan["max_seq_len"], 1.0 / float(D) ** 0.5, split_tiles,
+        max_splits, waves, _lib.stream_ptr(DEV)))
+    return out, lens_out, max_splits, waves
+
+
+def _clone_cache(cache):
+    def qt(t):
+        return fa.QuantizedTensor(t.values.clone(), t.scale.clone(), t.zero_point.clone(), t.block_size,
+                                  t.original_shape)
+
+    return fa.PagedKVCache(k_quant=qt(cache.k_quant), v_quant=qt(cache.v_quant), block_table=cache.block_table.clone(),
+                           lengths=cache.lengths.clone(), block_size=cache.block_size, max_seq_len=cache.max_seq_len)
+
+
+@pytest.mark.parametrize("H,D,qdt,splits,warps", [
+    (8, 128, torch.float16, None, None),      # few rows: splits merged in-kernel
+    (8, 128, torch.float16, "3", "16"),       # 16-wave splits: workspace + merge launch
+    (32, 128, torch.float16, None, None),     # one split per row
+    (8, 64, torch.bfloat16, None, None),
+    (4, 256, torch.float32, "2", None),
+])
+def test_fused_append_decode_bit_identical_to_append_then_decode(monkeypatch, H, D, qdt, splits, warps):
+    """fs_paged_decode_append_i8 against fs_append_tokens_i8 + paged decode on a copy of the same
+    store: pages, scales, zero points, advanced lengths and outputs bit-identical.  Positions: a
+    page's first row (64), its last row (399), mid-page rows (37, 1), the last, part-padded page
+    (699), a table entry of -1 at the position (250: token dropped, length kept) and a position
+    past the table and max_seq_len (710: likewise)."""
+
+    if splits:
+        monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", splits)
+    if warps:
+        monkeypatch.setenv("FLASHSPEC_NUM_WARPS", warps)
+    B, S, bs, max_seq = 7, 700, 16, 704
+    announce(f"fused append+decode B{B} H{H} D{D} S{S} q {qdt} splits {splits} warps {warps}")
+    k, v = randn((B, H, S, D), 71), randn((B, H, S, D), 72)
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=bs, block_table_pattern="shuffled",
+                                       layout_seed=3)
+    pos = [64, 399, 37, 250, 1, 699, 710]
+    table = cache.block_table.clone()
+    table[3, 250 // bs] = -1
+    cache = fa.PagedKVCache(k_quant=cache.k_quant, v_quant=cache.v_quant, block_table=table,
+                            lengths=cache.lengths, block_size=bs, max_seq_len=cache.max_seq_len)
+    lens_in = torch.tensor(pos, dtype=torch.int64, device=DEV)
+    plan = {"max_seq_len": max_seq}
+    q = randn((B, H, D), 73, qdt).to(DEV)
+    kn, vn = randn((B, H, 1, D), 74, qdt).to(DEV), randn((B, H, 1, D), 75, qdt).to(DEV)
+    ref_cache = _clone_cache(cache)
+    lens_ref, after = _append_then_decode_reference(ref_cache, kn, vn, lens_in, plan)
+    ref = fa.paged_quant_attention_triton(q, after)
+    out, lens_out, max_splits, waves = _fused_append_decode(cache, q, kn, vn, lens_in, plan)
+    torch.cuda.synchronize(DEV)
+    announce(f"plan: {max_splits} splits x {waves} waves")
+    assert lens_out.tolist() == lens_ref.tolist() == [65, 400, 38, 250, 2, 700, 710]
+    for ours, theirs, name in ((cache.k_quant, ref_cache.k_quant, "K"), (cache.v_quant, ref_cache.v_quant, "V")):
+        assert torch.equal(ours.values, theirs.values), f"{name} values"
+        assert torch.equal(ours.scale.view(torch.int32), theirs.scale.view(torch.int32)), f"{name} scales"
+        assert torch.equal(ours.zero_point, theirs.zero_point), f"{name} zero points"
+    assert torch.equal(out, ref), "fused output vs append + decode"
+    # against the oracle on the appended store; request 3 keeps a -1 entry inside its length, which
+    # the reference PyTorch path reads as page 0 (the documented divergence), so it is left out
+    keep = [0, 1, 2, 4, 5, 6]
+    ora = op.OracleCache(from_qt(cache.k_quant), from_qt(cache.v_quant), np_of(table)[keep],
+                         np.array(lens_out.tolist(), dtype=np.int64)[keep], bs, max_seq)
+    assert_attention_close(out[keep], oa.paged_quant_attention(np_of(q.float())[keep], ora), qdt, "fused vs oracle")

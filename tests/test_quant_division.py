@@ -1,5 +1,5 @@
 """The vectorized quantizer divides by the block scale with a reciprocal and one FMA
-correction step (flashspec_amd/csrc/fs_quant.hip, div_by_scale).  This checks, on the CPU
+correction step (flashspec_amd/csrc/fs_common.h, div_by_scale).  This checks, on the CPU
 with a correctly rounded fmaf, that the step reproduces IEEE float32 division bit for bit
 over every finite fp16 input and random fp32 inputs, for quantizer-like scales, all-ones
 significands and random normal scales (only the sign of a zero quotient may differ)."""
