@@ -74,6 +74,12 @@ _SIGNATURES = {
          c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int,
          c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_void_p],
     ),
+    "fs_tree_verify_merged": (
+        c_int,
+        [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+         c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int,
+         c_int64, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_int, c_void_p],
+    ),
     "fs_tree_mfma_path": (c_int, [c_int, c_int, c_int]),
     "fs_tree_nodes_per_workgroup": (c_int, [c_int, c_int, c_int, c_int, c_int64, c_int]),
     "fs_quantize_i8_channel": (

@@ -603,30 +603,6 @@ __device__ __forceinline__ float allreduce_groups(float x) {
 // is all zero again when the kernel ends.  Nobody waits for
 // a workgroup that has not yet arrived; the waits end within the latency of stores already issued
 // (bounded by kMergeSpins regardless, after which the row is written as NaN).
-constexpr int kMergeSpins = 1 << 14;
-
-__device__ __forceinline__ void publish(unsigned long long* w, float x) {
-  __hip_atomic_store(w, (1ull << 32) | __float_as_uint(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void clear_word(unsigned long long* w) {
-  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ unsigned long long load_word(const unsigned long long* w) {
-  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The value of word w, given a first load v of it: reloads until the tag is set.
-__device__ __forceinline__ float settle_word(unsigned long long v, const unsigned long long* w, bool& ok) {
-  for (int n = 0; (v >> 32) != 1ull && n < kMergeSpins; ++n) {
-    __builtin_amdgcn_s_sleep(1);
-    v = load_word(w);
-  }
-  ok = ok && (v >> 32) == 1ull;
-  return __uint_as_float((unsigned)v);
-}
-
 // Thread tid holds dims tid + k * blockDim.x (k < DPT) of its split's un-normalized state a[k], with
 // the split's max M (log2 units) and denominator L.
 template <int DPT, typename QT>

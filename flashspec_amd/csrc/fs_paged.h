@@ -80,6 +80,34 @@ struct DecodeParams {
   int64_t* lengths_out;
 };
 
+// Words of the in-kernel split merge (decode rows and tree verification): a split's state goes out
+// as 64-bit words tagged 1 in the upper half with relaxed agent-scope atomic stores, so a reader
+// sees a word whole or not at all and waits on the tag, not on a fence; the waits are bounded by
+// kMergeSpins (a row whose words never land is written as NaN).
+constexpr int kMergeSpins = 1 << 14;
+
+__device__ __forceinline__ void publish(unsigned long long* w, float x) {
+  __hip_atomic_store(w, (1ull << 32) | __float_as_uint(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void clear_word(unsigned long long* w) {
+  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long load_word(const unsigned long long* w) {
+  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The value of word w, given a first load v of it: reloads until the tag is set.
+__device__ __forceinline__ float settle_word(unsigned long long v, const unsigned long long* w, bool& ok) {
+  for (int n = 0; (v >> 32) != 1ull && n < kMergeSpins; ++n) {
+    __builtin_amdgcn_s_sleep(1);
+    v = load_word(w);
+  }
+  ok = ok && (v >> 32) == 1ull;
+  return __uint_as_float((unsigned)v);
+}
+
 // Bytes of a merge area: the counts padded to 256 bytes, then the slots.
 __host__ __device__ inline int64_t merge_area_bytes(int64_t rows, int64_t max_splits, int64_t head_dim) {
   return (rows * 4 + 255) / 256 * 256 + rows * max_splits * (head_dim + 2) * 8;

@@ -215,17 +215,15 @@ __device__ __forceinline__ int tree_parent_lane(const int64_t* parents, int b, i
   return (pa >= 0 && pa < lane) ? (int)pa : -1;
 }
 
-// Finishes row (b, n, h) of a tree verification from its merged prefix state (running max M
-// in log2 units, denominator L, accumulator over dims lane + 64c): attends to the draft
-// tokens on node n's path to the root (parents[b, a]; a parent outside [0, a) ends the path,
-// at most nq steps) with the same online softmax and writes the output row.  With nq <= 64
-// the path is walked in registers over `pl` (tree_parent_lane) and its tokens are taken four
-// at a time, so their K/V rows load together; larger trees walk parents in memory.
+// Adds to row (b, n, h)'s softmax state (running max M in log2 units, denominator L,
+// accumulator over dims lane + 64c) the draft tokens on node n's path to the root (parents[b, a];
+// a parent outside [0, a) ends the path, at most nq steps), with the same online softmax.  With
+// nq <= 64 the path is walked in registers over `pl` (tree_parent_lane) and its tokens are taken
+// four at a time, so their K/V rows load together; larger trees walk parents in memory.
 template <typename QT, typename DT>
-__device__ __forceinline__ void tree_path_finish(float M, float L, float (&acc)[4], int pl, const QT* qrow,
-                                                 const DT* dk, const DT* dv, const int64_t* parents, QT* orow,
-                                                 int b, int n, int h, int nq, int heads, int D, float qk_scale,
-                                                 int lane) {
+__device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (&acc)[4], int pl, const QT* qrow,
+                                                     const DT* dk, const DT* dv, const int64_t* parents, int b, int n,
+                                                     int h, int nq, int heads, int D, float qk_scale, int lane) {
   float qv[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -305,6 +303,15 @@ __device__ __forceinline__ void tree_path_finish(float M, float L, float (&acc)[
       a = (pa >= 0 && pa < a) ? (int)pa : -1;
     }
   }
+}
+
+// tree_path_accumulate, then the output row acc / L.
+template <typename QT, typename DT>
+__device__ __forceinline__ void tree_path_finish(float M, float L, float (&acc)[4], int pl, const QT* qrow,
+                                                 const DT* dk, const DT* dv, const int64_t* parents, QT* orow,
+                                                 int b, int n, int h, int nq, int heads, int D, float qk_scale,
+                                                 int lane) {
+  tree_path_accumulate<QT, DT>(M, L, acc, pl, qrow, dk, dv, parents, b, n, h, nq, heads, D, qk_scale, lane);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int d = lane + c * kWave;
@@ -361,6 +368,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   __shared__ float s_ml[tree_waves_cap_dp(DP) * kNodeGroup * 2];
   __shared__ float s_fin[kNodeGroup * ROW];  // merged states of the group's nodes (fused tail)
   __shared__ float s_finml[kNodeGroup * 2];
+  __shared__ int s_last;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -637,6 +645,31 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   }
 
   const int pl = p.fuse_tail ? tree_parent_lane(p.parents, b, nq, lane) : -1;
+  // Rows of several splits with fuse_tail and a merge area merge inside the launch: each split
+  // publishes its per-node states (fs_paged.h's tagged words, slots [row, split, D + 2] with row =
+  // (b * nq + node) * heads + h) and counts itself in on the workgroup's (request, head, node
+  // group) unit; the last split to arrive merges every node in split order and finishes it.
+  const bool merge_here = p.fuse_tail && p.merge_count != nullptr && nsplit > 1;
+  const size_t rs = (size_t)D + 2;
+  auto slot = [&](int node, int sp) {
+    return p.merge_slots + (((size_t)b * nq + node) * p.heads + h) * p.max_splits * rs + (size_t)sp * rs;
+  };
+  // one split's rows: wave w finishes the group's nodes w, w + W, ... from s_fin / s_finml
+  auto finish_group = [&](int gnode0, int nodes_here) {
+    for (int n = w; n < nodes_here; n += W) {
+      const int node = gnode0 + n;
+      const size_t row = ((size_t)b * nq + node) * p.heads + h;
+      float fin[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = lane + c * kWave;
+        fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
+      }
+      tree_path_finish<QT, QT>(s_finml[2 * n], s_finml[2 * n + 1], fin, pl, (const QT*)p.q + row * D,
+                               (const QT*)p.draft_k, (const QT*)p.draft_v, p.parents, (QT*)p.out + row * D, b, node,
+                               h, nq, p.heads, D, p.qk_scale, lane);
+    }
+  };
   // The node groups merge one at a time through the same LDS buffers.
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
@@ -685,23 +718,143 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
       }
     }
     if (!p.fuse_tail) continue;
-    // one split: the workgroup finishes the group's rows (path tokens, output), wave w taking
-    // nodes w, w + W, ...
     __syncthreads();
+    if (!merge_here) {
+      // one split: the workgroup finishes the group's rows (path tokens, output)
+      finish_group(gnode0, nodes_here);
+      continue;
+    }
+    // several splits: wave w publishes the states of the group's nodes w, w + W, ..., the ones with
+    // node % nsplit == split after adding their path tokens (each path joins exactly one split's
+    // state: the merge is associative), so the path work is spread over the splits and done
+    // before the merge
     for (int n = w; n < nodes_here; n += W) {
       const int node = gnode0 + n;
-      const size_t row = ((size_t)b * nq + node) * p.heads + h;
-      float fin[4];
+      float M = s_finml[2 * n], L = s_finml[2 * n + 1], fin[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d = lane + c * kWave;
         fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
       }
-      tree_path_finish<QT, QT>(s_finml[2 * n], s_finml[2 * n + 1], fin, pl, (const QT*)p.q + row * D,
-                               (const QT*)p.draft_k, (const QT*)p.draft_v, p.parents, (QT*)p.out + row * D, b, node,
-                               h, nq, p.heads, D, p.qk_scale, lane);
+      if (node % nsplit == split) {
+        const size_t row = ((size_t)b * nq + node) * p.heads + h;
+        tree_path_accumulate<QT, QT>(M, L, fin, pl, (const QT*)p.q + row * D, (const QT*)p.draft_k,
+                                     (const QT*)p.draft_v, p.parents, b, node, h, nq, p.heads, D, p.qk_scale, lane);
+      }
+      unsigned long long* ws = slot(node, split);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = lane + c * kWave;
+        if (d < D) publish(ws + d, fin[c]);
+      }
+      if (lane == 0) {
+        publish(ws + D, M);
+        publish(ws + D + 1, L);
+      }
     }
   }
+  if (!merge_here) return;
+
+  __syncthreads();  // every word of this split is on its way before it counts itself in
+  const int unit = (b * p.heads + h) * groups + u.grp;
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(p.merge_count + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)(nsplit - 1);
+  __syncthreads();
+  if (!s_last) return;  // the whole workgroup
+  // Per node group: (1) the (m, l) words of every (node, split), one thread each, into LDS (s_acc is
+  // free now); (2) per node the split weights exp2(m_s - M) and L = sum_s l_s * weight, in split
+  // order; (3) per (node, dim) the output sum_s x_s * weight / L, with each thread's loads of up to
+  // 4 entries x 2 splits issued together before any is waited on.  A word that never lands makes
+  // its row NaN.
+  float* s_w = s_acc;  // [node][split]: m, then the weight
+  float* s_l = s_acc + kNodeGroup * p.max_splits;
+  const int nthr = blockDim.x;
+  for (int gi = 0; gi < NG; ++gi) {
+    const int gnode0 = node0 + gi * kNodeGroup;
+    const int nodes_here = min(kNodeGroup, nq - gnode0);
+    if (gi > 0) __syncthreads();  // the previous group is done with s_acc and s_finml
+    for (int t = threadIdx.x; t < nodes_here * nsplit; t += nthr) {
+      const int n = t / nsplit, sp = t - n * nsplit;
+      const unsigned long long* ws = slot(gnode0 + n, sp);
+      const unsigned long long vm = load_word(ws + D), vl = load_word(ws + D + 1);
+      bool ok = true;
+      const float m = settle_word(vm, ws + D, ok), l = settle_word(vl, ws + D + 1, ok);
+      s_w[n * p.max_splits + sp] = m;
+      s_l[n * p.max_splits + sp] = ok ? l : __builtin_nanf("");  // a NaN weight reaches the whole row
+    }
+    __syncthreads();
+    for (int n = threadIdx.x; n < nodes_here; n += nthr) {
+      float M = kNegBig;
+      for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, s_w[n * p.max_splits + sp]);
+      float L = 0.f;
+      for (int sp = 0; sp < nsplit; ++sp) {
+        const float wgt = fast_exp2(s_w[n * p.max_splits + sp] - M);
+        L = fmaf(s_l[n * p.max_splits + sp], wgt, L);
+        s_w[n * p.max_splits + sp] = wgt;
+      }
+      s_finml[2 * n] = M;
+      s_finml[2 * n + 1] = L;
+    }
+    __syncthreads();
+    constexpr int EB = 4, SB = 2;  // entries and splits per batch of loads
+    for (int e0 = threadIdx.x; e0 < nodes_here * D; e0 += EB * nthr) {
+      float a[EB] = {0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < nsplit; s0 += SB) {
+        unsigned long long v[EB][SB];
+#pragma unroll
+        for (int i = 0; i < EB; ++i) {
+          const int e = e0 + i * nthr;
+          const int n = e / D, d = e - n * D;
+#pragma unroll
+          for (int c = 0; c < SB; ++c)
+            v[i][c] = (e < nodes_here * D && s0 + c < nsplit) ? load_word(slot(gnode0 + n, s0 + c) + d) : 0ull;
+        }
+#pragma unroll
+        for (int i = 0; i < EB; ++i) {
+          const int e = e0 + i * nthr;
+          const int n = e / D, d = e - n * D;
+#pragma unroll
+          for (int c = 0; c < SB; ++c) {
+            if (e < nodes_here * D && s0 + c < nsplit) {
+              bool ok = true;
+              const float x = settle_word(v[i][c], slot(gnode0 + n, s0 + c) + d, ok);
+              a[i] = fmaf(ok ? x : __builtin_nanf(""), s_w[n * p.max_splits + s0 + c], a[i]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < EB; ++i) {
+        const int e = e0 + i * nthr;
+        if (e < nodes_here * D) {
+          const int n = e / D, d = e - n * D;
+          const float L = s_finml[2 * n + 1];
+          const size_t row = ((size_t)b * nq + gnode0 + n) * p.heads + h;
+          ((QT*)p.out)[row * D + d] = from_f32<QT>(L > 0.f ? a[i] / L : 0.f);
+        }
+      }
+    }
+  }
+  // leave the area zero, after a barrier (every word has been read): the words of every node and
+  // split, then the count
+  __syncthreads();
+  for (int gi = 0; gi < NG; ++gi) {
+    const int gnode0 = node0 + gi * kNodeGroup;
+    const int nodes_here = min(kNodeGroup, nq - gnode0);
+    for (int e = threadIdx.x; e < nodes_here * D; e += blockDim.x) {
+      const int n = e / D, d = e - n * D;
+      for (int sp = 0; sp < nsplit; ++sp) {
+        unsigned long long* ws = slot(gnode0 + n, sp);
+        clear_word(ws + d);
+        if (d == 0) {
+          clear_word(ws + D);
+          clear_word(ws + D + 1);
+        }
+      }
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(p.merge_count + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side ---------------------------------------------------------------------------
@@ -852,7 +1005,8 @@ static int tree_verify(const void* q, int q_dtype, const int8_t* k_values, const
                        const void* draft_v, int draft_dtype, const int64_t* parents, void* out, void* workspace,
                        int64_t workspace_bytes, int batch, int nodes, int heads, int head_dim, int64_t num_pages,
                        int page_size, int quant_block, int max_seq_len, float sm_scale, int split_tiles,
-                       int max_splits, int waves_per_block, int prefix_kernel, void* stream, int vfmt, int per_channel) {
+                       int max_splits, int waves_per_block, int prefix_kernel, void* stream, int vfmt, int per_channel,
+                       void* merge_area = nullptr, int64_t merge_bytes = -1) {
   if (prefix_kernel < 0 || prefix_kernel > 4)
     return set_error(FS_ERR_INVALID, "prefix_kernel must be 0 (auto), 1 (row kernel), 2 (multi-query kernel), "
                                      "3 or 4 (multi-query kernel with 16- or 32-node workgroups)");
@@ -869,20 +1023,26 @@ static int tree_verify(const void* q, int q_dtype, const int8_t* k_values, const
   if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
                             table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, nodes,
                             heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
-                            max_splits, waves_per_block, !mq, vfmt, per_channel))
+                            max_splits, waves_per_block, !mq, vfmt, per_channel, merge_area, merge_bytes))
     return rc;
   if (!draft_k || !draft_v || !parents) return set_error(FS_ERR_INVALID, "tree verify: null draft or parents pointer");
   if (draft_dtype != FS_F32 && draft_dtype != FS_F16 && draft_dtype != FS_BF16)
     return set_error(FS_ERR_INVALID, "draft dtype code must be 0, 1 or 2");
+  const bool merged = p.merge_count != nullptr;  // splits merge in the prefix kernel (merge area bound)
+  if (merged && (!mq || draft_dtype != q_dtype))
+    return set_error(FS_ERR_INVALID, "tree verify with a merge area needs the multi-query kernel and drafts in q's "
+                                     "dtype");
   p.force_partials = 1;
+  // drafts in q's dtype and one split (or a merge area): the multi-query kernel finishes the rows
+  // itself; otherwise split partials go to the workspace for the tail kernel
+  const bool finishes = mq && draft_dtype == q_dtype && (p.max_splits == 1 || merged);
   const int64_t need = fs_decode_workspace_bytes(p.rows, p.max_splits, p.head_dim);
-  if (workspace_bytes < need || p.part_acc == nullptr)
+  if (!finishes && (workspace_bytes < need || p.part_acc == nullptr))
     return set_error(FS_ERR_INVALID, "tree verify workspace too small (" + std::to_string(workspace_bytes) + " < " +
                                          std::to_string(need) + " bytes)");
   hipStream_t st = (hipStream_t)stream;
   if (mq) {
-    // one split and drafts in q's dtype: the multi-query kernel finishes the rows itself
-    p.fuse_tail = (p.max_splits == 1 && draft_dtype == q_dtype) ? 1 : 0;
+    p.fuse_tail = finishes ? 1 : 0;
     p.draft_k = draft_k;
     p.draft_v = draft_v;
     p.parents = parents;
@@ -942,4 +1102,26 @@ extern "C" int fs_tree_verify_i8_channel(const void* q, int q_dtype, const int8_
                      table_cols, lengths, draft_k, draft_v, draft_dtype, parents, out, workspace, workspace_bytes, batch,
                      nodes, heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
                      max_splits, waves_per_block, prefix_kernel, stream, kVfInt8, 1);
+}
+
+extern "C" int fs_tree_verify_merged(const void* q, int q_dtype, int kv_format, const void* k_values,
+                                     const float* k_scale, const int16_t* k_zero, const void* v_values,
+                                     const float* v_scale, const int16_t* v_zero, const void* block_table,
+                                     int table_index_bytes, int64_t table_cols, const int64_t* lengths,
+                                     const void* draft_k, const void* draft_v, const int64_t* parents, void* out,
+                                     void* merge_area, int64_t merge_area_bytes, int batch, int nodes, int heads,
+                                     int head_dim, int64_t num_pages, int page_size, int quant_block, int max_seq_len,
+                                     float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                                     int nodes_per_workgroup, void* stream) {
+  if (kv_format != 0 && kv_format != 1)
+    return set_error(FS_ERR_INVALID, "kv_format must be 0 (affine INT8) or 1 (FP8 E4M3) for the multi-query kernel");
+  if (nodes_per_workgroup != 0 && nodes_per_workgroup != 16 && nodes_per_workgroup != 32)
+    return set_error(FS_ERR_INVALID, "nodes_per_workgroup must be 0 (the library's choice), 16 or 32");
+  const int prefix_kernel = nodes_per_workgroup == 16 ? 3 : (nodes_per_workgroup == 32 ? 4 : 2);
+  return tree_verify(q, q_dtype, (const int8_t*)k_values, k_scale, kv_format == 1 ? nullptr : k_zero,
+                     (const int8_t*)v_values, v_scale, kv_format == 1 ? nullptr : v_zero, block_table,
+                     table_index_bytes, table_cols, lengths, draft_k, draft_v, q_dtype, parents, out, nullptr, 0,
+                     batch, nodes, heads, head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale,
+                     split_tiles, max_splits, waves_per_block, prefix_kernel, stream,
+                     kv_format == 1 ? kVfFp8 : kVfInt8, 0, merge_area, merge_area_bytes < 0 ? 0 : merge_area_bytes);
 }

@@ -27,7 +27,7 @@ import torch
 from . import _lib
 from .paged import PagedKVCache
 from .quant import build_compression_stats, is_fp8, is_per_channel
-from .triton_utils import device_cu_count, launch_plan, plan_tree_splits
+from .triton_utils import device_cu_count, launch_plan, merge_area, plan_tree_splits
 
 __all__ = ["tree_verify_attention", "validate_parents", "path_mask", "tree_shape"]
 
@@ -134,9 +134,25 @@ def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
         tiled, waves, split_tiles, max_splits, block_n = launch_plan(max_seq_len, rows, head_dim,
                                                                      int(cache.block_size), int(kq.block_size), dev,
                                                                      per_channel=per_channel)
+    out = torch.empty_like(q_c)
+    stream = _lib.stream_ptr(dev)
+    plan = {"num_splits": float(max_splits), "split_tiles": float(split_tiles), "num_warps": float(waves),
+            "block_n": float(block_n), "tiled_path": float(tiled), "mfma_prefix": float(use_mfma),
+            "nodes_per_workgroup": float(per_wg if use_mfma else 1)}
+    if use_mfma and dk_c.dtype == q_c.dtype:
+        # the multi-query kernel finishes every row itself: split rows merge inside the launch
+        area, area_bytes = merge_area(dev, rows, max_splits, head_dim, stream) if max_splits > 1 else (None, 0)
+        _lib.check(lib.fs_tree_verify_merged(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), 1 if fp8 else 0, kq.values.data_ptr(), kq.scale.data_ptr(),
+            None if fp8 else kq.zero_point.data_ptr(), vq.values.data_ptr(), vq.scale.data_ptr(),
+            None if fp8 else vq.zero_point.data_ptr(), table.data_ptr(), table.element_size(), int(table.shape[1]),
+            lengths.data_ptr(), dk_c.data_ptr(), dv_c.data_ptr(), parents_dev.data_ptr(), out.data_ptr(),
+            _lib.ptr(area), area_bytes, batch, nodes, heads, head_dim, int(kq.values.shape[0]),
+            int(cache.block_size), int(kq.block_size), max_seq_len, 1.0 / math.sqrt(head_dim), split_tiles,
+            max_splits, waves, per_wg, stream))
+        return out, plan
     ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    out = torch.empty_like(q_c)
     store = ([kq.values.data_ptr(), kq.scale.data_ptr(), vq.values.data_ptr(), vq.scale.data_ptr()] if fp8 else
              [kq.values.data_ptr(), kq.scale.data_ptr(), kq.zero_point.data_ptr(), vq.values.data_ptr(),
               vq.scale.data_ptr(), vq.zero_point.data_ptr()])
@@ -147,10 +163,7 @@ def _hip(q, cache, draft_k, draft_v, parents_dev, dims, kernel):
         dv_c.data_ptr(), _lib.dtype_code(dk_c.dtype), parents_dev.data_ptr(), out.data_ptr(), workspace.data_ptr(),
         ws_bytes, batch, nodes, heads, head_dim, int(kq.values.shape[0]), int(cache.block_size), int(kq.block_size),
         max_seq_len, 1.0 / math.sqrt(head_dim), split_tiles, max_splits, waves,
-        (3 if per_wg == 16 else 4) if use_mfma else 1, _lib.stream_ptr(dev)))
-    plan = {"num_splits": float(max_splits), "split_tiles": float(split_tiles), "num_warps": float(waves),
-            "block_n": float(block_n), "tiled_path": float(tiled), "mfma_prefix": float(use_mfma),
-            "nodes_per_workgroup": float(per_wg if use_mfma else 1)}
+        (3 if per_wg == 16 else 4) if use_mfma else 1, stream))
     return out, plan
 
 

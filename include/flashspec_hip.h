@@ -229,6 +229,29 @@ int fs_tree_verify_i8_channel(const void* q, int q_dtype,
                               void* stream);
 
 /*
+ * Tree verification on the multi-query kernel with its split merge inside the launch: rows
+ * whose prefix splits (max_splits > 1) publish per-node states to `merge_area`
+ * (fs_paged_decode_merged's contract: zero-filled before the first call, left zero by every
+ * call, fs_decode_merge_area_bytes(batch * nodes * heads, max_splits, head_dim) bytes, one
+ * area per stream), and the last split of each (request, head, node group) merges them and
+ * finishes the rows (path tokens, output) -- no workspace and no tail launch.  kv_format 0 =
+ * affine INT8 per block or token, 1 = FP8 E4M3 (zero arrays unused); drafts in q's dtype;
+ * nodes_per_workgroup 0 (the library's choice), 16 or 32.  Other arguments as for
+ * fs_tree_verify_i8.  No counterpart in the reference (its Kernel 3 is planned only,
+ * doc/TODO.MD:186-237).
+ */
+int fs_tree_verify_merged(const void* q, int q_dtype, int kv_format,
+                          const void* k_values, const float* k_scale, const int16_t* k_zero,
+                          const void* v_values, const float* v_scale, const int16_t* v_zero,
+                          const void* block_table, int table_index_bytes, int64_t table_cols,
+                          const int64_t* lengths, const void* draft_k, const void* draft_v,
+                          const int64_t* parents, void* out, void* merge_area, int64_t merge_area_bytes,
+                          int batch, int nodes, int heads, int head_dim, int64_t num_pages,
+                          int page_size, int quant_block, int max_seq_len, float sm_scale,
+                          int split_tiles, int max_splits, int waves_per_block,
+                          int nodes_per_workgroup, void* stream);
+
+/*
  * 1 when fs_tree_verify_i8 can run its multi-query prefix kernel on this store: head_dim 64,
  * 128 or 256, page_size a multiple of 16, quant_block 1 or a multiple of 16 dividing the
  * page.  No counterpart in the reference (tree verification is not implemented there).
