@@ -147,6 +147,12 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
          c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p],
     ),
+    "fs_paged_decode_ordered": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int, c_int, c_int64, c_int,
+         c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+    ),
     "fs_paged_decode_append_i8": (
         c_int,
         [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

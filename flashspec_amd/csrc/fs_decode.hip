@@ -1676,6 +1676,33 @@ extern "C" int fs_paged_decode_append_i8(const void* q, int q_dtype, const void*
   return FS_OK;
 }
 
+extern "C" int fs_paged_decode_ordered(const void* q, int q_dtype, const int8_t* k_values, const float* k_scale,
+                                       const int16_t* k_zero, const int8_t* v_values, const float* v_scale,
+                                       const int16_t* v_zero, const void* block_table, int table_index_bytes,
+                                       int64_t table_cols, const int64_t* lengths, const int32_t* request_order,
+                                       void* out, void* workspace, int64_t workspace_bytes, void* merge_area,
+                                       int64_t merge_area_bytes, int batch, int heads, int head_dim,
+                                       int64_t num_pages, int page_size, int quant_block, int max_seq_len,
+                                       float sm_scale, int split_tiles, int max_splits, int waves_per_block,
+                                       void* stream) {
+  DecodeParams p;
+  bool tiled = false;
+  if (int rc = paged_params(p, tiled, q, k_values, k_scale, k_zero, v_values, v_scale, v_zero, block_table,
+                            table_index_bytes, table_cols, lengths, out, workspace, workspace_bytes, batch, 1, heads,
+                            head_dim, num_pages, page_size, quant_block, max_seq_len, sm_scale, split_tiles,
+                            max_splits, waves_per_block, true, kVfInt8, 0, merge_area,
+                            merge_area != nullptr ? (merge_area_bytes < 0 ? 0 : merge_area_bytes) : -1))
+    return rc;
+  if (!tiled) return set_error(FS_ERR_INVALID, "a request order needs the tiled decode path");
+  p.request_order = request_order;
+  hipStream_t st = (hipStream_t)stream;
+  if (int rc = launch_decode<true>(p, q_dtype, tiled, waves_per_block, st)) return rc;
+  if (p.max_splits > 1 && p.merge_count == nullptr)  // split partials: the merge launch
+    return fs_combine_splits(workspace, lengths, out, q_dtype, batch, heads, head_dim, max_seq_len, split_tiles,
+                             max_splits, stream);
+  return FS_OK;
+}
+
 extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype,
                                  int batch, int heads, int head_dim, int seq_len, int split_tiles,
                                  int max_splits, void* stream) {

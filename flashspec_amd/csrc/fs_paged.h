@@ -78,6 +78,10 @@ struct DecodeParams {
   const void* append_k;
   const void* append_v;
   int64_t* lengths_out;
+  // Dispatch order of the requests (tiled decode): workgroups take request request_order[i] in the
+  // place of request i (a permutation of [0, batch); NULL = natural order).  Serving batches pass
+  // their requests longest first, so the last round of workgroups holds short rows.
+  const int32_t* request_order;
 };
 
 // Words of the in-kernel split merge (decode rows and tree verification): a split's state goes out
@@ -149,7 +153,12 @@ __device__ __forceinline__ Unit decode_unit(const DecodeParams& p, int bid, int 
   t /= nq;
   const int hh = t % hg;
   t /= hg;
-  const int b = t % batch, x = t / batch;
+  int b = t % batch;
+  const int x = t / batch;
+  if (p.request_order != nullptr) {
+    const int o = p.request_order[b];
+    if ((unsigned)o < (unsigned)batch) b = o;  // an entry outside the batch keeps the natural request
+  }
   return {(b * nq + n) * p.heads + x * hg + hh, split};
 }
 

@@ -85,8 +85,12 @@ def _validate_triton_paged_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
 
 
 def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, return_stats: bool = False,
+                                      request_order: torch.Tensor | None = None,
                                       ) -> torch.Tensor | tuple[torch.Tensor, dict[str, float]]:
-    """Launch the HIP paged kernel (replaces triton_paged.py:338-450); no dense K/V is built."""
+    """Launch the HIP paged kernel (replaces triton_paged.py:338-450); no dense K/V is built.
+
+    ``request_order`` (device int32 permutation of the batch, affine INT8 stores on the tiled path):
+    dispatch the requests in that order (``fs_paged_decode_ordered``); the output is the same."""
 
     kq, vq = cache.k_quant, cache.v_quant
     dev = q.device
@@ -115,6 +119,20 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
         max_seq_len, rows, head_dim, int(cache.block_size), int(kq.block_size), dev, per_channel=per_channel,
         light=light)
     stream = _lib.stream_ptr(dev)
+    if request_order is not None and tiled and not per_channel and not is_fp8(kq):
+        area, area_bytes, workspace, ws_bytes = None, 0, None, 0
+        if max_splits > 1 and waves <= MERGE_MAX_WAVES:
+            area, area_bytes = merge_area(dev, rows, max_splits, head_dim, stream)
+        elif max_splits > 1:
+            ws_bytes = int(lib.fs_decode_workspace_bytes(rows, max_splits, head_dim))
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.fs_paged_decode_ordered(
+            q_c.data_ptr(), _lib.dtype_code(q_c.dtype), *(t.data_ptr() for t in kv), table.data_ptr(),
+            table.element_size(), int(table.shape[1]), lengths.data_ptr(), request_order.data_ptr(), out.data_ptr(),
+            _lib.ptr(workspace), ws_bytes, _lib.ptr(area), area_bytes, batch, heads, head_dim, num_pages,
+            int(cache.block_size), int(kq.block_size), max_seq_len, sm_scale, split_tiles, max_splits, waves, stream))
+        return _paged_result(out, return_stats, cache, q_c, max_seq_len, max_splits, block_n, waves, split_tiles,
+                             tiled)
     if tiled and max_splits > 1 and waves <= MERGE_MAX_WAVES:
         # split rows merge inside the decode launch (no workspace, no merge launch)
         area, area_bytes = merge_area(dev, rows, max_splits, head_dim, stream)

@@ -109,6 +109,10 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert fused(16, 96, 7, 9) == _lib.FS_ERR_INVALID and "64, 128 or 256" in lib.fs_last_error().decode()
     assert fused(16, 128, 7, 7) == _lib.FS_ERR_INVALID and "lengths_out" in lib.fs_last_error().decode()
     assert fused(16, 128, 7, None) == _lib.FS_ERR_INVALID
+    # a request order needs the tiled path (head_dim 36 takes the generic kernel)
+    rc = lib.fs_paged_decode_ordered(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 1, None, 0, None, 0, 2, 2, 36, 8, 16, 16,
+                                     64, 0.1, 4, 1, 1, None)
+    assert rc == _lib.FS_ERR_INVALID and "tiled" in lib.fs_last_error().decode()
 
 
 def test_no_alloc_entry_point_rejects_plans_beyond_its_array():

@@ -316,3 +316,43 @@ def test_fused_append_decode_bit_identical_to_append_then_decode(monkeypatch, H,
     ora = op.OracleCache(from_qt(cache.k_quant), from_qt(cache.v_quant), np_of(table)[keep],
                          np.array(lens_out.tolist(), dtype=np.int64)[keep], bs, max_seq)
     assert_attention_close(out[keep], oa.paged_quant_attention(np_of(q.float())[keep], ora), qdt, "fused vs oracle")
+
+
+@pytest.mark.parametrize("splits,warps", [(None, None), ("3", None), ("3", "16")])
+def test_request_order_gives_the_same_rows(monkeypatch, splits, warps):
+    """fs_paged_decode_ordered with the natural order (NULL), reversed, longest-first and random
+    permutations: outputs bit-identical to the plain paged decode, for one-split, merged-split and
+    workspace-split plans."""
+
+    if splits:
+        monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", splits)
+    if warps:
+        monkeypatch.setenv("FLASHSPEC_NUM_WARPS", warps)
+    B, H, S, D = 6, 8, 700, 128
+    announce(f"request order B{B} H{H} S{S} splits {splits} warps {warps}")
+    k, v = randn((B, H, S, D), 81), randn((B, H, S, D), 82)
+    lengths = torch.tensor([700, 5, 333, 0, 640, 17], dtype=torch.int64)
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=16, lengths=lengths.to(DEV),
+                                       block_table_pattern="shuffled", layout_seed=5)
+    q = randn((B, H, D), 83).to(DEV)
+    ref = fa.paged_quant_attention_triton(q, cache)
+    from flashspec_amd.triton_paged import _run_paged_quant_attention_triton
+
+    g = torch.Generator().manual_seed(1)
+    orders = [None, list(range(B))[::-1], sorted(range(B), key=lambda i: -int(lengths[i])),
+              torch.randperm(B, generator=g).tolist()]
+    for order in orders:
+        dev_order = None if order is None else torch.tensor(order, dtype=torch.int32, device=DEV)
+        out = _run_paged_quant_attention_triton(q, cache, request_order=dev_order)
+        assert torch.equal(out, ref), f"order {order}"
+
+
+def test_decode_batch_dispatches_longest_first():
+    announce("decode batch request order")
+    alloc, rids = build_request_pool([300, 17, 1000, 64], heads=4, head_dim=128, headroom_tokens=8, seed=2,
+                                     device=DEV)
+    batch = DecodeBatch(alloc, rids, max_new_tokens=2)
+    assert batch._order.cpu().tolist() == [2, 0, 3, 1]
+    q = randn((4, 4, 128), 90).to(DEV)
+    assert torch.equal(batch.attend(q), fa.paged_quant_attention_triton(q, alloc.to_cache(rids)))
+    batch.close()
