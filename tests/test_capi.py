@@ -113,6 +113,17 @@ def test_invalid_arguments_are_rejected_before_launch():
     rc = lib.fs_paged_decode_ordered(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 1, None, 0, None, 0, 2, 2, 36, 8, 16, 16,
                                      64, 0.1, 4, 1, 1, None)
     assert rc == _lib.FS_ERR_INVALID and "tiled" in lib.fs_last_error().decode()
+    # tree verification with the in-launch merge: INT8 or FP8 only, 16 / 32 / library-chosen node groups,
+    # the multi-query kernel's shapes
+    tree = lib.fs_tree_verify_merged
+
+    def merged(kv_format=0, npw=0, head_dim=128):
+        return tree(1, 1, kv_format, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 1, 1, 1, None, 0, 2, 4, 2, head_dim, 8, 16, 16,
+                    64, 0.1, 4, 1, 8, npw, None)
+
+    assert merged(kv_format=2) == _lib.FS_ERR_INVALID and "kv_format" in lib.fs_last_error().decode()
+    assert merged(npw=8) == _lib.FS_ERR_INVALID and "nodes_per_workgroup" in lib.fs_last_error().decode()
+    assert merged(head_dim=96) == _lib.FS_ERR_INVALID and "multi-query" in lib.fs_last_error().decode()
 
 
 def test_no_alloc_entry_point_rejects_plans_beyond_its_array():
