@@ -8,10 +8,10 @@
 //   O[d, n] += sum_t (u[t, d] - zv[t]) * P'[n, t]       v_mfma_f32_16x16x32_f16, A = V^T,    B = P'
 //
 // (u = stored int8 + 128; the P.V product takes two tiles, 32 tokens, at once).  K
-// bytes enter the product as fp16 1024 + u (one byte permute and
-// one XOR per pair), and the zero point is removed on the fp32 scores as (1024 + zk) * sum(q)
+// bytes enter the product as fp16 1024 + u (one XOR per four bytes, one byte permute per
+// pair), and the zero point is removed on the fp32 scores as (1024 + zk) * sum(q)
 // per node, as in the row kernel; V bytes become u - zv exactly in fp16 (integers in
-// [-255, 255]) with one more packed fp16 add per pair.  The key scale multiplies the fp32
+// [-255, 255]) with one permute, one XOR and one packed fp16 add per pair.  The key scale multiplies the fp32
 // scores; the value scale is folded into the weights as
 // P' = P * vs / vref, with vref the largest value scale among the wave's tiles, so that
 // P' <= 2^8 fits fp16 (the wave's output is multiplied by vref at the end).  P' enters the
@@ -44,22 +44,28 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kNodeGroup = 16;  // draft nodes per wave: the N dimension of the MFMA tiles
+constexpr size_t kLdsBytesPerCu = 160 * 1024;  // gfx950
 
 // Waves per workgroup: 8 (4 for head_dim 256, whose ~250 registers per lane leave one wave
 // per SIMD).  Measured: 12-wave workgroups (the register file holds 3 waves per SIMD at
 // head_dim 128) run 6-12% slower than 8-wave ones.
 __host__ __device__ constexpr int tree_waves_cap_dp(int DP) { return DP == 256 ? 4 : 8; }
 
-// Byte pair -> fp16 pair (1024 + u_a, 1024 + u_b): the permute puts the two raw bytes in the
-// low bytes of the halves (high bytes zero), XOR 0x6480 flips the int8 sign bit (u = raw ^
-// 0x80) and sets the fp16 exponent of 1024.
+// Byte pair -> fp16 pair (1024 + u_a, 1024 + u_b), V side: the permute puts the two raw bytes
+// (of two token rows) in the low bytes of the halves (high bytes zero), XOR 0x6480 flips the int8
+// sign bit (u = raw ^ 0x80) and sets the fp16 exponent of 1024.
 constexpr uint32_t kHalfBias = 0x64806480u;
 
+// K side (the four bytes of a dword are consecutive dims of one row): one XOR flips the four
+// sign bits, and each permute takes the exponent byte 0x64 from its other operand (selector 4).
+constexpr uint32_t kExpBytes = 0x64646464u;
+
 __device__ __forceinline__ f16x8_t k_step_f16(uint32_t w0, uint32_t w1) {
-  const uint32_t a = __builtin_amdgcn_perm(0u, w0, 0x0c010c00u) ^ kHalfBias;
-  const uint32_t b = __builtin_amdgcn_perm(0u, w0, 0x0c030c02u) ^ kHalfBias;
-  const uint32_t c = __builtin_amdgcn_perm(0u, w1, 0x0c010c00u) ^ kHalfBias;
-  const uint32_t d = __builtin_amdgcn_perm(0u, w1, 0x0c030c02u) ^ kHalfBias;
+  const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
+  const uint32_t a = __builtin_amdgcn_perm(kExpBytes, x0, 0x04010400u);
+  const uint32_t b = __builtin_amdgcn_perm(kExpBytes, x0, 0x04030402u);
+  const uint32_t c = __builtin_amdgcn_perm(kExpBytes, x1, 0x04010400u);
+  const uint32_t d = __builtin_amdgcn_perm(kExpBytes, x1, 0x04030402u);
   const u32x4_t v = {a, b, c, d};
   return __builtin_bit_cast(f16x8_t, v);
 }
@@ -217,13 +223,16 @@ __device__ __forceinline__ int tree_parent_lane(const int64_t* parents, int b, i
 
 // Adds to row (b, n, h)'s softmax state (running max M in log2 units, denominator L,
 // accumulator over dims lane + 64c) the draft tokens on node n's path to the root (parents[b, a];
-// a parent outside [0, a) ends the path, at most nq steps), with the same online softmax.  With
-// nq <= 64 the path is walked in registers over `pl` (tree_parent_lane) and its tokens are taken
-// four at a time, so their K/V rows load together; larger trees walk parents in memory.
+// a parent outside [0, a) ends the path, at most nq steps), with the same online softmax.  dk / dv
+// point at draft node 0's K / V row of (b, h), node a's row at a * stride (global memory, or a
+// copy in LDS).  With nq <= 64 the path is walked in registers over `pl` (tree_parent_lane) and its
+// tokens are taken four at a time, so their K/V rows load together; larger trees walk parents in
+// memory.
 template <typename QT, typename DT>
 __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (&acc)[4], int pl, const QT* qrow,
-                                                     const DT* dk, const DT* dv, const int64_t* parents, int b, int n,
-                                                     int h, int nq, int heads, int D, float qk_scale, int lane) {
+                                                     const DT* dk, const DT* dv, size_t stride,
+                                                     const int64_t* parents, int b, int n, int nq, int D,
+                                                     float qk_scale, int lane) {
   float qv[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -246,7 +255,7 @@ __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (
       float kx[4][4], vx[4][4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const size_t kr = (((size_t)b * nq + (idx[i] < 0 ? 0 : idx[i])) * heads + h) * D;
+        const size_t kr = (size_t)(idx[i] < 0 ? 0 : idx[i]) * stride;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int d = lane + c * kWave;
@@ -281,7 +290,7 @@ __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (
   } else {
     int a = n;
     for (int step = 0; step < nq && a >= 0; ++step) {
-      const size_t kr = (((size_t)b * nq + a) * heads + h) * D;
+      const size_t kr = (size_t)a * stride;
       float dot = 0.f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -305,18 +314,23 @@ __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (
   }
 }
 
-// tree_path_accumulate, then the output row acc / L.
-template <typename QT, typename DT>
-__device__ __forceinline__ void tree_path_finish(float M, float L, float (&acc)[4], int pl, const QT* qrow,
-                                                 const DT* dk, const DT* dv, const int64_t* parents, QT* orow,
-                                                 int b, int n, int h, int nq, int heads, int D, float qk_scale,
-                                                 int lane) {
-  tree_path_accumulate<QT, DT>(M, L, acc, pl, qrow, dk, dv, parents, b, n, h, nq, heads, D, qk_scale, lane);
+// The output row acc / L (dims lane + 64c).
+template <typename QT>
+__device__ __forceinline__ void tree_write_row(float L, const float (&acc)[4], QT* orow, int D, int lane) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int d = lane + c * kWave;
     if (d < D) orow[d] = from_f32<QT>(L > 0.f ? acc[c] / L : 0.f);
   }
+}
+
+// tree_path_accumulate, then the output row acc / L.
+template <typename QT, typename DT>
+__device__ __forceinline__ void tree_path_finish(float M, float L, float (&acc)[4], int pl, const QT* qrow,
+                                                 const DT* dk, const DT* dv, size_t stride, const int64_t* parents,
+                                                 QT* orow, int b, int n, int nq, int D, float qk_scale, int lane) {
+  tree_path_accumulate<QT, DT>(M, L, acc, pl, qrow, dk, dv, stride, parents, b, n, nq, D, qk_scale, lane);
+  tree_write_row<QT>(L, acc, orow, D, lane);
 }
 
 // Row = (b * nq + n) * heads + h of a tree verification: merges the prefix partial states the
@@ -353,8 +367,9 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
       if (d < D) acc[c] = fmaf(pacc[(size_t)sp * D + d], wgt, acc[c]);
     }
   }
-  tree_path_finish<QT, DT>(M, L, acc, pl, q + (size_t)row * D, dk, dv, parents, out + (size_t)row * D, b, n, h, nq,
-                           heads, D, qk_scale, lane);
+  const size_t r0 = ((size_t)b * nq * heads + h) * D;  // draft node 0 of (b, h)
+  tree_path_finish<QT, DT>(M, L, acc, pl, q + (size_t)row * D, dk + r0, dv + r0, (size_t)heads * D, parents,
+                           out + (size_t)row * D, b, n, nq, D, qk_scale, lane);
 }
 
 template <int DP, typename QT, int QM, int NG, int VF>
@@ -369,6 +384,16 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   __shared__ float s_fin[kNodeGroup * ROW];  // merged states of the group's nodes (fused tail)
   __shared__ float s_finml[kNodeGroup * 2];
   __shared__ int s_last;
+  // Trees of up to 64 nodes: the request's draft K / V rows of head h and the workgroup's query
+  // rows, copied to LDS after the prefix loop (rows: K of nodes 0..nq-1, V of nodes 0..nq-1, q of
+  // the workgroup's nodes), so that the path walks read LDS instead of making one global round
+  // trip per four path tokens of every node.  Instances where the copy would not fit (or, at
+  // head_dim 64, would stop two workgroups sharing a CU) walk global memory.
+  constexpr size_t kBaseLds = sizeof(s_acc) + sizeof(s_ml) + sizeof(s_fin) + sizeof(s_finml) + sizeof(s_last);
+  constexpr size_t kStageBytes = (size_t)(2 * kWave + NG * kNodeGroup) * DP * sizeof(QT);
+  constexpr bool STAGE =
+      DP >= 128 ? kBaseLds + kStageBytes <= kLdsBytesPerCu : 2 * (kBaseLds + kStageBytes) <= kLdsBytesPerCu;
+  __shared__ __attribute__((aligned(16))) unsigned char s_stage[STAGE ? kStageBytes : 16];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -423,13 +448,14 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
 
   // the NG node groups' queries (nodes past nq: zero queries, never written)
   MqQuery<QT, DP> q[NG];
-  float qmul[NG];
+  float qmul[NG], qsm[NG];  // qsm: sum(q) * qmul, the zero-point term's factor
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     const int node = node0 + gi * kNodeGroup + nl;
     const size_t qrow = (((size_t)b * nq + node) * p.heads + h) * D;
     q[gi].load((const QT*)p.q + (node < nq ? qrow : 0), node < nq, g);
     qmul[gi] = q[gi].mul * (TOK ? p.qk_scale : 1.f);
+    qsm[gi] = q[gi].sum * qmul[gi];
   }
 
   const int8_t* kbase = p.kv[0];
@@ -471,9 +497,13 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     for (int jb = 0; jb < J; ++jb) acc[gi][jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Scores of tile k for each node group (4 tokens 4g + r of node l % 16, masked to kNegBig),
+  // Scores of tile k for each node group (4 tokens 4g + r of node l % 16, masked to -inf),
   // the tile's value factors vs / vref and fp16 -(1024 + zv) for those tokens.  The K bytes are
   // converted once for all groups.
+  // A masked score is -inf: its weight exp2(-inf - m) is 0 against the running max m, which
+  // starts at the finite kNegBig and only grows, so the weights need no test of their own.
+  // With block parameters each score is one FMA, S * (ks * qmul) + (-(1024 + zk) * ks) *
+  // (sum(q) * qmul), whose addend is -inf for a masked token.
   auto scores = [&](const MqTile<DP, TOK>& t, int k, float (&sc)[NG][4], float (&vfac)[4], f16x4_t& nzv) {
     const bool backed = k < nk && off_of(k) >= 0;
     const int token0 = (first + W * k) * kTile + 4 * g;
@@ -519,13 +549,26 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
           sacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q[gi].lo[s], sacc[gi], 0, 0, 0);
       }
     }
+    bool ok[4];
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
+    for (int r = 0; r < 4; ++r) ok[r] = backed && token0 + r < len;
+    if constexpr (TOK) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool ok = backed && token0 + r < len;
-        const float raw_s = ZP ? fmaf(-kzo[r], q[gi].sum, sacc[gi][r]) : sacc[gi][r];
-        sc[gi][r] = ok ? raw_s * (ksc[r] * qmul[gi]) : kNegBig;
+      for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float raw_s = ZP ? fmaf(-kzo[r], q[gi].sum, sacc[gi][r]) : sacc[gi][r];
+          sc[gi][r] = ok[r] ? raw_s * (ksc[r] * qmul[gi]) : -__builtin_inff();
+        }
+      }
+    } else {
+      const float nkz = -kzo[0] * ksc[0];
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        const float kq = ksc[0] * qmul[gi];
+        const float bias = ZP ? nkz * qsm[gi] : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[gi][r] = fmaf(sacc[gi][r], kq, ok[r] ? bias : -__builtin_inff());
       }
     }
     // -(1024 + z) straight from the integer (exact in fp16 for zero points in [0, 255]); no
@@ -570,7 +613,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float sv = e < 4 ? sa[gi][e] : sb[gi][e - 4];
-        const float pr = sv > kNegBig ? fast_exp2(sv - m[gi]) : 0.f;
+        const float pr = fast_exp2(sv - m[gi]);
         l[gi] += pr;
         const float pv = pr * (e < 4 ? fa[e] : fb[e - 4]);
         const _Float16 ph = (_Float16)pv;
@@ -645,6 +688,46 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   }
 
   const int pl = p.fuse_tail ? tree_parent_lane(p.parents, b, nq, lane) : -1;
+  const bool staged = STAGE && p.fuse_tail && nq <= kWave &&
+                      (((uintptr_t)p.draft_k | (uintptr_t)p.draft_v | (uintptr_t)p.q) & 15) == 0;
+  const QT* s_dk = reinterpret_cast<const QT*>(s_stage);
+  const QT* s_dv = s_dk + (size_t)nq * D;
+  const QT* s_q = s_dv + (size_t)nq * D;
+  const size_t r0 = ((size_t)b * nq * p.heads + h) * D;  // draft node 0 of (b, h)
+  if (staged) {
+    constexpr int CPR = DP * (int)sizeof(QT) / 16;  // 16-byte chunks per row (D == DP on this path)
+    const int total = (2 * nq + min(NG * kNodeGroup, nq - node0)) * CPR;
+    auto src = [&](int e) {
+      const int r = e / CPR, c = e - r * CPR;
+      const QT* row = r < nq       ? (const QT*)p.draft_k + r0 + (size_t)r * p.heads * D
+                      : r < 2 * nq ? (const QT*)p.draft_v + r0 + (size_t)(r - nq) * p.heads * D
+                                   : (const QT*)p.q + (((size_t)b * nq + node0 + (r - 2 * nq)) * p.heads + h) * D;
+      return reinterpret_cast<const uint4*>(row) + c;
+    };
+    constexpr int kBatch = 8;  // loads in flight per thread before their stores
+    for (int e0 = threadIdx.x; e0 < total; e0 += kBatch * blockDim.x) {
+      uint4 v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) v[i] = *src(min(e0 + i * (int)blockDim.x, total - 1));  // in bounds
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + i * blockDim.x;
+        if (e < total) reinterpret_cast<uint4*>(s_stage)[e] = v[i];
+      }
+    }
+  }
+  // node `node`'s path tokens into (M, L, acc); the copy is visible after the node group's first barrier
+  auto walk = [&](float& M, float& L, float (&acc)[4], int node) __attribute__((always_inline)) {
+    if (staged) {
+      tree_path_accumulate<QT, QT>(M, L, acc, pl, s_q + (size_t)(node - node0) * D, s_dk, s_dv, (size_t)D,
+                                   p.parents, b, node, nq, D, p.qk_scale, lane);
+    } else {
+      const size_t row = ((size_t)b * nq + node) * p.heads + h;
+      tree_path_accumulate<QT, QT>(M, L, acc, pl, (const QT*)p.q + row * D, (const QT*)p.draft_k + r0,
+                                   (const QT*)p.draft_v + r0, (size_t)p.heads * D, p.parents, b, node, nq, D,
+                                   p.qk_scale, lane);
+    }
+  };
   // Rows of several splits with fuse_tail and a merge area merge inside the launch: each split
   // publishes its per-node states (fs_paged.h's tagged words, slots [row, split, D + 2] with row =
   // (b * nq + node) * heads + h) and counts itself in on the workgroup's (request, head, node
@@ -665,9 +748,9 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
         const int d = lane + c * kWave;
         fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
       }
-      tree_path_finish<QT, QT>(s_finml[2 * n], s_finml[2 * n + 1], fin, pl, (const QT*)p.q + row * D,
-                               (const QT*)p.draft_k, (const QT*)p.draft_v, p.parents, (QT*)p.out + row * D, b, node,
-                               h, nq, p.heads, D, p.qk_scale, lane);
+      float M = s_finml[2 * n], L = s_finml[2 * n + 1];
+      walk(M, L, fin, node);
+      tree_write_row<QT>(L, fin, (QT*)p.out + row * D, D, lane);
     }
   };
   // The node groups merge one at a time through the same LDS buffers.
@@ -736,11 +819,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
         const int d = lane + c * kWave;
         fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
       }
-      if (node % nsplit == split) {
-        const size_t row = ((size_t)b * nq + node) * p.heads + h;
-        tree_path_accumulate<QT, QT>(M, L, fin, pl, (const QT*)p.q + row * D, (const QT*)p.draft_k,
-                                     (const QT*)p.draft_v, p.parents, b, node, h, nq, p.heads, D, p.qk_scale, lane);
-      }
+      if (node % nsplit == split) walk(M, L, fin, node);
       unsigned long long* ws = slot(node, split);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
