@@ -121,6 +121,16 @@ __device__ __forceinline__ float wave_min_valu(float x) {
   return fminf(r32.a, r32.b);
 }
 
+// Sum over the whole wave, every lane getting the same bits: each step adds the same two
+// operands in both lanes of a partner pair (and addition commutes).
+__device__ __forceinline__ float wave_sum_valu(float x) {
+  x = group_sum<16>(x);
+  const LanePair r16 = swap16(x, x);
+  x = r16.a + r16.b;
+  const LanePair r32 = swap32(x, x);
+  return r32.a + r32.b;
+}
+
 __device__ __forceinline__ int readlane_i32(int x, int lane) { return __builtin_amdgcn_readlane(x, lane); }
 __device__ __forceinline__ float readlane_f32(float x, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));

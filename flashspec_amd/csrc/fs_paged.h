@@ -63,6 +63,7 @@ struct DecodeParams {
   // Multi-query tree kernel with one split: it finishes the rows itself (path tokens from
   // draft_k / draft_v, which then have q's dtype, and parents) instead of leaving partials.
   int fuse_tail;
+  int pace_waves;  // multi-query tree kernel: the waves sharing a SIMD pace each other
   const void* draft_k;
   const void* draft_v;
   const int64_t* parents;

@@ -228,16 +228,19 @@ __device__ __forceinline__ int tree_parent_lane(const int64_t* parents, int b, i
 // copy in LDS).  With nq <= 64 the path is walked in registers over `pl` (tree_parent_lane) and its
 // tokens are taken four at a time, so their K/V rows load together; larger trees walk parents in
 // memory.
-template <typename QT, typename DT>
+constexpr int kPathBatch = 4;  // path tokens per step of the walk
+
+template <typename QT, typename DT, int CMAX = 4>
 __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (&acc)[4], int pl, const QT* qrow,
                                                      const DT* dk, const DT* dv, size_t stride,
                                                      const int64_t* parents, int b, int n, int nq, int D,
                                                      float qk_scale, int lane) {
-  float qv[4];
+  float qv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 0; c < CMAX; ++c) {
     const int d = lane + c * kWave;
-    qv[c] = d < D ? to_f32(qrow[d]) : 0.f;
+    const float x = to_f32(qrow[d < D ? d : 0]);
+    qv[c] = d < D ? x : 0.f;
   }
   if (nq <= kWave) {
     uint64_t path = 0;
@@ -246,44 +249,48 @@ __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (
       a = __builtin_amdgcn_readlane(pl, a);
     }
     while (path) {
-      int idx[4];
+      int idx[kPathBatch];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPathBatch; ++i) {
         idx[i] = path ? __builtin_ctzll(path) : -1;
         path &= path - 1;  // no-op once empty
       }
-      float kx[4][4], vx[4][4];
+      // every load unconditional (masked entries read node 0 / dim 0, in bounds) so that the
+      // batch's loads issue together
+      float kx[kPathBatch][CMAX], vx[kPathBatch][CMAX];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPathBatch; ++i) {
         const size_t kr = (size_t)(idx[i] < 0 ? 0 : idx[i]) * stride;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < CMAX; ++c) {
           const int d = lane + c * kWave;
+          const size_t o = kr + (d < D ? d : 0);
+          const float kv = to_f32(dk[o]), vv = to_f32(dv[o]);
           const bool ok = idx[i] >= 0 && d < D;
-          kx[i][c] = ok ? to_f32(dk[kr + d]) : 0.f;
-          vx[i][c] = ok ? to_f32(dv[kr + d]) : 0.f;
+          kx[i][c] = ok ? kv : 0.f;
+          vx[i][c] = ok ? vv : 0.f;
         }
       }
-      float sc[4];
+      float sc[kPathBatch];
       float mn = M;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPathBatch; ++i) {
         float dot = 0.f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dot = fmaf(qv[c], kx[i][c], dot);
-        sc[i] = wave_sum(dot) * qk_scale;
+        for (int c = 0; c < CMAX; ++c) dot = fmaf(qv[c], kx[i][c], dot);
+        sc[i] = wave_sum_valu(dot) * qk_scale;
         if (idx[i] >= 0) mn = fmaxf(mn, sc[i]);
       }
       const float alpha = fast_exp2(M - mn);
       L *= alpha;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] *= alpha;
+      for (int c = 0; c < CMAX; ++c) acc[c] *= alpha;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kPathBatch; ++i) {
         const float pr = idx[i] >= 0 ? fast_exp2(sc[i] - mn) : 0.f;
         L += pr;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] = fmaf(pr, vx[i][c], acc[c]);
+        for (int c = 0; c < CMAX; ++c) acc[c] = fmaf(pr, vx[i][c], acc[c]);
       }
       M = mn;
     }
@@ -297,7 +304,7 @@ __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (
         const int d = lane + c * kWave;
         if (d < D) dot = fmaf(qv[c], to_f32(dk[kr + d]), dot);
       }
-      const float sc = wave_sum(dot) * qk_scale;
+      const float sc = wave_sum_valu(dot) * qk_scale;
       const float mn = fmaxf(M, sc);
       const float alpha = fast_exp2(M - mn), pr = fast_exp2(sc - mn);
       L = L * alpha + pr;
@@ -385,7 +392,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   __shared__ float s_finml[kNodeGroup * 2];
   __shared__ int s_last;
   // Trees of up to 64 nodes: the request's draft K / V rows of head h and the workgroup's query
-  // rows, copied to LDS after the prefix loop (rows: K of nodes 0..nq-1, V of nodes 0..nq-1, q of
+  // rows, copied to LDS before the prefix loop (rows: K of nodes 0..nq-1, V of nodes 0..nq-1, q of
   // the workgroup's nodes), so that the path walks read LDS instead of making one global round
   // trip per four path tokens of every node.  Instances where the copy would not fit (or, at
   // head_dim 64, would stop two workgroups sharing a CU) walk global memory.
@@ -673,20 +680,30 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     }
   };
 
+  // Waves w and w ^ 4 of an 8-wave workgroup share a SIMD, where the older one wins every tie
+  // for issue: measured, waves 0-3 finished their tiles 25-40% before waves 4-7, which then ran
+  // alone.  With p.pace_waves (grids of more workgroups than CUs, where a CU takes its next
+  // workgroup only once the slowest wave is done) each wave posts its progress in LDS and lowers
+  // its priority while it is ahead of its partner: a scheduling hint only, the work and its order
+  // stay fixed.  Measured at B8 x 64 nodes (two workgroups per CU in turn) 137 -> 133.6 us; with
+  // one workgroup per CU it cost 0.6-0.8 us.
+  __shared__ int s_prog[8];
+  const bool balance = W == 8 && p.pace_waves;
+  auto pace = [&](int k) {
+    if (!balance) return;
+    if (lane == 0) __hip_atomic_store(&s_prog[w], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int pk =
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(&s_prog[w ^ 4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (k > pk)
+      __builtin_amdgcn_s_setprio(0);
+    else
+      __builtin_amdgcn_s_setprio(2);
+  };
+
   // two pairs of register buffers: tiles k+2, k+3 are in flight while k, k+1 are consumed
   MqTile<DP, TOK> ta, tb, tc, td;
   load(ta, 0);
   load(tb, 1);
-  for (int k = 0; k < nk; k += 4) {
-    load(tc, k + 2);
-    load(td, k + 3);
-    consume_pair(ta, tb, k);
-    if (k + 2 >= nk) break;
-    load(ta, k + 4);
-    load(tb, k + 5);
-    consume_pair(tc, td, k + 2);
-  }
-
   const int pl = p.fuse_tail ? tree_parent_lane(p.parents, b, nq, lane) : -1;
   const bool staged = STAGE && p.fuse_tail && nq <= kWave &&
                       (((uintptr_t)p.draft_k | (uintptr_t)p.draft_v | (uintptr_t)p.q) & 15) == 0;
@@ -716,14 +733,31 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
       }
     }
   }
+  if (balance && lane == 0) __hip_atomic_store(&s_prog[w], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (int k = 0; k < nk; k += 4) {
+    load(tc, k + 2);
+    load(td, k + 3);
+    pace(k);
+    consume_pair(ta, tb, k);
+    if (k + 2 >= nk) break;
+    load(ta, k + 4);
+    load(tb, k + 5);
+    pace(k + 2);
+    consume_pair(tc, td, k + 2);
+  }
+  if (balance) {
+    if (lane == 0) __hip_atomic_store(&s_prog[w], 1 << 30, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_s_setprio(0);
+  }
+
   // node `node`'s path tokens into (M, L, acc); the copy is visible after the node group's first barrier
   auto walk = [&](float& M, float& L, float (&acc)[4], int node) __attribute__((always_inline)) {
     if (staged) {
-      tree_path_accumulate<QT, QT>(M, L, acc, pl, s_q + (size_t)(node - node0) * D, s_dk, s_dv, (size_t)D,
+      tree_path_accumulate<QT, QT, DP / 64>(M, L, acc, pl, s_q + (size_t)(node - node0) * D, s_dk, s_dv, (size_t)D,
                                    p.parents, b, node, nq, D, p.qk_scale, lane);
     } else {
       const size_t row = ((size_t)b * nq + node) * p.heads + h;
-      tree_path_accumulate<QT, QT>(M, L, acc, pl, (const QT*)p.q + row * D, (const QT*)p.draft_k + r0,
+      tree_path_accumulate<QT, QT, DP / 64>(M, L, acc, pl, (const QT*)p.q + row * D, (const QT*)p.draft_k + r0,
                                    (const QT*)p.draft_v + r0, (size_t)p.heads * D, p.parents, b, node, nq, D,
                                    p.qk_scale, lane);
     }
@@ -1006,6 +1040,18 @@ static void launch_mq_q(const DecodeParams& p, bool tok, int per_wave, dim3 grid
   }
 }
 
+// CUs of the current device (0 if it cannot be read), read once per device.
+static int device_cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int cu = 0;
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cached[dev] = cu;
+  }
+  return cached[dev];
+}
+
 // Preconditions checked by the caller: paged store, valid pointers, workspace for rows x
 // max_splits partials, tree_mfma_path() true.  per_wave: draft nodes per workgroup, 16 or 32
 // (0: the library's choice for the current device).
@@ -1018,9 +1064,8 @@ int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves, int p
   const bool q_fp32 = q_dtype == FS_F32;
   const int batch_heads = p.rows / p.nq;
   if (per_wave == 0) {
-    int dev = 0, cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      return set_error(FS_ERR_RUNTIME, "tree verify: cannot read the device's CU count");
+    const int cu = device_cu_count();
+    if (cu <= 0) return set_error(FS_ERR_RUNTIME, "tree verify: cannot read the device's CU count");
     per_wave = tree_nodes_per_wave(p.head_dim, p.nq, q_fp32, tok, batch_heads, cu);
   } else if (per_wave != kNodeGroup &&
              (per_wave != 2 * kNodeGroup || tree_max_nodes_per_wave(p.head_dim, q_fp32, tok) != per_wave)) {
@@ -1031,11 +1076,13 @@ int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves, int p
   const int batch = p.rows / (p.heads * p.nq);
   const int64_t units = (int64_t)batch * p.heads * groups * p.max_splits;
   if (units > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "tree verify grid too large");
+  DecodeParams pp = p;
+  pp.pace_waves = units > device_cu_count();
   const dim3 grid((unsigned)units), block(kWave * waves);
   switch (q_dtype) {
-    case FS_F32: launch_mq_q<float>(p, tok, per_wave, grid, block, st); break;
-    case FS_F16: launch_mq_q<__half>(p, tok, per_wave, grid, block, st); break;
-    case FS_BF16: launch_mq_q<__hip_bfloat16>(p, tok, per_wave, grid, block, st); break;
+    case FS_F32: launch_mq_q<float>(pp, tok, per_wave, grid, block, st); break;
+    case FS_F16: launch_mq_q<__half>(pp, tok, per_wave, grid, block, st); break;
+    case FS_BF16: launch_mq_q<__hip_bfloat16>(pp, tok, per_wave, grid, block, st); break;
     default: return set_error(FS_ERR_INVALID, "q dtype code must be 0 (f32), 1 (f16) or 2 (bf16)");
   }
   return check_launch("tree_prefix_mfma");
