@@ -200,6 +200,8 @@ MFMA_CASES = [
     (2, 4, 600, 128, 16, 16, "fp8_block", torch.float16, [600, 250]),         # FP8 codes as fp16 operands
     (1, 4, 300, 64, 20, 32, "fp8_block", torch.bfloat16, [300]),
     (2, 2, 400, 256, 6, 16, "fp8_block", torch.float32, [400, 7]),
+    # 512 workgroups of 32 nodes: more than one per CU, so the waves pace each other; drafts staged in LDS
+    (8, 32, 256, 128, 64, 16, "affine_block", torch.float16, [256, 256, 100, 256, 17, 256, 256, 240]),
 ]
 
 
@@ -346,3 +348,31 @@ def test_tree_parents_cache_reuse_and_change():
         bad = par.clone()
         bad[1, 2] = 5
         fa.tree_verify_attention(q, cache, dk, dv, bad)
+
+
+def test_tree_mfma_unaligned_drafts_walk_global_memory():
+    """Draft tensors whose data does not start on a 16-byte boundary are not copied to LDS: the
+    path walks then read global memory, with the same arithmetic in the same order, so the output
+    is bit-identical to the aligned call's."""
+
+    announce("tree mfma unaligned drafts")
+    B, H, S, D, N = 2, 8, 600, 128, 20
+    parents = torch.tensor(_random_parents(B, N, 77)).to(DEV)
+    q = randn((B, N, H, D), 91, torch.float32).to(torch.float16).to(DEV)
+    k, v = randn((B, H, S, D), 92).to(DEV), randn((B, H, S, D), 93).to(DEV)
+    dk = randn((B, N, H, D), 94, torch.float32).to(torch.float16).to(DEV)
+    dv = randn((B, N, H, D), 95, torch.float32).to(torch.float16).to(DEV)
+    cache = fa.PagedKVCache.from_dense(k, v, 16, lengths=torch.tensor([600, 311]).to(DEV))
+    n = dk.numel()
+    raw_k = torch.empty(n + 8, dtype=torch.float16, device=DEV)
+    raw_v = torch.empty(n + 8, dtype=torch.float16, device=DEV)
+    dk_off = raw_k[1:n + 1].view(B, N, H, D)  # 2 bytes past the allocation's start
+    dv_off = raw_v[1:n + 1].view(B, N, H, D)
+    dk_off.copy_(dk)
+    dv_off.copy_(dv)
+    assert dk_off.data_ptr() % 16 != 0 and dk_off.is_contiguous()
+    a, st = fa.tree_verify_attention(q, cache, dk, dv, parents, return_stats=True, kernel="mfma")
+    b = fa.tree_verify_attention(q, cache, dk_off, dv_off, parents, kernel="mfma")
+    torch.cuda.synchronize(DEV)
+    assert st["mfma_prefix"] == 1.0
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
