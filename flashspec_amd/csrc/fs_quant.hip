@@ -511,8 +511,8 @@ append_tokens_vec_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageSto
       mx = fmaxf(mx, x[c][i]);
     }
   }
-  mn = wave_min(mn);
-  mx = wave_max(mx);
+  mn = wave_min_valu(mn);  // DPP and lane swaps: no LDS round trips on the append's latency chain
+  mx = wave_max_valu(mx);
   const float scale = fmaxf((mx - mn) / 255.0f, 1.0e-8f);
   const float zero = fminf(fmaxf(__builtin_rintf(-mn / scale), 0.0f), 255.0f);
   const float rcp = 1.0f / scale;

@@ -361,7 +361,7 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
   const float* pacc = part_acc + (size_t)row * max_splits * D;
   float M = kNegBig;
   for (int sp = lane; sp < nsplit; sp += kWave) M = fmaxf(M, ml[2 * sp]);
-  M = wave_max(M);
+  M = wave_max_valu(M);
   float L = 0.f;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
@@ -449,7 +449,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
       }
     }
   }
-  vmax = wave_max(vmax);
+  vmax = wave_max_valu(vmax);
   const float vref = vmax > 0.f ? vmax : 1.f;
   const float inv_vref = 1.f / vref;
 
