@@ -102,21 +102,32 @@ __device__ __forceinline__ f16x4_t v_block_fp8(uint32_t t0, uint32_t t1, uint32_
   return f16x4_t{lo[0], lo[1], hi[0], hi[1]};
 }
 
-// J bytes of one token row (J = D / 16: 4, 8 or 16).  Plain (cached) loads, unlike the row
-// kernel's non-temporal ones: the node groups of one (request, head) read the same tiles, and
-// measured at 16 and 64 nodes cached loads are 1-4% faster.
+// NT: non-temporal loads, as in the row kernel, where one workgroup reads each (request, head)'s
+// tiles; plain (cached) loads where several node groups of one (request, head) read the same tiles
+// and the later ones hit L2.  Measured (A/B, one box): non-temporal B4 x 1 node 33.1 -> 30.5 us,
+// B8 x 16 62.6 -> 59.2, but B8 x 64 (two node groups) 132.3 -> 140.2.
+template <bool NT, typename V>
+__device__ __forceinline__ V tile_load(const int8_t* p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load((const V*)p);
+  else
+    return *(const V*)p;
+}
+
+// J bytes of one token row (J = D / 16: 4, 8 or 16).
 template <int J>
 struct VBytes {
   uint32_t w[J / 4];
+  template <bool NT>
   __device__ __forceinline__ void load(const int8_t* p) {
     if constexpr (J == 16) {
-      const uint4 v = *(const uint4*)p;
-      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+      const u32x4_t v = tile_load<NT, u32x4_t>(p);
+      w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
     } else if constexpr (J == 8) {
-      const u32x2_t v = *(const u32x2_t*)p;
+      const u32x2_t v = tile_load<NT, u32x2_t>(p);
       w[0] = v.x; w[1] = v.y;
     } else {
-      w[0] = *(const uint32_t*)p;
+      w[0] = tile_load<NT, uint32_t>(p);
     }
   }
 };
@@ -379,7 +390,7 @@ tree_tail_kernel(const float* part_ml, const float* part_acc, const int64_t* len
                            out + (size_t)row * D, b, n, nq, D, qk_scale, lane);
 }
 
-template <int DP, typename QT, int QM, int NG, int VF>
+template <int DP, typename QT, int QM, int NG, int VF, bool NT>
 __global__ void __launch_bounds__(kWave * tree_waves_cap_dp(DP))
 tree_prefix_mfma_kernel(const DecodeParams p) {
   constexpr bool TOK = QM == kQmToken;
@@ -479,9 +490,12 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     const size_t to = o < 0 ? 0 : (size_t)o;
     const int8_t* kp = kbase + to + (size_t)nl * D;
 #pragma unroll
-    for (int c = 0; c < C; ++c) t.k[c] = *(const uint4*)(kp + 16 * (4 * c + g));
+    for (int c = 0; c < C; ++c) {
+      const u32x4_t kv = tile_load<NT, u32x4_t>(kp + 16 * (4 * c + g));
+      t.k[c] = make_uint4(kv[0], kv[1], kv[2], kv[3]);
+    }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) t.v[e].load(vbase + to + (size_t)(4 * g + e) * D + J * nl);
+    for (int e = 0; e < 4; ++e) t.v[e].template load<NT>(vbase + to + (size_t)(4 * g + e) * D + J * nl);
     if constexpr (TOK) {
       const size_t tok0 = to / D;
 #pragma unroll
@@ -1003,11 +1017,19 @@ int tree_nodes_per_wave(int head_dim, int nodes, bool q_fp32, bool tok, int64_t 
 
 template <int DP, typename QT, int NG, int VF>
 static void launch_mq_vf(const DecodeParams& p, bool tok, dim3 grid, dim3 block, hipStream_t st) {
+  // one node group per (request, head): nothing else reads its tiles, so they load non-temporally
+  const bool nt = p.nq <= NG * kNodeGroup;
   if (tok) {
-    if constexpr (NG == 1 || DP <= 64)
-      hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken, NG, VF>), grid, block, 0, st, p);
+    if constexpr (NG == 1 || DP <= 64) {
+      if (nt)
+        hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken, NG, VF, true>), grid, block, 0, st, p);
+      else
+        hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmToken, NG, VF, false>), grid, block, 0, st, p);
+    }
+  } else if (nt) {
+    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock, NG, VF, true>), grid, block, 0, st, p);
   } else {
-    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock, NG, VF>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((tree_prefix_mfma_kernel<DP, QT, kQmBlock, NG, VF, false>), grid, block, 0, st, p);
   }
 }
 
