@@ -809,8 +809,12 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     if (gi > 0) __syncthreads();  // the previous group's merge and tail are done with the LDS
     // node totals over the four lane groups; accumulator to value units
     float lt = l[gi];
-    lt += __shfl_xor(lt, 16, kWave);
-    lt += __shfl_xor(lt, 32, kWave);
+    {
+      const LanePair r16 = swap16(lt, lt);  // rows of 16 lanes r0 + r1 and r2 + r3 (lane groups g)
+      lt = r16.a + r16.b;
+      const LanePair r32 = swap32(lt, lt);
+      lt = r32.a + r32.b;
+    }
     float* my_acc = s_acc + (size_t)(w * kNodeGroup + nl) * ROW;
 #pragma unroll
     for (int jb = 0; jb < J; ++jb) {
@@ -822,30 +826,39 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
       s_ml[2 * (w * kNodeGroup + nl) + 1] = lt;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < nodes_here * D; e += blockDim.x) {
-      const int n = e / D, d = e - n * D;
+    // per node, once: M over the waves, the weights exp2(m_w - M) (in place of m_w) and L, in wave
+    // order; then every (node, dim) sums the waves' accumulators with those weights
+    if ((int)threadIdx.x < nodes_here) {
+      const int n = threadIdx.x;
       float M = kNegBig;
       for (int ww = 0; ww < W; ++ww) M = fmaxf(M, s_ml[2 * (ww * kNodeGroup + n)]);
-      float L = 0.f, a = 0.f;
+      float L = 0.f;
       for (int ww = 0; ww < W; ++ww) {
         const float f = fast_exp2(s_ml[2 * (ww * kNodeGroup + n)] - M);
         L = fmaf(s_ml[2 * (ww * kNodeGroup + n) + 1], f, L);
-        a = fmaf(s_acc[(size_t)(ww * kNodeGroup + n) * ROW + d], f, a);
+        s_ml[2 * (ww * kNodeGroup + n)] = f;
       }
       if (p.fuse_tail) {
+        s_finml[2 * n] = M;
+        s_finml[2 * n + 1] = L;
+      } else {
+        const size_t ws = ((size_t)(b * nq + gnode0 + n) * p.heads + h) * p.max_splits + split;
+        p.part_ml[2 * ws] = M;
+        p.part_ml[2 * ws + 1] = L;
+      }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nodes_here * D; e += blockDim.x) {
+      const int n = e / D, d = e - n * D;
+      float a = 0.f;
+      for (int ww = 0; ww < W; ++ww)
+        a = fmaf(s_acc[(size_t)(ww * kNodeGroup + n) * ROW + d], s_ml[2 * (ww * kNodeGroup + n)], a);
+      if (p.fuse_tail) {
         s_fin[n * ROW + d] = a;
-        if (d == 0) {
-          s_finml[2 * n] = M;
-          s_finml[2 * n + 1] = L;
-        }
       } else {
         const int row = (b * nq + gnode0 + n) * p.heads + h;
         const size_t ws = (size_t)row * p.max_splits + split;
         p.part_acc[ws * D + d] = a;
-        if (d == 0) {
-          p.part_ml[2 * ws] = M;
-          p.part_ml[2 * ws + 1] = L;
-        }
       }
     }
     if (!p.fuse_tail) continue;
