@@ -156,13 +156,33 @@ struct MqQuery {
 
   // Lane (node n = l % 16, group g = l / 16) holds dims 16*(4c + g) + i, c < DP/64, i < 16,
   // as elements 16c + i; step s of the product uses elements [8s, 8s + 8).
-  __device__ __forceinline__ void load(const QT* qrow, bool present, int g) {
-    float x[DP / 4];
+  // fetch() issues the loads of those values (16-byte loads when the row is 16-byte aligned,
+  // which DP * sizeof(QT) keeps for every row once q is): the kernel calls it first, so the
+  // query round trip overlaps the tile metadata's, and prepare() converts them.
+  static constexpr int kPer = (int)sizeof(QT);  // 16-byte words per 16 values
+  static constexpr int kRaw = DP / 64 * kPer;
+  __device__ __forceinline__ static void fetch(uint4 (&raw)[kRaw], const QT* qrow, int g, bool vec) {
 #pragma unroll
     for (int c = 0; c < DP / 64; ++c) {
+      const QT* src = qrow + 16 * (4 * c + g);
+      if (vec) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[16 * c + i] = present ? to_f32(qrow[16 * (4 * c + g) + i]) : 0.f;
+        for (int j = 0; j < kPer; ++j) raw[c * kPer + j] = reinterpret_cast<const uint4*>(src)[j];
+      } else {
+        QT t[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t[i] = src[i];
+        __builtin_memcpy(&raw[c * kPer], t, sizeof(t));
+      }
     }
+  }
+
+  __device__ __forceinline__ void prepare(const uint4 (&raw)[kRaw], bool present) {
+    QT vals[DP / 4];
+    __builtin_memcpy(vals, raw, sizeof(vals));
+    float x[DP / 4];
+#pragma unroll
+    for (int e = 0; e < DP / 4; ++e) x[e] = present ? to_f32(vals[e]) : 0.f;
     float scale = 1.f;
     mul = 1.f;
     if constexpr (!std::is_same<QT, __half>::value) {
@@ -430,13 +450,24 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   const int first = split * p.split_tiles + w;
   const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
   const int nk = first < tile_end ? (tile_end - first + W - 1) / W : 0;  // <= kMaxTilesPerWave
+  const int D = DP;
+
+  // the NG node groups' query values (nodes past nq read node 0's row and are zeroed)
+  using Query = MqQuery<QT, DP>;
+  uint4 qraw[NG][Query::kRaw];
+  const bool qvec = ((uintptr_t)p.q & 15) == 0;
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const int node = node0 + gi * kNodeGroup + nl;
+    const size_t qrow = (((size_t)b * nq + min(node, nq - 1)) * p.heads + h) * D;
+    Query::fetch(qraw[gi], (const QT*)p.q + qrow, g, qvec);
+  }
 
   // lane k resolves the wave's k-th tile: byte offset of its 16 K/V rows (-1: unbacked) and,
   // in block mode, its quantization parameters; vmax = largest value scale it holds
   int64_t my_off = -1;
   float my_ks = 0.f, my_vs = 0.f, vmax = 0.f;
   int my_kz = 0, my_vz = 0;
-  const int D = DP;
   if (lane < nk) {
     const int tile = first + W * lane;
     if constexpr (TOK) {
@@ -464,17 +495,9 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   const float vref = vmax > 0.f ? vmax : 1.f;
   const float inv_vref = 1.f / vref;
 
-  // the NG node groups' queries (nodes past nq: zero queries, never written)
-  MqQuery<QT, DP> q[NG];
+  // the queries as MFMA operands, prepared once the first tiles are in flight
+  Query q[NG];
   float qmul[NG], qsm[NG];  // qsm: sum(q) * qmul, the zero-point term's factor
-#pragma unroll
-  for (int gi = 0; gi < NG; ++gi) {
-    const int node = node0 + gi * kNodeGroup + nl;
-    const size_t qrow = (((size_t)b * nq + node) * p.heads + h) * D;
-    q[gi].load((const QT*)p.q + (node < nq ? qrow : 0), node < nq, g);
-    qmul[gi] = q[gi].mul * (TOK ? p.qk_scale : 1.f);
-    qsm[gi] = q[gi].sum * qmul[gi];
-  }
 
   const int8_t* kbase = p.kv[0];
   const int8_t* vbase = p.kv[1];
@@ -725,29 +748,33 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   const QT* s_dv = s_dk + (size_t)nq * D;
   const QT* s_q = s_dv + (size_t)nq * D;
   const size_t r0 = ((size_t)b * nq * p.heads + h) * D;  // draft node 0 of (b, h)
+  if (balance && lane == 0) __hip_atomic_store(&s_prog[w], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   if (staged) {
+    // 16-byte chunk e of the copy goes to s_stage + 16 e; wave w moves chunks [64 j, 64 j + 64) for
+    // j = w, w + W, ... with direct global-to-LDS loads (lane l's 16 bytes land at the wave's LDS
+    // address + 16 l), so the copy needs no registers and no wait before the prefix loop: it
+    // completes behind the first tiles and is waited for once the loop is done.
     constexpr int CPR = DP * (int)sizeof(QT) / 16;  // 16-byte chunks per row (D == DP on this path)
-    const int total = (2 * nq + min(NG * kNodeGroup, nq - node0)) * CPR;
-    auto src = [&](int e) {
-      const int r = e / CPR, c = e - r * CPR;
-      const QT* row = r < nq       ? (const QT*)p.draft_k + r0 + (size_t)r * p.heads * D
-                      : r < 2 * nq ? (const QT*)p.draft_v + r0 + (size_t)(r - nq) * p.heads * D
-                                   : (const QT*)p.q + (((size_t)b * nq + node0 + (r - 2 * nq)) * p.heads + h) * D;
-      return reinterpret_cast<const uint4*>(row) + c;
-    };
-    constexpr int kBatch = 8;  // loads in flight per thread before their stores
-    for (int e0 = threadIdx.x; e0 < total; e0 += kBatch * blockDim.x) {
-      uint4 v[kBatch];
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) v[i] = *src(min(e0 + i * (int)blockDim.x, total - 1));  // in bounds
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        const int e = e0 + i * blockDim.x;
-        if (e < total) reinterpret_cast<uint4*>(s_stage)[e] = v[i];
+    const int total = (2 * nq + min(NG * kNodeGroup, nq - node0)) * CPR;  // <= kStageBytes / 16
+    for (int e0 = w * kWave; e0 < total; e0 += W * kWave) {
+      const int e = e0 + lane;
+      if (e < total) {
+        const int r = e / CPR, c = e - r * CPR;
+        const QT* row = r < nq       ? (const QT*)p.draft_k + r0 + (size_t)r * p.heads * D
+                        : r < 2 * nq ? (const QT*)p.draft_v + r0 + (size_t)(r - nq) * p.heads * D
+                                     : (const QT*)p.q + (((size_t)b * nq + node0 + (r - 2 * nq)) * p.heads + h) * D;
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(reinterpret_cast<const uint4*>(row) + c),
+            (__attribute__((address_space(3))) void*)(s_stage + (size_t)e0 * 16), 16, 0, 0);
       }
     }
   }
-  if (balance && lane == 0) __hip_atomic_store(&s_prog[w], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    q[gi].prepare(qraw[gi], node0 + gi * kNodeGroup + nl < nq);
+    qmul[gi] = q[gi].mul * (TOK ? p.qk_scale : 1.f);
+    qsm[gi] = q[gi].sum * qmul[gi];
+  }
   for (int k = 0; k < nk; k += 4) {
     load(tc, k + 2);
     load(td, k + 3);
@@ -763,6 +790,8 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     if (lane == 0) __hip_atomic_store(&s_prog[w], 1 << 30, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     __builtin_amdgcn_s_setprio(0);
   }
+  // this wave's share of the LDS copy has landed before the barriers that precede the walks
+  if (staged) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // node `node`'s path tokens into (M, L, acc); the copy is visible after the node group's first barrier
   auto walk = [&](float& M, float& L, float (&acc)[4], int node) __attribute__((always_inline)) {
