@@ -417,6 +417,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   constexpr bool ZP = VF == kVfInt8;  // zero points (INT8); FP8 codes are the values
   constexpr int C = DP / 64, J = DP / 16, KS = DP / 32;
   constexpr int ROW = DP + 4;  // padded LDS row (floats)
+  constexpr bool kDraftMfma = std::is_same<QT, __half>::value;  // draft_pair below
   __shared__ float s_acc[tree_waves_cap_dp(DP) * kNodeGroup * ROW];
   __shared__ float s_ml[tree_waves_cap_dp(DP) * kNodeGroup * 2];
   __shared__ float s_fin[kNodeGroup * ROW];  // merged states of the group's nodes (fused tail)
@@ -462,6 +463,10 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     const size_t qrow = (((size_t)b * nq + min(node, nq - 1)) * p.heads + h) * D;
     Query::fetch(qraw[gi], (const QT*)p.q + qrow, g, qvec);
   }
+  // lane a's parent in trees of up to 64 nodes (the fused tail's path walks), as tree_parent_lane,
+  // loaded here and resolved once the tile metadata is in: a load waited for after the tile loads
+  // would wait for the tiles as well, loads completing in order
+  const int64_t pa = p.fuse_tail && nq <= kWave && lane < nq ? p.parents[(size_t)b * nq + lane] : -1;
 
   // lane k resolves the wave's k-th tile: byte offset of its 16 K/V rows (-1: unbacked) and,
   // in block mode, its quantization parameters; vmax = largest value scale it holds
@@ -494,6 +499,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   vmax = wave_max_valu(vmax);
   const float vref = vmax > 0.f ? vmax : 1.f;
   const float inv_vref = 1.f / vref;
+  const int pl = (pa >= 0 && pa < lane) ? (int)pa : -1;
 
   // the queries as MFMA operands, prepared once the first tiles are in flight
   Query q[NG];
@@ -717,6 +723,112 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     }
   };
 
+  // Draft tokens [32 j, 32 j + 32) of fp16 drafts copied to LDS (rows: K of nodes 0..nq-1, then V),
+  // as the two 16-token tiles of a pair: S = K_draft . q on MFMA with the lanes' layout of the
+  // prefix tiles, token a masked for node n unless a is n or one of its ancestors (the bit mask
+  // follows the parent lanes `pl` up to the root), the same online softmax update, and P . V with
+  // the fp16 V rows as the A operand into a zeroed accumulator that joins acc in its value units
+  // (1 / vref).  The path walks do the same sum one token at a time.
+  auto draft_pair = [&](int j) {
+    const unsigned char* kst = s_stage;
+    const unsigned char* vst = s_stage + (size_t)nq * D * sizeof(QT);
+    uint64_t anc[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      const int node = node0 + gi * kNodeGroup + nl;
+      int a = node < nq ? node : -1;
+      uint64_t msk = 0;
+      while (__any(a >= 0)) {  // parents precede their children: at most nq steps
+        if (a >= 0) msk |= 1ull << a;
+        const int up = __shfl(pl, a < 0 ? 0 : a, kWave);
+        a = a < 0 ? -1 : up;
+      }
+      anc[gi] = msk;
+    }
+    float s2[2][NG][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int tok = min(32 * j + 16 * t + nl, nq - 1);  // K row of token row nl (clamped: masked)
+      f32x4_t sacc[NG];
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) sacc[gi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const f16x8_t kf = *reinterpret_cast<const f16x8_t*>(
+            kst + ((size_t)tok * D + 16 * (4 * (s >> 1) + g) + 8 * (s & 1)) * sizeof(QT));
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) sacc[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q[gi].hi[s], sacc[gi], 0, 0, 0);
+      }
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        const float kq = q[gi].mul * p.qk_scale;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int a = 32 * j + 16 * t + 4 * g + r;
+          const bool ok = a < nq && ((anc[gi] >> a) & 1);
+          s2[t][gi][r] = ok ? sacc[gi][r] * kq : -__builtin_inff();
+        }
+      }
+    }
+    f16x8_t pw[NG], pl2[NG];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      float mt = kNegBig;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, fmaxf(s2[0][gi][r], s2[1][gi][r]));
+      if (__any(mt > m[gi] + kRescaleSlack)) {
+        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+        const float mnew = fmaxf(m[gi], mt);
+        const float alpha = fast_exp2(m[gi] - mnew);
+        m[gi] = mnew;
+        l[gi] *= alpha;
+#pragma unroll
+        for (int jb = 0; jb < J; ++jb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[gi][jb][r] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pr = fast_exp2(s2[e >> 2][gi][e & 3] - m[gi]);
+        l[gi] += pr;
+        const _Float16 ph = (_Float16)pr;
+        pw[gi][e] = ph;
+        pl2[gi][e] = (_Float16)(pr - (float)ph);
+      }
+    }
+    // V rows of tokens 32 j + 16 t + 4 g + e, dims [J nl, J nl + J) in two halves (clamped rows:
+    // weight 0)
+    constexpr int JH = J / 2;
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      _Float16 vr[2][4][JH];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = min(32 * j + 16 * t + 4 * g + e, nq - 1);
+          __builtin_memcpy(vr[t][e], vst + ((size_t)row * D + J * nl + JH * hb) * sizeof(QT), JH * sizeof(QT));
+        }
+      }
+#pragma unroll
+      for (int jh = 0; jh < JH; ++jh) {
+        const int jb = JH * hb + jh;
+        const f16x8_t vf = {vr[0][0][jh], vr[0][1][jh], vr[0][2][jh], vr[0][3][jh],
+                            vr[1][0][jh], vr[1][1][jh], vr[1][2][jh], vr[1][3][jh]};
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pw[gi], d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl2[gi], d, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[gi][jb][r] = fmaf(d[r], inv_vref, acc[gi][jb][r]);
+        }
+      }
+    }
+  };
+
   // Waves w and w ^ 4 of an 8-wave workgroup share a SIMD, where the older one wins every tie
   // for issue: measured, waves 0-3 finished their tiles 25-40% before waves 4-7, which then ran
   // alone.  With p.pace_waves (grids of more workgroups than CUs, where a CU takes its next
@@ -741,24 +853,28 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   MqTile<DP, TOK> ta, tb, tc, td;
   load(ta, 0);
   load(tb, 1);
-  const int pl = p.fuse_tail ? tree_parent_lane(p.parents, b, nq, lane) : -1;
   const bool staged = STAGE && p.fuse_tail && nq <= kWave &&
                       (((uintptr_t)p.draft_k | (uintptr_t)p.draft_v | (uintptr_t)p.q) & 15) == 0;
   const QT* s_dk = reinterpret_cast<const QT*>(s_stage);
   const QT* s_dv = s_dk + (size_t)nq * D;
   const QT* s_q = s_dv + (size_t)nq * D;
   const size_t r0 = ((size_t)b * nq * p.heads + h) * D;  // draft node 0 of (b, h)
+  // fp16 drafts of a staged tree enter the wave states as tile pairs (draft_pair below), split 0's
+  // only, so that each draft token joins exactly one split's state: the pairs a workgroup's nodes
+  // can reach (their ancestors precede them) go to waves j % W, here 0 and 1, which finish their
+  // prefix tiles first
+  const bool draft_mfma = kDraftMfma && staged;
+  const int npairs = draft_mfma && split == 0 ? (min(nq, node0 + NG * kNodeGroup) + 31) / 32 : 0;
   if (balance && lane == 0) __hip_atomic_store(&s_prog[w], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  if (staged) {
-    // 16-byte chunk e of the copy goes to s_stage + 16 e; wave w moves chunks [64 j, 64 j + 64) for
-    // j = w, w + W, ... with direct global-to-LDS loads (lane l's 16 bytes land at the wave's LDS
-    // address + 16 l), so the copy needs no registers and no wait before the prefix loop: it
-    // completes behind the first tiles and is waited for once the loop is done.
-    constexpr int CPR = DP * (int)sizeof(QT) / 16;  // 16-byte chunks per row (D == DP on this path)
-    const int total = (2 * nq + min(NG * kNodeGroup, nq - node0)) * CPR;  // <= kStageBytes / 16
-    for (int e0 = w * kWave; e0 < total; e0 += W * kWave) {
+  // 16-byte chunk e of the copy goes to s_stage + 16 e, moved by direct global-to-LDS loads (lane
+  // l's 16 bytes land at the wave's LDS address + 16 l) in runs of 64 chunks, so the copy needs no
+  // registers and no wait before the prefix loop: it completes behind the first tiles and is waited
+  // for once the loop is done.
+  constexpr int CPR = DP * (int)sizeof(QT) / 16;  // 16-byte chunks per row (D == DP on this path)
+  auto copy_rows = [&](int c0, int c1, int e_first, int e_step) {  // chunks [c0, c1)
+    for (int e0 = c0 + e_first; e0 < c1; e0 += e_step) {
       const int e = e0 + lane;
-      if (e < total) {
+      if (e < c1) {
         const int r = e / CPR, c = e - r * CPR;
         const QT* row = r < nq       ? (const QT*)p.draft_k + r0 + (size_t)r * p.heads * D
                         : r < 2 * nq ? (const QT*)p.draft_v + r0 + (size_t)(r - nq) * p.heads * D
@@ -768,12 +884,31 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
             (__attribute__((address_space(3))) void*)(s_stage + (size_t)e0 * 16), 16, 0, 0);
       }
     }
+  };
+  if (draft_mfma) {
+    // wave w copies the K and V rows of its own pairs j = w, w + W, ... ([32 j, 32 j + 32)): no
+    // barrier needed
+    for (int j = w; j < npairs; j += W) {
+      const int t0 = 32 * j, t1 = min(nq, t0 + 32);
+      copy_rows(t0 * CPR, t1 * CPR, 0, kWave);
+      copy_rows((nq + t0) * CPR, (nq + t1) * CPR, 0, kWave);
+    }
+  } else if (staged) {
+    // K, V of every node and the workgroup's q rows, for the path walks: wave w moves the runs
+    // j = w, w + W, ...; visible to all waves after the node group's first barrier
+    copy_rows(0, (2 * nq + min(NG * kNodeGroup, nq - node0)) * CPR, w * kWave, W * kWave);  // <= kStageBytes / 16
   }
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     q[gi].prepare(qraw[gi], node0 + gi * kNodeGroup + nl < nq);
     qmul[gi] = q[gi].mul * (TOK ? p.qk_scale : 1.f);
     qsm[gi] = q[gi].sum * qmul[gi];
+  }
+  // the draft pairs start the states of waves 0, 1, once their own copies have landed (behind the
+  // first two tiles, which the loop needs first anyway)
+  if (w < npairs) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (int j = w; j < npairs; j += W) draft_pair(j);
   }
   for (int k = 0; k < nk; k += 4) {
     load(tc, k + 2);
@@ -791,7 +926,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
     __builtin_amdgcn_s_setprio(0);
   }
   // this wave's share of the LDS copy has landed before the barriers that precede the walks
-  if (staged) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (staged && !draft_mfma) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // node `node`'s path tokens into (M, L, acc); the copy is visible after the node group's first barrier
   auto walk = [&](float& M, float& L, float (&acc)[4], int node) __attribute__((always_inline)) {
@@ -826,7 +961,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
         fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
       }
       float M = s_finml[2 * n], L = s_finml[2 * n + 1];
-      walk(M, L, fin, node);
+      if (!draft_mfma) walk(M, L, fin, node);
       tree_write_row<QT>(L, fin, (QT*)p.out + row * D, D, lane);
     }
   };
@@ -909,7 +1044,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
         const int d = lane + c * kWave;
         fin[c] = d < D ? s_fin[n * ROW + d] : 0.f;
       }
-      if (node % nsplit == split) walk(M, L, fin, node);
+      if (!draft_mfma && node % nsplit == split) walk(M, L, fin, node);
       unsigned long long* ws = slot(node, split);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {

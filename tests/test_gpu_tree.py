@@ -202,6 +202,9 @@ MFMA_CASES = [
     (2, 2, 400, 256, 6, 16, "fp8_block", torch.float32, [400, 7]),
     # 512 workgroups of 32 nodes: more than one per CU, so the waves pace each other; drafts staged in LDS
     (8, 32, 256, 128, 64, 16, "affine_block", torch.float16, [256, 256, 100, 256, 17, 256, 256, 240]),
+    # fp16 drafts as MFMA tile pairs in split 0 of rows that split, and with an empty prefix
+    (2, 4, 3000, 128, 48, 16, "affine_block", torch.float16, [3000, 0]),
+    (1, 4, 900, 64, 40, 16, "affine_block", torch.float16, [900]),          # head_dim 64: V rows in halves
 ]
 
 
@@ -351,9 +354,9 @@ def test_tree_parents_cache_reuse_and_change():
 
 
 def test_tree_mfma_unaligned_drafts_walk_global_memory():
-    """Draft tensors whose data does not start on a 16-byte boundary are not copied to LDS: the
-    path walks then read global memory, with the same arithmetic in the same order, so the output
-    is bit-identical to the aligned call's."""
+    """Draft tensors whose data does not start on a 16-byte boundary are not copied to LDS: each
+    node's path is then walked in global memory, token by token, where aligned fp16 drafts enter
+    the prefix states as MFMA tile pairs.  Both match the oracle, and each other to fp32 rounding."""
 
     announce("tree mfma unaligned drafts")
     B, H, S, D, N = 2, 8, 600, 128, 20
@@ -375,4 +378,8 @@ def test_tree_mfma_unaligned_drafts_walk_global_memory():
     b = fa.tree_verify_attention(q, cache, dk_off, dv_off, parents, kernel="mfma")
     torch.cuda.synchronize(DEV)
     assert st["mfma_prefix"] == 1.0
-    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    ref = ot.tree_verify_attention(np_of(q.float()), from_cache(cache), np_of(dk.float()), np_of(dv.float()),
+                                   np_of(parents))
+    assert_attention_close(a, ref, torch.float16, "aligned drafts")
+    assert_attention_close(b, ref, torch.float16, "unaligned drafts")
+    assert (a.float() - b.float()).abs().max().item() <= 2e-3
