@@ -792,6 +792,13 @@ decode_rows_kernel(const DecodeParams p) {
   __shared__ int s_last;
 
   const int lane = threadIdx.x & (kWave - 1);
+  // The kernel arguments and the grid size that the start-up needs, requested in one batch: first
+  // used inside branches, they would otherwise go out in several scalar round trips, one behind the
+  // other, ahead of the row's first loads.
+  asm volatile("" ::"s"(p.q), "s"(p.kv[0]), "s"(p.kv[1]), "s"(p.sc[0]), "s"(p.sc[1]), "s"(p.zp[0]), "s"(p.zp[1]),
+               "s"(p.table), "s"(p.table_cols), "s"(p.table_bytes), "s"(p.lengths), "s"(p.rows), "s"(p.heads),
+               "s"(p.head_dim), "s"(p.seq_len), "s"(p.num_pages), "s"(p.quant_block), "s"(p.page_size),
+               "s"(p.split_tiles), "s"(p.qk_scale), "s"(p.nq), "s"(p.request_order), "s"(gridDim.x), "s"(blockDim.x));
   // wave-uniform by construction; readfirstlane lets the compiler keep everything derived
   // from it (tile counts, tile offsets, load base addresses) in scalar registers
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -800,6 +807,17 @@ decode_rows_kernel(const DecodeParams p) {
   const int row = unit.row, split = unit.split;
   const int b = row / (p.heads * queries_per_head(p));
   const int h = row % p.heads;
+  // The lane's 16 query values (dims [16j, 16j + 16), j = lane % LPT), fetched as 16-byte loads
+  // now, so that their round trip overlaps the row length's and the block table's; converted
+  // once the first tile is on its way.  Head dims that are odd multiples of 8, and queries not
+  // 16-byte aligned, load them there instead.
+  uint4 qraw[sizeof(QT)];
+  const bool qvec = !T8 && ((uintptr_t)p.q & 15) == 0 && 16 * (lane % LPT) < p.head_dim;
+  if (qvec) {
+    const uint4* src = reinterpret_cast<const uint4*>((const QT*)p.q + (size_t)row * p.head_dim + 16 * (lane % LPT));
+#pragma unroll
+    for (int i = 0; i < (int)sizeof(QT); ++i) qraw[i] = src[i];
+  }
   // Lane k of wave w resolves the wave's k-th tile, first + W*k, once: base index (-1 = not
   // backed by a page or past the row) and (key scale * qk_scale, key zero, value scale,
   // value zero).  Waves take tiles w, w+W, w+2W, ...: all waves of all workgroups sweep
@@ -844,16 +862,44 @@ decode_rows_kernel(const DecodeParams p) {
       my_meta1 = t1.meta;
     } else if constexpr (TOK) {
       my_base = token_index<PAGED>(p, b, h, row, my_tile);
-    } else {
+    } else if constexpr (!PAGED) {
       const TileIndex ti = tile_index<PAGED>(p, b, h, row, my_tile);
       my_base = ti.data;
       my_meta = ti.meta;
     }
   }
+  // Paged tiles (other than 8-token and per-token ones): every lane loads the table entry of its
+  // tile, its column clamped into the table (lanes past the wave's tiles or the table discard
+  // theirs), as raw 32-bit words with no branch and no arithmetic on them, so that nothing waits
+  // before the row length's load goes out too; tile_index's checks follow once both have landed.
+  bool my_ok = false;
+  int32_t my_lo = -1, my_hi = -1;
+  if constexpr (PAGED && !SUB && !TOK) {
+    const int lp = my_tile / (p.page_size / kTile);
+    my_ok = lane < nk_max && my_tile < end_max && lp < p.table_cols;
+    if (p.table_cols > 0) {
+      const int64_t idx = (int64_t)b * p.table_cols + min(lp, p.table_cols - 1);
+      const int32_t* e = (const int32_t*)((const char*)p.table + (idx << (p.table_bytes == 4 ? 2 : 3)));
+      my_lo = e[0];
+      my_hi = e[p.table_bytes == 4 ? 0 : 1];  // int32 tables: the same word
+    }
+  }
+  // one wait covers the row length and the table (the length is read into scalar registers, which
+  // needs its value at once); clamped below as row_length / row_length_after_append do
+  const int64_t len_raw = p.lengths != nullptr ? p.lengths[b] : (int64_t)p.seq_len;
+  if constexpr (PAGED && !SUB && !TOK) {
+    const int64_t pg = !my_ok                ? -1
+                       : p.table_bytes == 4 ? (int64_t)my_lo
+                                            : (int64_t)(((uint64_t)(uint32_t)my_hi << 32) | (uint32_t)my_lo);
+    const TileIndex ti = tile_from_page(p, h, my_tile, pg);
+    my_base = ti.data;
+    my_meta = ti.meta;
+  }
 
   // APP: the row covers the appended token too (a token whose page is not backed lies in an
   // unbacked tile and stays masked, which is what the separate append + decode would give)
-  const int len = APP ? row_length_after_append(p.lengths, b, p.seq_len) : row_length(p.lengths, b, p.seq_len);
+  const int64_t len_cap = APP ? (len_raw >= 0 ? len_raw + 1 : 0) : (len_raw < 0 ? 0 : len_raw);
+  const int len = (int)(len_cap < (int64_t)p.seq_len ? len_cap : (int64_t)p.seq_len);
   const int nsplit = row_splits(len, p.split_tiles);
   if (split >= nsplit) return;  // whole workgroup, before any barrier
   const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
@@ -861,12 +907,27 @@ decode_rows_kernel(const DecodeParams p) {
   // CHB: tiles of the row's last block past its end stay in the loop as empty tiles
   if (lane >= nk || my_tile >= tile_end) my_base = my_base1 = -1;
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
+  // the tile parameters as stored; converted (convert_params) once the first tile's loads are out,
+  // so that they share its round trip
+  float ks_raw = 0.f, vs_raw = 0.f;
+  int kz_raw = 0, vz_raw = 0;
   if (!TOK && !CH && my_base >= 0) {
-    my_ks = p.sc[0][my_meta] * p.qk_scale;
-    my_kz = VF == kVfInt8 ? (float)p.zp[0][my_meta] : 0.f;
-    my_vs = p.sc[1][my_meta];
-    my_vz = VF == kVfInt8 ? (float)p.zp[1][my_meta] : 0.f;
+    ks_raw = p.sc[0][my_meta];
+    vs_raw = p.sc[1][my_meta];
+    if constexpr (VF == kVfInt8) {
+      kz_raw = p.zp[0][my_meta];
+      vz_raw = p.zp[1][my_meta];
+    }
   }
+  auto convert_params = [&]() {
+    // the empty asm keeps the conversions here: folded into the load's branch, they would wait there
+    asm volatile("" : "+v"(ks_raw), "+v"(vs_raw), "+v"(kz_raw), "+v"(vz_raw));
+    my_ks = ks_raw * p.qk_scale;
+    my_kz = (float)kz_raw;
+    my_vs = vs_raw;
+    my_vz = (float)vz_raw;
+  };
+  if constexpr (APP) convert_params();  // the append below updates the parameters of its tile
   float my_ks1 = 0.f, my_kz1 = 0.f, my_vs1 = 0.f, my_vz1 = 0.f;
   if constexpr (SUB) {
     if (my_base1 >= 0) {
@@ -911,13 +972,21 @@ decode_rows_kernel(const DecodeParams p) {
   const int rstride = RPL * D;
   using QS = typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>, QSlice<QT>>::type;
   QS q;
-  if (straddle)
-    q.load8((const QT*)p.q + (size_t)row * D + 16 * j);
-  else if (active)
-    q.load((const QT*)p.q + (size_t)row * D + 16 * j);
-  else
-    q.clear();
-  const float qsum = group_sum<LPT>(q.sum());
+  float qsum = 0.f;
+  auto prepare_q = [&]() {
+    if (straddle) {
+      q.load8((const QT*)p.q + (size_t)row * D + 16 * j);
+    } else if (qvec) {
+      QT qv[16];
+      __builtin_memcpy(qv, qraw, sizeof(qv));
+      q.load(qv);
+    } else if (active) {
+      q.load((const QT*)p.q + (size_t)row * D + 16 * j);
+    } else {
+      q.clear();
+    }
+    qsum = group_sum<LPT>(q.sum());
+  };
 
   LaneState st;
   st.m = kNegBig;
@@ -1047,6 +1116,8 @@ decode_rows_kernel(const DecodeParams p) {
     if (k_app >= 0) finish_append(append());
   }
   load(ta, 0);
+  if constexpr (!APP) convert_params();
+  prepare_q();
   for (int k = 0; k < nk; k += 2) {
     load(tb2, k + 1);
     consume(ta, k);

@@ -212,6 +212,16 @@ __device__ __forceinline__ TileIndex tile_index(const DecodeParams& p, int b, in
   }
 }
 
+// The second half of tile_index<true>, for a kernel that loads the table entries itself: the
+// tile of head h that table entry pg (-1: none) names for sequence tile `tile`.
+__device__ __forceinline__ TileIndex tile_from_page(const DecodeParams& p, int h, int tile, int64_t pg) {
+  const int tpq = p.quant_block / kTile, tpp = p.page_size / kTile;
+  const int sub = tile - tile / tpp * tpp;
+  if (pg < 0 || pg >= p.num_pages) return {-1, 0};
+  const int64_t ph = pg * p.heads + h;
+  return {(int)(ph * tpp + sub), (int)(ph * (tpp / tpq) + sub / tpq)};
+}
+
 // 8-token sub-tile `u` of (b, h) for stores whose quant block or page is 8 tokens (an odd
 // multiple of 8): `data` in units of 8*D value bytes, `meta` the scale / zero entry of the
 // quant block holding it; data = -1 when not backed by an allocated page.
