@@ -920,8 +920,9 @@ decode_rows_kernel(const DecodeParams p) {
     }
   }
   auto convert_params = [&]() {
-    // the empty asm keeps the conversions here: folded into the load's branch, they would wait there
-    asm volatile("" : "+v"(ks_raw), "+v"(vs_raw), "+v"(kz_raw), "+v"(vz_raw));
+    // the empty asm keeps the conversions here, and the tile loads ahead of them: folded into the
+    // loads' branch, or with the tile loads moved below them, they would wait before those go out
+    asm volatile("" : "+v"(ks_raw), "+v"(vs_raw), "+v"(kz_raw), "+v"(vz_raw)::"memory");
     my_ks = ks_raw * p.qk_scale;
     my_kz = (float)kz_raw;
     my_vs = vs_raw;
