@@ -884,6 +884,41 @@ decode_rows_kernel(const DecodeParams p) {
       my_hi = e[p.table_bytes == 4 ? 0 : 1];  // int32 tables: the same word
     }
   }
+  const int D = p.head_dim;
+  const int j = lane % LPT;  // dim slice [16j, 16j+16)
+  const int g = lane / LPT;  // token row within a load
+  const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
+  // T8: the lane whose dims [16j, 16j + 16) pass the row end (D = 16j + 8) loads the row's last
+  // 16 bytes, [D - 16, D), and keeps their upper half as its dims 16j .. 16j + 7
+  const bool straddle = T8 && active && 16 * j + 16 > D;
+  const int col = active ? (straddle ? D - 16 : 16 * j) : 0;
+  const int lane_off = g * D + col;
+  const int rstride = RPL * D;
+  // two register buffers: tile k+1 is in flight while tile k is consumed
+  TileRegs<DP> ta, tb2;
+  // the tile parameters as stored; converted (convert_params) once the first tile's loads are out,
+  // so that they share its round trip
+  float ks_raw = 0.f, vs_raw = 0.f;
+  int kz_raw = 0, vz_raw = 0;
+  auto load_params = [&]() {
+    if (!TOK && !CH && my_base >= 0) {
+      ks_raw = p.sc[0][my_meta];
+      vs_raw = p.sc[1][my_meta];
+      if constexpr (VF == kVfInt8) {
+        kz_raw = p.zp[0][my_meta];
+        vz_raw = p.zp[1][my_meta];
+      }
+    }
+  };
+  // SPEC (contiguous rows, block parameters): tile addresses and parameter indices need neither a
+  // table nor the row length, so the lanes' parameters and the wave's first tile load before the
+  // row length has landed (one round trip fewer); lanes and tiles past the row end are masked
+  // below as they are everywhere else, and the speculative loads stay inside the row's store.
+  constexpr bool SPEC = !PAGED && QM == kQmBlock;
+  if constexpr (SPEC) {
+    load_params();
+    load_tile<DP>(ta, p.kv[0], p.kv[1], readlane_i32(my_base, 0), D, lane_off, rstride);
+  }
   // one wait covers the row length and the table (the length is read into scalar registers, which
   // needs its value at once); clamped below as row_length / row_length_after_append do
   const int64_t len_raw = p.lengths != nullptr ? p.lengths[b] : (int64_t)p.seq_len;
@@ -907,26 +942,16 @@ decode_rows_kernel(const DecodeParams p) {
   // CHB: tiles of the row's last block past its end stay in the loop as empty tiles
   if (lane >= nk || my_tile >= tile_end) my_base = my_base1 = -1;
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
-  // the tile parameters as stored; converted (convert_params) once the first tile's loads are out,
-  // so that they share its round trip
-  float ks_raw = 0.f, vs_raw = 0.f;
-  int kz_raw = 0, vz_raw = 0;
-  if (!TOK && !CH && my_base >= 0) {
-    ks_raw = p.sc[0][my_meta];
-    vs_raw = p.sc[1][my_meta];
-    if constexpr (VF == kVfInt8) {
-      kz_raw = p.zp[0][my_meta];
-      vz_raw = p.zp[1][my_meta];
-    }
-  }
+  if constexpr (!SPEC) load_params();
   auto convert_params = [&]() {
     // the empty asm keeps the conversions here, and the tile loads ahead of them: folded into the
     // loads' branch, or with the tile loads moved below them, they would wait before those go out
     asm volatile("" : "+v"(ks_raw), "+v"(vs_raw), "+v"(kz_raw), "+v"(vz_raw)::"memory");
-    my_ks = ks_raw * p.qk_scale;
-    my_kz = (float)kz_raw;
-    my_vs = vs_raw;
-    my_vz = (float)vz_raw;
+    const bool backed = my_base >= 0;  // SPEC loaded lanes now masked: their parameters stay 0
+    my_ks = backed ? ks_raw * p.qk_scale : 0.f;
+    my_kz = backed ? (float)kz_raw : 0.f;
+    my_vs = backed ? vs_raw : 0.f;
+    my_vz = backed ? (float)vz_raw : 0.f;
   };
   if constexpr (APP) convert_params();  // the append below updates the parameters of its tile
   float my_ks1 = 0.f, my_kz1 = 0.f, my_vs1 = 0.f, my_vz1 = 0.f;
@@ -961,16 +986,6 @@ decode_rows_kernel(const DecodeParams p) {
     }
   }
 
-  const int D = p.head_dim;
-  const int j = lane % LPT;  // dim slice [16j, 16j+16)
-  const int g = lane / LPT;  // token row within a load
-  const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
-  // T8: the lane whose dims [16j, 16j + 16) pass the row end (D = 16j + 8) loads the row's last
-  // 16 bytes, [D - 16, D), and keeps their upper half as its dims 16j .. 16j + 7
-  const bool straddle = T8 && active && 16 * j + 16 > D;
-  const int col = active ? (straddle ? D - 16 : 16 * j) : 0;
-  const int lane_off = g * D + col;
-  const int rstride = RPL * D;
   using QS = typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>, QSlice<QT>>::type;
   QS q;
   float qsum = 0.f;
@@ -1111,12 +1126,10 @@ decode_rows_kernel(const DecodeParams p) {
       my_vz = prm[3];
     }
   };
-  // two register buffers: tile k+1 is in flight while tile k is consumed
-  TileRegs<DP> ta, tb2;
   if constexpr (APP) {
     if (k_app >= 0) finish_append(append());
   }
-  load(ta, 0);
+  if constexpr (!SPEC) load(ta, 0);
   if constexpr (!APP) convert_params();
   prepare_q();
   for (int k = 0; k < nk; k += 2) {
