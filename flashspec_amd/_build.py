@@ -43,9 +43,16 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; set HIPCC")
 
 
+# Per-source flags.  The tiled decode kernel leads its arguments with seven 64-bit start-up words
+# that gfx950 preloads into SGPRs (kernel-argument preload, 14 dwords).
+SOURCE_FLAGS = {
+    "fs_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=7"],
+}
+
+
 def _compile(src: Path, extra: list[str]) -> tuple[Path, str]:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr[-8000:]}")

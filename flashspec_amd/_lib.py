@@ -145,7 +145,7 @@ _SIGNATURES = {
     "fs_append_tokens_i8": (
         c_int,
         [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
-         c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p],
+         c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p],
     ),
     "fs_paged_decode_ordered": (
         c_int,
@@ -157,7 +157,7 @@ _SIGNATURES = {
         c_int,
         [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
          c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int, c_int,
-         c_int64, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p],
+         c_int64, c_int, c_int, c_float, c_int, c_int, c_int, c_void_p, c_void_p],
     ),
 }
 

@@ -20,4 +20,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* fs_last_error(void) { return fs::g_last_error.c_str(); }
 
-extern "C" int fs_abi_version(void) { return 1; }
+extern "C" int fs_abi_version(void) { return 2; }

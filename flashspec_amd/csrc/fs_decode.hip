@@ -20,6 +20,7 @@
 // src/flashspec/triton_paged.py:119-299 (masking of tokens past the row length and
 // of unallocated pages; a row with no valid token writes zeros, triton_utils.py:181-186).
 
+#include <atomic>
 #include <type_traits>
 
 #include "fs_paged.h"
@@ -615,11 +616,11 @@ __device__ __forceinline__ void merge_splits_here(const DecodeParams& p, int* s_
 #pragma unroll
   for (int k = 0; k < DPT; ++k) {
     const int d = tid + k * nthr;
-    if (d < D) publish(own + d, a[k]);
+    if (d < D) publish(own + d, a[k], p.merge_tag);
   }
   if (tid == 0) {
-    publish(own + D, M);
-    publish(own + D + 1, L);
+    publish(own + D, M, p.merge_tag);
+    publish(own + D + 1, L, p.merge_tag);
   }
   // the first group of the other splits' words is loaded before the count comes back: the last
   // arrival then usually finds them landed (its partners published before they counted themselves
@@ -666,12 +667,12 @@ __device__ __forceinline__ void merge_splits_here(const DecodeParams& p, int* s_
         for (int k = 0; k < DPT; ++k) x[k] = a[k];
         if (s != split) {
           const unsigned long long* ws = slots + (size_t)s * rs;
-          m = settle_word(v[c][0], ws + D, ok);
-          l = settle_word(v[c][1], ws + D + 1, ok);
+          m = settle_word(v[c][0], ws + D, ok, p.merge_tag);
+          l = settle_word(v[c][1], ws + D + 1, ok, p.merge_tag);
 #pragma unroll
           for (int k = 0; k < DPT; ++k) {
             const int d = tid + k * nthr;
-            x[k] = d < D ? settle_word(v[c][2 + k], ws + d, ok) : 0.f;
+            x[k] = d < D ? settle_word(v[c][2 + k], ws + d, ok, p.merge_tag) : 0.f;
           }
         }
         const float mn = fmaxf(Mr, m);
@@ -777,9 +778,39 @@ constexpr int max_tiled_waves(int DP, int QM = kQmBlock) {
 // Register layout (64, 128 or 256 dims) that serves a head_dim on the tiled path.
 __host__ __device__ constexpr int padded_head_dim(int D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
 
+// ---- start-up words ------------------------------------------------------------------------------
+// The tiled kernel takes four pointers and three 64-bit words ahead of its DecodeParams.  gfx950
+// preloads the first 14 dwords of a kernel's arguments into SGPRs before its first instruction
+// (kernel-argument preload; this file is compiled with -amdgpu-kernarg-preload-count), so the
+// start-up's first loads -- the query, the block-table entries, the row length -- go out at once
+// instead of behind the fetch of the argument block, and the work unit needs no division:
+//   block table (paged), lengths (null: seq_len), q, request order (null: none),
+//   w4 heads | head_dim << 16 | table_cols << 32
+//   w5 split_tiles | batch << 16 | seq_len << 32
+//   w6 log2(waves) | int64 table << 3 | log2(tiles per page) << 4 | grouped heads << 9
+//      | log2(tiles per quant block) << 10 | queries per head << 16 | n_blocks << 32
+// (a log2 field of kLog2None: not a power of two, divided at run time).  The grid is
+// (8 * max_splits, heads / 8 * nq, batch) when heads divide by 8 ("grouped") and
+// (max_splits, heads * nq, batch) otherwise.  The dispatcher hands workgroups to the XCDs
+// round-robin in dispatch order (x fastest), so in the grouped grid XCD x = blockIdx.x % 8 owns
+// heads [x*H/8, (x+1)*H/8) of every request with all their splits: an XCD streams an H/8-head slab
+// of each page rather than one 2 KiB head slice of every page, while every XCD gets the same share
+// of each request (ragged lengths stay balanced).  Measured on one MI355X against the plain order:
+// B8 H32 S4096 paged 46.1 vs 46.9 us, 64 ragged requests 616 vs 624 us; giving each XCD whole
+// requests instead is as fast on uniform lengths but 1.35x slower when lengths descend.
+struct StartWords {
+  const void* table;
+  const int64_t* lengths;
+  const void* q;
+  const int32_t* order;
+  uint64_t w4, w5, w6;
+};
+constexpr int kLog2None = 31;
+
 template <int DP, typename QT, bool PAGED, int QM, int VF>
 __global__ void __launch_bounds__(kWave * max_tiled_waves(DP, QM))
-decode_rows_kernel(const DecodeParams p) {
+decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int32_t* w3, uint64_t w4, uint64_t w5,
+                   uint64_t w6, const DecodeParams p) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
   constexpr bool T8 = QM == kQmBlockTail8 || QM == kQmTokenTail8;  // head_dim an odd multiple of 8
   constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken || QM == kQmTokenTail8, CHB = QM == kQmChannelBlocks;
@@ -792,29 +823,43 @@ decode_rows_kernel(const DecodeParams p) {
   __shared__ int s_last;
 
   const int lane = threadIdx.x & (kWave - 1);
-  // The kernel arguments and the grid size that the start-up needs, requested in one batch: first
-  // used inside branches, they would otherwise go out in several scalar round trips, one behind the
-  // other, ahead of the row's first loads.
-  asm volatile("" ::"s"(p.q), "s"(p.kv[0]), "s"(p.kv[1]), "s"(p.sc[0]), "s"(p.sc[1]), "s"(p.zp[0]), "s"(p.zp[1]),
-               "s"(p.table), "s"(p.table_cols), "s"(p.table_bytes), "s"(p.lengths), "s"(p.rows), "s"(p.heads),
-               "s"(p.head_dim), "s"(p.seq_len), "s"(p.num_pages), "s"(p.quant_block), "s"(p.page_size),
-               "s"(p.split_tiles), "s"(p.qk_scale), "s"(p.nq), "s"(p.request_order), "s"(gridDim.x), "s"(blockDim.x));
+  // (the first four words are pointer arguments, so that the compiler knows them global)
+  const void* const table = w0;
+  const int64_t* const lengths = w1;
+  const QT* const qp = (const QT*)w2;
+  const int32_t* const order = w3;
+  const int heads = (int)(w4 & 0xffffu), D = (int)((w4 >> 16) & 0xffffu), table_cols = (int)(w4 >> 32);
+  const int split_tiles = (int)(w5 & 0xffffu), batch = (int)((w5 >> 16) & 0xffffu), seq_len = (int)(w5 >> 32);
+  const int wlog = (int)(w6 & 7u), W = 1 << wlog;
+  const bool table8 = (w6 >> 3) & 1u, grouped = (w6 >> 9) & 1u;
+  const int tpp_log2 = (int)((w6 >> 4) & 31u), tpq_log2 = (int)((w6 >> 10) & 31u);
+  const int nq = (int)((w6 >> 16) & 0xffffu), n_blocks = (int)(w6 >> 32);
   // wave-uniform by construction; readfirstlane lets the compiler keep everything derived
   // from it (tile counts, tile offsets, load base addresses) in scalar registers
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int W = blockDim.x / kWave;
-  const Unit unit = decode_unit(p, blockIdx.x, gridDim.x);
-  const int row = unit.row, split = unit.split;
-  const int b = row / (p.heads * queries_per_head(p));
-  const int h = row % p.heads;
+  // the work unit (request b, query n, head h, split) from the grid
+  const int split = grouped ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int hg = grouped ? heads >> 3 : heads;
+  int hh = (int)blockIdx.y, n = 0;
+  if (nq > 1) {
+    hh = (int)blockIdx.y / nq;
+    n = (int)blockIdx.y - hh * nq;
+  }
+  int b = (int)blockIdx.z;
+  if (order != nullptr) {
+    const int o = order[b];
+    if ((unsigned)o < (unsigned)batch) b = o;  // an entry outside the batch keeps the natural request
+  }
+  const int h = (grouped ? (int)(blockIdx.x & 7) * hg : 0) + hh;
+  const int row = (b * nq + n) * heads + h;
   // The lane's 16 query values (dims [16j, 16j + 16), j = lane % LPT), fetched as 16-byte loads
   // now, so that their round trip overlaps the row length's and the block table's; converted
   // once the first tile is on its way.  Head dims that are odd multiples of 8, and queries not
   // 16-byte aligned, load them there instead.
   uint4 qraw[sizeof(QT)];
-  const bool qvec = !T8 && ((uintptr_t)p.q & 15) == 0 && 16 * (lane % LPT) < p.head_dim;
+  const bool qvec = !T8 && ((uintptr_t)qp & 15) == 0 && 16 * (lane % LPT) < D;
   if (qvec) {
-    const uint4* src = reinterpret_cast<const uint4*>((const QT*)p.q + (size_t)row * p.head_dim + 16 * (lane % LPT));
+    const uint4* src = reinterpret_cast<const uint4*>(qp + (size_t)row * D + 16 * (lane % LPT));
 #pragma unroll
     for (int i = 0; i < (int)sizeof(QT); ++i) qraw[i] = src[i];
   }
@@ -829,22 +874,22 @@ decode_rows_kernel(const DecodeParams p) {
   // each in turn, so that one parameter load serves G tiles (the host keeps every split a
   // whole number of blocks).
   const int G = CHB ? p.quant_block / kTile : 1;
-  const int sb0 = CHB ? split * p.split_tiles / G : 0;
-  const int first = split * p.split_tiles + w;
+  const int sb0 = CHB ? split * split_tiles / G : 0;
+  const int first = split * split_tiles + w;
   // tiles of this wave below tile `end`
   auto wave_tiles = [&](int end) {
     if constexpr (CHB) {
       const int eb = (end + G - 1) / G;
-      return sb0 + w < eb ? (eb - sb0 - w + W - 1) / W * G : 0;
+      return sb0 + w < eb ? ((eb - sb0 - w + W - 1) >> wlog) * G : 0;
     } else {
-      return first < end ? (end - first + W - 1) / W : 0;
+      return first < end ? (end - first + W - 1) >> wlog : 0;
     }
   };
-  const int tiles_max = (p.seq_len + kTile - 1) / kTile;
-  const int end_max = min(tiles_max, (split + 1) * p.split_tiles);
+  const int tiles_max = (int)(((unsigned)seq_len + kTile - 1) / kTile);
+  const int end_max = min(tiles_max, (split + 1) * split_tiles);
   const int nk_max = wave_tiles(end_max);
   // the wave's lane-th tile
-  int my_tile = first + W * lane;
+  int my_tile = first + (lane << wlog);
   if constexpr (CHB) {
     const int bi = lane / G;
     my_tile = (sb0 + w + W * bi) * G + (lane - bi * G);
@@ -863,9 +908,10 @@ decode_rows_kernel(const DecodeParams p) {
     } else if constexpr (TOK) {
       my_base = token_index<PAGED>(p, b, h, row, my_tile);
     } else if constexpr (!PAGED) {
-      const TileIndex ti = tile_index<PAGED>(p, b, h, row, my_tile);
-      my_base = ti.data;
-      my_meta = ti.meta;
+      // tile_index<false>, with the quant block's tile count from the start-up words
+      const int tpq = tpq_log2 != kLog2None ? 1 << tpq_log2 : p.quant_block / kTile;
+      my_base = row * n_blocks * tpq + my_tile;
+      my_meta = row * n_blocks + (tpq_log2 != kLog2None ? my_tile >> tpq_log2 : my_tile / tpq);
     }
   }
   // Paged tiles (other than 8-token and per-token ones): every lane loads the table entry of its
@@ -875,16 +921,22 @@ decode_rows_kernel(const DecodeParams p) {
   bool my_ok = false;
   int32_t my_lo = -1, my_hi = -1;
   if constexpr (PAGED && !SUB && !TOK) {
-    const int lp = my_tile / (p.page_size / kTile);
-    my_ok = lane < nk_max && my_tile < end_max && lp < p.table_cols;
-    if (p.table_cols > 0) {
-      const int64_t idx = (int64_t)b * p.table_cols + min(lp, p.table_cols - 1);
-      const int32_t* e = (const int32_t*)((const char*)p.table + (idx << (p.table_bytes == 4 ? 2 : 3)));
-      my_lo = e[0];
-      my_hi = e[p.table_bytes == 4 ? 0 : 1];  // int32 tables: the same word
-    }
+    const int lp = tpp_log2 != kLog2None ? my_tile >> tpp_log2 : my_tile / (p.page_size / kTile);
+    my_ok = lane < nk_max && my_tile < end_max && lp < table_cols;
+    const int64_t idx = (int64_t)b * table_cols + min(lp, table_cols - 1);  // table_cols >= 1
+    const int32_t* e = (const int32_t*)((const char*)table + (idx << (table8 ? 3 : 2)));
+    my_lo = e[0];
+    my_hi = e[table8 ? 1 : 0];  // int32 tables: the same word
   }
-  const int D = p.head_dim;
+  // the row length, read into scalar registers (clamped below as row_length /
+  // row_length_after_append do)
+  const int64_t len_raw = lengths != nullptr ? lengths[b] : (int64_t)seq_len;
+  // The argument block's fields that the rest needs, requested in one batch now that the first
+  // loads are out (first used inside branches, they would go out in several scalar round trips one
+  // behind the other); the memory clobber keeps those loads ahead of it.
+  asm volatile("" ::"s"(p.kv[0]), "s"(p.kv[1]), "s"(p.sc[0]), "s"(p.sc[1]), "s"(p.zp[0]), "s"(p.zp[1]),
+               "s"(p.num_pages), "s"(p.quant_block), "s"(p.page_size), "s"(p.qk_scale)
+               : "memory");
   const int j = lane % LPT;  // dim slice [16j, 16j+16)
   const int g = lane / LPT;  // token row within a load
   const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
@@ -919,25 +971,30 @@ decode_rows_kernel(const DecodeParams p) {
     load_params();
     load_tile<DP>(ta, p.kv[0], p.kv[1], readlane_i32(my_base, 0), D, lane_off, rstride);
   }
-  // one wait covers the row length and the table (the length is read into scalar registers, which
-  // needs its value at once); clamped below as row_length / row_length_after_append do
-  const int64_t len_raw = p.lengths != nullptr ? p.lengths[b] : (int64_t)p.seq_len;
   if constexpr (PAGED && !SUB && !TOK) {
-    const int64_t pg = !my_ok                ? -1
-                       : p.table_bytes == 4 ? (int64_t)my_lo
-                                            : (int64_t)(((uint64_t)(uint32_t)my_hi << 32) | (uint32_t)my_lo);
-    const TileIndex ti = tile_from_page(p, h, my_tile, pg);
-    my_base = ti.data;
-    my_meta = ti.meta;
+    const int64_t pg = !my_ok    ? -1
+                       : !table8 ? (int64_t)my_lo
+                                 : (int64_t)(((uint64_t)(uint32_t)my_hi << 32) | (uint32_t)my_lo);
+    if (tpp_log2 != kLog2None && tpq_log2 != kLog2None) {  // tile_from_page with shifts
+      const int sub = my_tile & ((1 << tpp_log2) - 1);
+      const int64_t ph = pg * heads + h;
+      const bool backed = pg >= 0 && pg < p.num_pages;
+      my_base = backed ? (int)(ph << tpp_log2) + sub : -1;
+      my_meta = backed ? (int)(ph << (tpp_log2 - tpq_log2)) + (sub >> tpq_log2) : 0;
+    } else {
+      const TileIndex ti = tile_from_page(p, h, my_tile, pg);
+      my_base = ti.data;
+      my_meta = ti.meta;
+    }
   }
 
   // APP: the row covers the appended token too (a token whose page is not backed lies in an
   // unbacked tile and stays masked, which is what the separate append + decode would give)
   const int64_t len_cap = APP ? (len_raw >= 0 ? len_raw + 1 : 0) : (len_raw < 0 ? 0 : len_raw);
-  const int len = (int)(len_cap < (int64_t)p.seq_len ? len_cap : (int64_t)p.seq_len);
-  const int nsplit = row_splits(len, p.split_tiles);
+  const int len = (int)(len_cap < (int64_t)seq_len ? len_cap : (int64_t)seq_len);
+  const int nsplit = row_splits(len, split_tiles);
   if (split >= nsplit) return;  // whole workgroup, before any barrier
-  const int tile_end = min((len + kTile - 1) / kTile, (split + 1) * p.split_tiles);
+  const int tile_end = min((int)(((unsigned)len + kTile - 1) / kTile), (split + 1) * split_tiles);
   const int nk = wave_tiles(tile_end);  // <= kMaxTilesPerWave
   // CHB: tiles of the row's last block past its end stay in the loop as empty tiles
   if (lane >= nk || my_tile >= tile_end) my_base = my_base1 = -1;
@@ -971,18 +1028,20 @@ decode_rows_kernel(const DecodeParams p) {
   // lengths_out.
   int k_app = -1, app_off = 0;
   if constexpr (APP) {
-    const int64_t pos = p.lengths[b];
-    const bool in_range = pos >= 0 && pos < p.seq_len;
+    const int64_t pos = len_raw;
+    const bool in_range = pos >= 0 && pos < seq_len;
     if (in_range) {
-      const int rel = (int)(pos / kTile) - split * p.split_tiles;
-      if (rel >= 0 && rel < p.split_tiles && rel % W == w && readlane_i32(my_base, rel / W) >= 0) {
-        k_app = rel / W;  // nk - 1: the row's last token is pos
+      const int rel = (int)(pos / kTile) - split * split_tiles;
+      if (rel >= 0 && rel < split_tiles && (rel & (W - 1)) == w && readlane_i32(my_base, rel >> wlog) >= 0) {
+        k_app = rel >> wlog;  // nk - 1: the row's last token is pos
         app_off = (int)(pos % kTile);
       }
     }
     if (h == 0 && split == 0 && w == 0 && lane == 0) {
       const bool stored = in_range && tile_index<true>(p, b, 0, row, (int)(pos / kTile)).data >= 0;
       p.lengths_out[b] = stored ? pos + 1 : pos;  // fs_append_tokens_i8's rule
+      if (!stored && p.dropped != nullptr)
+        __hip_atomic_fetch_add(p.dropped, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
@@ -991,13 +1050,13 @@ decode_rows_kernel(const DecodeParams p) {
   float qsum = 0.f;
   auto prepare_q = [&]() {
     if (straddle) {
-      q.load8((const QT*)p.q + (size_t)row * D + 16 * j);
+      q.load8(qp + (size_t)row * D + 16 * j);
     } else if (qvec) {
       QT qv[16];
       __builtin_memcpy(qv, qraw, sizeof(qv));
       q.load(qv);
     } else if (active) {
-      q.load((const QT*)p.q + (size_t)row * D + 16 * j);
+      q.load(qp + (size_t)row * D + 16 * j);
     } else {
       q.clear();
     }
@@ -1284,14 +1343,18 @@ decode_generic_kernel(const DecodeParams p) {
 
 // ---- split merge (second launch) -----------------------------------------------------------------
 
+// appended = 1: `lengths` holds the positions before a fused one-token append, and each row covers
+// position + 1 tokens (row_length_after_append), as the decode launch that wrote the partials did.
 template <typename OT>
 __global__ void __launch_bounds__(256)
 combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t* lengths, OT* out, int rows,
-                      int heads, int D, int seq_len, int split_tiles, int max_splits) {
+                      int heads, int D, int seq_len, int split_tiles, int max_splits, int appended) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
   if (row >= rows) return;
-  const int nsplit = row_splits(row_length(lengths, row / heads, seq_len), split_tiles);
+  const int b = row / heads;
+  const int len = appended ? row_length_after_append(lengths, b, seq_len) : row_length(lengths, b, seq_len);
+  const int nsplit = row_splits(len, split_tiles);
   if (nsplit == 1) return;  // the decode kernel already wrote this row
   const float* ml = part_ml + (size_t)row * max_splits * 2;
   const float* pacc = part_acc + (size_t)row * max_splits * D;
@@ -1355,27 +1418,68 @@ static bool channel_whole_blocks(const DecodeParams& p) {
   return p.quant_block / kTile >= 2 && padded_head_dim(p.head_dim) <= 128;
 }
 
+// log2(v) for a power of two v >= 1, else kLog2None
+static int log2_or_none(int v) { return v >= 1 && (v & (v - 1)) == 0 ? __builtin_ctz((unsigned)v) : kLog2None; }
+
+// The start-up words and the grid of a tiled launch (layout at StartWords).
+static int tiled_launch_shape(const DecodeParams& p, int waves, StartWords& sw, dim3& grid) {
+  const int nq = p.nq > 1 ? p.nq : 1;
+  const int batch = p.rows / (p.heads * nq);
+  const bool grouped = p.heads % kXcds == 0;
+  const int hg = grouped ? p.heads / kXcds : p.heads;
+  if (batch > 0xffff) return set_error(FS_ERR_INVALID, "the tiled decode takes at most 65535 requests per launch");
+  if ((int64_t)hg * nq > 0xffff || p.heads > 0xffff)
+    return set_error(FS_ERR_INVALID, "too many heads (times query rows per head) for the tiled decode grid");
+  if (p.split_tiles > 0xffff) return set_error(FS_ERR_INVALID, "split_tiles too large for the tiled decode");
+  if (p.table_cols > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "block_table has too many columns");
+  if ((int64_t)p.max_splits * (grouped ? kXcds : 1) > 0x7fffffffLL)
+    return set_error(FS_ERR_INVALID, "decode grid too large");
+  const int tpq = p.quant_block / kTile;
+  sw.table = p.table;
+  sw.lengths = p.lengths;
+  sw.q = p.q;
+  sw.order = p.request_order;
+  sw.w4 = (uint64_t)(uint32_t)p.heads | (uint64_t)(uint32_t)p.head_dim << 16 | (uint64_t)p.table_cols << 32;
+  sw.w5 = (uint64_t)(uint32_t)p.split_tiles | (uint64_t)(uint32_t)batch << 16 | (uint64_t)(uint32_t)p.seq_len << 32;
+  sw.w6 = (uint64_t)__builtin_ctz((unsigned)waves) | (uint64_t)(p.table_bytes == 8) << 3 |
+            (uint64_t)log2_or_none(p.page_size / kTile) << 4 | (uint64_t)grouped << 9 |
+            (uint64_t)log2_or_none(tpq) << 10 | (uint64_t)(uint32_t)nq << 16 | (uint64_t)(uint32_t)p.n_blocks << 32;
+  grid = grouped ? dim3((unsigned)(kXcds * p.max_splits), (unsigned)(hg * nq), (unsigned)batch)
+                 : dim3((unsigned)p.max_splits, (unsigned)(p.heads * nq), (unsigned)batch);
+  return FS_OK;
+}
+
 template <typename QT, bool PAGED, int QM, int VF>
-static void launch_tiled_vf(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
+static void launch_tiled_vf(const DecodeParams& p, const StartWords& s, dim3 grid, dim3 block, hipStream_t st) {
+  const void *t = s.table, *q = s.q;
+  const int64_t* l = s.lengths;
+  const int32_t* o = s.order;
   switch (padded_head_dim(p.head_dim)) {
-    case 64: hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
-    case 128: hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, QM, VF>), grid, block, 0, st, p); break;
+    case 64:
+      hipLaunchKernelGGL((decode_rows_kernel<64, QT, PAGED, QM, VF>), grid, block, 0, st, t, l, q, o, s.w4,
+                         s.w5, s.w6, p);
+      break;
+    case 128:
+      hipLaunchKernelGGL((decode_rows_kernel<128, QT, PAGED, QM, VF>), grid, block, 0, st, t, l, q, o, s.w4,
+                         s.w5, s.w6, p);
+      break;
     default:  // the whole-block per-channel form is dispatched on the 64- and 128-dim layouts only
       if constexpr (QM != kQmChannelBlocks)
-        hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, QM, VF>), grid, block, 0, st, p);
+        hipLaunchKernelGGL((decode_rows_kernel<256, QT, PAGED, QM, VF>), grid, block, 0, st, t, l, q, o,
+                           s.w4, s.w5, s.w6, p);
       break;
   }
 }
 
 template <typename QT, bool PAGED, int QM>
-static void launch_tiled(const DecodeParams& p, dim3 grid, dim3 block, hipStream_t st) {
+static void launch_tiled(const DecodeParams& p, const StartWords& s, dim3 grid, dim3 block, hipStream_t st) {
   if constexpr (QM == kQmChannel || QM == kQmChannelBlocks || QM == kQmBlockAppend) {
-    launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);  // per-channel / appending stores are INT8
+    launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, s, grid, block, st);  // per-channel / appending stores are INT8
   } else {
     if (p.vfmt == kVfFp8)
-      launch_tiled_vf<QT, PAGED, QM, kVfFp8>(p, grid, block, st);
+      launch_tiled_vf<QT, PAGED, QM, kVfFp8>(p, s, grid, block, st);
     else
-      launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, grid, block, st);
+      launch_tiled_vf<QT, PAGED, QM, kVfInt8>(p, s, grid, block, st);
   }
 }
 
@@ -1383,27 +1487,29 @@ template <typename QT, bool PAGED>
 static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, hipStream_t st) {
   const dim3 block(kWave * waves_per_block);
   if (tiled) {
-    const dim3 grid((unsigned)((int64_t)p.rows * p.max_splits));
+    StartWords sw;
+    dim3 grid;
+    if (int rc = tiled_launch_shape(p, waves_per_block, sw, grid)) return rc;
     if constexpr (PAGED) {
       if (p.append_k != nullptr) {
-        launch_tiled<QT, PAGED, kQmBlockAppend>(p, grid, block, st);
+        launch_tiled<QT, PAGED, kQmBlockAppend>(p, sw, grid, block, st);
         return check_launch("paged_decode_append_kernel");
       }
     }
     if (p.per_channel && channel_whole_blocks(p))
-      launch_tiled<QT, PAGED, kQmChannelBlocks>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmChannelBlocks>(p, sw, grid, block, st);
     else if (p.per_channel)
-      launch_tiled<QT, PAGED, kQmChannel>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmChannel>(p, sw, grid, block, st);
     else if (p.quant_block == 1 && p.head_dim % 16 != 0)
-      launch_tiled<QT, PAGED, kQmTokenTail8>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmTokenTail8>(p, sw, grid, block, st);
     else if (p.quant_block == 1)
-      launch_tiled<QT, PAGED, kQmToken>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmToken>(p, sw, grid, block, st);
     else if (p.quant_block % kTile != 0)
-      launch_tiled<QT, PAGED, kQmSub>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmSub>(p, sw, grid, block, st);
     else if (p.head_dim % 16 != 0)
-      launch_tiled<QT, PAGED, kQmBlockTail8>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmBlockTail8>(p, sw, grid, block, st);
     else
-      launch_tiled<QT, PAGED, kQmBlock>(p, grid, block, st);
+      launch_tiled<QT, PAGED, kQmBlock>(p, sw, grid, block, st);
   } else {
     const int64_t waves = (int64_t)p.rows * p.max_splits;
     const dim3 grid((unsigned)((waves + waves_per_block - 1) / waves_per_block));
@@ -1437,6 +1543,14 @@ static void bind_workspace(DecodeParams& p, void* workspace) {
   p.part_ml = workspace ? (float*)workspace + (size_t)p.rows * p.max_splits * p.head_dim : nullptr;
 }
 
+// A fresh nonzero tag for a launch's merge words (DecodeParams::merge_tag).
+static unsigned next_merge_tag() {
+  static std::atomic<unsigned> counter{0};
+  unsigned t;
+  do t = counter.fetch_add(1, std::memory_order_relaxed) + 1; while (t == 0);
+  return t;
+}
+
 // Merge area layout: arrival counts [rows] (padded to 256 bytes), then tagged partial states
 // [rows, max_splits, head_dim + 2] as 64-bit words.
 static int bind_merge_area(DecodeParams& p, void* area, int64_t area_bytes) {
@@ -1449,6 +1563,7 @@ static int bind_merge_area(DecodeParams& p, void* area, int64_t area_bytes) {
                                          std::to_string(need) + " bytes)");
   p.merge_count = (unsigned*)area;
   p.merge_slots = (unsigned long long*)((char*)area + ((int64_t)p.rows * 4 + 255) / 256 * 256);
+  p.merge_tag = next_merge_tag();
   return FS_OK;
 }
 
@@ -1725,6 +1840,10 @@ extern "C" int fs_paged_decode_merged(const void* q, int q_dtype, int kv_format,
                       merge_area_bytes < 0 ? 0 : merge_area_bytes);
 }
 
+static int combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype, int batch,
+                          int heads, int head_dim, int seq_len, int split_tiles, int max_splits, int appended,
+                          void* stream);
+
 extern "C" int fs_paged_decode_append_i8(const void* q, int q_dtype, const void* k_new, const void* v_new,
                                          int8_t* k_values, float* k_scale, int16_t* k_zero, int8_t* v_values,
                                          float* v_scale, int16_t* v_zero, const void* block_table,
@@ -1733,7 +1852,7 @@ extern "C" int fs_paged_decode_append_i8(const void* q, int q_dtype, const void*
                                          void* merge_area, int64_t merge_area_bytes, int batch, int heads,
                                          int head_dim, int64_t num_pages, int page_size, int max_seq_len,
                                          float sm_scale, int split_tiles, int max_splits, int waves_per_block,
-                                         void* stream) {
+                                         unsigned* dropped, void* stream) {
   if (page_size != kTile)
     return set_error(FS_ERR_INVALID, "the fused append needs 16-token pages holding one quant block");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
@@ -1753,11 +1872,14 @@ extern "C" int fs_paged_decode_append_i8(const void* q, int q_dtype, const void*
   p.append_k = k_new;
   p.append_v = v_new;
   p.lengths_out = lengths_out;
+  p.dropped = dropped;
   hipStream_t st = (hipStream_t)stream;
   if (int rc = launch_decode<true>(p, q_dtype, tiled, waves_per_block, st)) return rc;
-  if (p.max_splits > 1 && p.merge_count == nullptr)  // split partials: merged over the advanced lengths
-    return fs_combine_splits(workspace, lengths_out, out, q_dtype, batch, heads, head_dim, max_seq_len, split_tiles,
-                             max_splits, stream);
+  // split partials: merged over the rows the decode covered, position + 1 tokens each (lengths_out holds
+  // the position itself where the token was not stored, but its masked tile still counted there)
+  if (p.max_splits > 1 && p.merge_count == nullptr)
+    return combine_splits(workspace, lengths_in, out, q_dtype, batch, heads, head_dim, max_seq_len, split_tiles,
+                          max_splits, 1, stream);
   return FS_OK;
 }
 
@@ -1788,9 +1910,10 @@ extern "C" int fs_paged_decode_ordered(const void* q, int q_dtype, const int8_t*
   return FS_OK;
 }
 
-extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype,
-                                 int batch, int heads, int head_dim, int seq_len, int split_tiles,
-                                 int max_splits, void* stream) {
+// The split merge launch over a decode's workspace (appended: see combine_splits_kernel).
+static int combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype, int batch,
+                          int heads, int head_dim, int seq_len, int split_tiles, int max_splits, int appended,
+                          void* stream) {
   if (batch <= 0 || heads <= 0 || head_dim <= 0 || head_dim > 256 || split_tiles <= 0 || max_splits <= 0)
     return set_error(FS_ERR_INVALID, "invalid combine shape");
   if (!workspace || !out) return set_error(FS_ERR_INVALID, "null workspace or output");
@@ -1802,18 +1925,24 @@ extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, 
   switch (out_dtype) {
     case FS_F32:
       hipLaunchKernelGGL(combine_splits_kernel<float>, grid, block, 0, st, ml, acc, lengths, (float*)out, rows,
-                         heads, head_dim, seq_len, split_tiles, max_splits);
+                         heads, head_dim, seq_len, split_tiles, max_splits, appended);
       break;
     case FS_F16:
       hipLaunchKernelGGL(combine_splits_kernel<__half>, grid, block, 0, st, ml, acc, lengths, (__half*)out, rows,
-                         heads, head_dim, seq_len, split_tiles, max_splits);
+                         heads, head_dim, seq_len, split_tiles, max_splits, appended);
       break;
     case FS_BF16:
       hipLaunchKernelGGL(combine_splits_kernel<__hip_bfloat16>, grid, block, 0, st, ml, acc, lengths,
-                         (__hip_bfloat16*)out, rows, heads, head_dim, seq_len, split_tiles, max_splits);
+                         (__hip_bfloat16*)out, rows, heads, head_dim, seq_len, split_tiles, max_splits, appended);
       break;
     default: return set_error(FS_ERR_INVALID, "out dtype code must be 0, 1 or 2");
   }
   return check_launch("combine_splits_kernel");
 }
 
+extern "C" int fs_combine_splits(const void* workspace, const int64_t* lengths, void* out, int out_dtype,
+                                 int batch, int heads, int head_dim, int seq_len, int split_tiles,
+                                 int max_splits, void* stream) {
+  return combine_splits(workspace, lengths, out, out_dtype, batch, heads, head_dim, seq_len, split_tiles, max_splits,
+                        0, stream);
+}

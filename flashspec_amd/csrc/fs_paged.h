@@ -72,6 +72,10 @@ struct DecodeParams {
   // the upper half); the last split of a row to arrive merges the row and zeroes what it used.
   unsigned* merge_count;
   unsigned long long* merge_slots;
+  // The launch's tag in the upper half of its merge words (never 0, taken from a per-process counter
+  // at every launch): a word that a split of an earlier launch stored after that launch had given up
+  // waiting for it and cleared the area carries another tag, so it never passes for a later launch's.
+  unsigned merge_tag;
   // One-token append fused into the paged decode (kQmBlockAppend): `lengths` holds each request's
   // position before the append; the new K / V rows append_k / append_v [rows, head_dim] (q's
   // dtype) go into the page at that position, which is requantized in place, and the advanced
@@ -79,6 +83,7 @@ struct DecodeParams {
   const void* append_k;
   const void* append_v;
   int64_t* lengths_out;
+  unsigned* dropped;  // counts the appended tokens that were not stored (NULL: not counted)
   // Dispatch order of the requests (tiled decode): workgroups take request request_order[i] in the
   // place of request i (a permutation of [0, batch); NULL = natural order).  Serving batches pass
   // their requests longest first, so the last round of workgroups holds short rows.
@@ -86,13 +91,15 @@ struct DecodeParams {
 };
 
 // Words of the in-kernel split merge (decode rows and tree verification): a split's state goes out
-// as 64-bit words tagged 1 in the upper half with relaxed agent-scope atomic stores, so a reader
-// sees a word whole or not at all and waits on the tag, not on a fence; the waits are bounded by
-// kMergeSpins (a row whose words never land is written as NaN).
+// as 64-bit words with the launch's tag in the upper half (DecodeParams::merge_tag), stored with
+// relaxed agent-scope atomic stores, so a reader sees a word whole or not at all and waits on the
+// tag, not on a fence; the waits are bounded by kMergeSpins (a row whose words never land is written
+// as NaN).
 constexpr int kMergeSpins = 1 << 14;
 
-__device__ __forceinline__ void publish(unsigned long long* w, float x) {
-  __hip_atomic_store(w, (1ull << 32) | __float_as_uint(x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void publish(unsigned long long* w, float x, unsigned tag) {
+  __hip_atomic_store(w, ((unsigned long long)tag << 32) | __float_as_uint(x), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void clear_word(unsigned long long* w) {
@@ -103,13 +110,14 @@ __device__ __forceinline__ unsigned long long load_word(const unsigned long long
   return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The value of word w, given a first load v of it: reloads until the tag is set.
-__device__ __forceinline__ float settle_word(unsigned long long v, const unsigned long long* w, bool& ok) {
-  for (int n = 0; (v >> 32) != 1ull && n < kMergeSpins; ++n) {
+// The value of word w, given a first load v of it: reloads until it carries the launch's tag.
+__device__ __forceinline__ float settle_word(unsigned long long v, const unsigned long long* w, bool& ok,
+                                            unsigned tag) {
+  for (int n = 0; (unsigned)(v >> 32) != tag && n < kMergeSpins; ++n) {
     __builtin_amdgcn_s_sleep(1);
     v = load_word(w);
   }
-  ok = ok && (v >> 32) == 1ull;
+  ok = ok && (unsigned)(v >> 32) == tag;
   return __uint_as_float((unsigned)v);
 }
 
@@ -120,47 +128,13 @@ __host__ __device__ inline int64_t merge_area_bytes(int64_t rows, int64_t max_sp
 
 __device__ __forceinline__ int queries_per_head(const DecodeParams& p) { return p.nq > 1 ? p.nq : 1; }
 
-// The dispatcher hands workgroups to the XCDs round-robin (workgroup i to XCD i % 8).
-// decode_unit renumbers them so that XCD x owns heads [x*H/8, (x+1)*H/8) of every batch
-// (all their splits): an XCD then streams an H/8-head slab of each page instead of one
-// 2 KiB head slice of every page, while every XCD still gets the same share of each
-// request, so ragged lengths stay balanced across XCDs.  Measured on one MI355X against the
-// plain order: B8 H32 S4096 paged 46.1 vs 46.9 us, 64 ragged requests 616 vs 624 us.
-// Giving each XCD whole batches instead is as fast on uniform lengths but 1.35x slower
-// when lengths descend across the batch.  Heads not divisible by 8 keep the plain order.
+// The dispatcher hands workgroups to the XCDs round-robin (workgroup i to XCD i % 8), each with its
+// own L2.  xcd_chunked_unit renumbers a 1-D grid of `units` so that XCD x takes the x-th eighth of
+// the units in order (the tree kernel orders its units so that an eighth is a slab of heads).
 __device__ __forceinline__ int xcd_chunked_unit(int bid, int units) {
   const int per = units / kXcds, rem = units - per * kXcds;
   const int x = bid % kXcds, k = bid / kXcds;
   return x * per + min(x, rem) + k;
-}
-
-struct Unit {
-  int row, split;
-};
-
-__device__ __forceinline__ Unit decode_unit(const DecodeParams& p, int bid, int units) {
-  // pos = (((x * batch + b) * hg + hh) * nq + n) * max_splits + split with head h = x * hg + hh
-  // and row = (b * nq + n) * heads + h; with hg = heads (heads not divisible by 8) the same
-  // formula is the plain order, x = 0.  The nq query rows of one (request, head) are adjacent
-  // on one XCD, so they read the same pages at the same time (L2 hits after the first).
-  const bool grouped = p.heads % kXcds == 0;
-  const int hg = grouped ? p.heads / kXcds : p.heads;
-  const int nq = queries_per_head(p);
-  const int pos = grouped ? xcd_chunked_unit(bid, units) : bid;
-  const int batch = p.rows / (p.heads * nq);
-  const int split = pos % p.max_splits;
-  int t = pos / p.max_splits;
-  const int n = t % nq;
-  t /= nq;
-  const int hh = t % hg;
-  t /= hg;
-  int b = t % batch;
-  const int x = t / batch;
-  if (p.request_order != nullptr) {
-    const int o = p.request_order[b];
-    if ((unsigned)o < (unsigned)batch) b = o;  // an entry outside the batch keeps the natural request
-  }
-  return {(b * nq + n) * p.heads + x * hg + hh, split};
 }
 
 __device__ __forceinline__ int row_length(const int64_t* lengths, int b, int seq_len) {

@@ -420,14 +420,21 @@ struct PageStore {
   int16_t* zero;
 };
 
+// The advanced length of request b after its token at `pos` was stored (ok) or dropped; a dropped
+// token also counts into *dropped when the caller gave a counter.
+__device__ __forceinline__ void count_append(int64_t* lengths_out, unsigned* dropped, int b, int64_t pos, bool ok) {
+  lengths_out[b] = ok ? pos + 1 : pos;
+  if (!ok && dropped != nullptr) __hip_atomic_fetch_add(dropped, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One decode token per request (see fs_append_tokens_i8).  Group (kv, b, h): position
 // pos = lengths_in[b] lands in row pos % page of page table[b, pos / page]; the page is
 // dequantized (stale rows included), that row replaced, and the page requantized in place.
 template <typename XT, typename IT>
 __global__ void __launch_bounds__(256)
 append_tokens_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageStore vs, int64_t num_pages,
-                     const IT* table, int table_cols, const int64_t* lengths_in, int64_t* lengths_out, int B,
-                     int H, int page, int D) {
+                     const IT* table, int table_cols, const int64_t* lengths_in, int64_t* lengths_out,
+                     unsigned* dropped, int B, int H, int page, int D) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const int64_t rows = (int64_t)B * H;
@@ -440,7 +447,7 @@ append_tokens_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageStore v
   const int64_t lp = pos >= 0 ? pos / page : -1;
   const int64_t pg = (lp >= 0 && lp < table_cols) ? (int64_t)table[(size_t)b * table_cols + lp] : -1;
   const bool ok = pg >= 0 && pg < num_pages;
-  if (kv == 0 && h == 0 && lane == 0) lengths_out[b] = ok ? pos + 1 : pos;
+  if (kv == 0 && h == 0 && lane == 0) count_append(lengths_out, dropped, b, pos, ok);
   if (!ok) return;
   const int off = (int)(pos - lp * page);
   const PageStore st = kv ? vs : ks;
@@ -463,7 +470,7 @@ template <int CH, typename XT>
 __global__ void __launch_bounds__(256)
 append_tokens_vec_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageStore vs, int64_t num_pages,
                          const void* table, int table_bytes, int table_cols, const int64_t* lengths_in,
-                         int64_t* lengths_out, int B, int H, int page, int D) {
+                         int64_t* lengths_out, unsigned* dropped, int B, int H, int page, int D) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t grp = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const int64_t rows = (int64_t)B * H;
@@ -480,7 +487,7 @@ append_tokens_vec_kernel(const XT* k_new, const XT* v_new, PageStore ks, PageSto
     pg = table_bytes == 4 ? (int64_t)((const int32_t*)table)[ti] : ((const int64_t*)table)[ti];
   }
   const bool ok = pg >= 0 && pg < num_pages;
-  if (kv == 0 && h == 0 && lane == 0) lengths_out[b] = ok ? pos + 1 : pos;
+  if (kv == 0 && h == 0 && lane == 0) count_append(lengths_out, dropped, b, pos, ok);
   if (!ok) return;
   const int off = (int)(pos - lp * page);
   const PageStore st = kv ? vs : ks;
@@ -649,13 +656,14 @@ static int launch_vec_blocks(int ch, dim3 grid, hipStream_t st, const XT* x, int
 template <typename XT>
 static int launch_vec_append(int ch, dim3 grid, hipStream_t st, const XT* k_new, const XT* v_new, PageStore ks,
                              PageStore vs, int64_t num_pages, const void* table, int table_bytes, int table_cols,
-                             const int64_t* lengths_in, int64_t* lengths_out, int B, int H, int page, int D) {
+                             const int64_t* lengths_in, int64_t* lengths_out, unsigned* dropped, int B, int H,
+                             int page, int D) {
   const dim3 block(256);
   switch (ch) {
-    case 1: hipLaunchKernelGGL((append_tokens_vec_kernel<1, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
-    case 2: hipLaunchKernelGGL((append_tokens_vec_kernel<2, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
-    case 4: hipLaunchKernelGGL((append_tokens_vec_kernel<4, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
-    default: hipLaunchKernelGGL((append_tokens_vec_kernel<8, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, B, H, page, D); break;
+    case 1: hipLaunchKernelGGL((append_tokens_vec_kernel<1, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, dropped, B, H, page, D); break;
+    case 2: hipLaunchKernelGGL((append_tokens_vec_kernel<2, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, dropped, B, H, page, D); break;
+    case 4: hipLaunchKernelGGL((append_tokens_vec_kernel<4, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, dropped, B, H, page, D); break;
+    default: hipLaunchKernelGGL((append_tokens_vec_kernel<8, XT>), grid, block, 0, st, k_new, v_new, ks, vs, num_pages, table, table_bytes, table_cols, lengths_in, lengths_out, dropped, B, H, page, D); break;
   }
   return check_launch("append_tokens");
 }
@@ -789,7 +797,7 @@ extern "C" int fs_append_tokens_i8(const void* k_new, const void* v_new, int src
                                    int16_t* v_zero, int64_t num_pages, const void* block_table,
                                    int table_index_bytes, int table_cols, const int64_t* lengths_in,
                                    int64_t* lengths_out, int batch, int heads, int head_dim, int page_size,
-                                   void* stream) {
+                                   unsigned* dropped, void* stream) {
   if (batch <= 0) return FS_OK;
   if (heads <= 0 || head_dim <= 0 || page_size <= 0 || num_pages <= 0 || table_cols <= 0)
     return set_error(FS_ERR_INVALID, "append_tokens: sizes must be positive");
@@ -808,16 +816,16 @@ extern "C" int fs_append_tokens_i8(const void* k_new, const void* v_new, int src
   if (is_pow2_chunks(ch) && ((uintptr_t)k_new % 16) == 0 && ((uintptr_t)v_new % 16) == 0 &&
       ((uintptr_t)k_values % 8) == 0 && ((uintptr_t)v_values % 8) == 0) {
     switch (src_dtype) {
-      case FS_F32: return launch_vec_append<float>(ch, grid, st, (const float*)k_new, (const float*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, batch, heads, page_size, head_dim);
-      case FS_F16: return launch_vec_append<__half>(ch, grid, st, (const __half*)k_new, (const __half*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, batch, heads, page_size, head_dim);
-      case FS_BF16: return launch_vec_append<__hip_bfloat16>(ch, grid, st, (const __hip_bfloat16*)k_new, (const __hip_bfloat16*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, batch, heads, page_size, head_dim);
+      case FS_F32: return launch_vec_append<float>(ch, grid, st, (const float*)k_new, (const float*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, dropped, batch, heads, page_size, head_dim);
+      case FS_F16: return launch_vec_append<__half>(ch, grid, st, (const __half*)k_new, (const __half*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, dropped, batch, heads, page_size, head_dim);
+      case FS_BF16: return launch_vec_append<__hip_bfloat16>(ch, grid, st, (const __hip_bfloat16*)k_new, (const __hip_bfloat16*)v_new, ks, vs, num_pages, block_table, table_index_bytes, table_cols, lengths_in, lengths_out, dropped, batch, heads, page_size, head_dim);
       default: return set_error(FS_ERR_INVALID, "append_tokens: dtype code must be 0, 1 or 2");
     }
   }
 #define FS_APPEND(XT, IT)                                                                                       \
   hipLaunchKernelGGL((append_tokens_kernel<XT, IT>), grid, block, 0, st, (const XT*)k_new, (const XT*)v_new, ks, \
-                     vs, num_pages, (const IT*)block_table, table_cols, lengths_in, lengths_out, batch, heads,   \
-                     page_size, head_dim)
+                     vs, num_pages, (const IT*)block_table, table_cols, lengths_in, lengths_out, dropped, batch, \
+                     heads, page_size, head_dim)
 #define FS_APPEND_IDX(XT) \
   if (table_index_bytes == 4) FS_APPEND(XT, int32_t); else FS_APPEND(XT, int64_t)
   switch (src_dtype) {

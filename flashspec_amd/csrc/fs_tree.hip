@@ -224,8 +224,8 @@ struct TreeUnit {
 };
 
 // pos = ((((x * batch + b) * hg + hh) * groups + grp) * max_splits + split, head h = x * hg + hh:
-// XCD x owns heads [x*H/8, (x+1)*H/8) of every request (plain order when H % 8 != 0), as in
-// the row kernel's decode_unit.
+// XCD x owns heads [x*H/8, (x+1)*H/8) of every request (plain order when H % 8 != 0), as the row
+// decode kernel's grid gives it.
 __device__ __forceinline__ TreeUnit tree_unit(const DecodeParams& p, int groups, int bid, int units) {
   const bool grouped = p.heads % kXcds == 0;
   const int hg = grouped ? p.heads / kXcds : p.heads;
@@ -1049,11 +1049,11 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d = lane + c * kWave;
-        if (d < D) publish(ws + d, fin[c]);
+        if (d < D) publish(ws + d, fin[c], p.merge_tag);
       }
       if (lane == 0) {
-        publish(ws + D, M);
-        publish(ws + D + 1, L);
+        publish(ws + D, M, p.merge_tag);
+        publish(ws + D + 1, L, p.merge_tag);
       }
     }
   }
@@ -1071,7 +1071,9 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   // order; (3) per (node, dim) the output sum_s x_s * weight / L, with each thread's loads of up to
   // 4 entries x 2 splits issued together before any is waited on.  A word that never lands makes
   // its row NaN.
-  float* s_w = s_acc;  // [node][split]: m, then the weight
+  // [node][split]: m, then the weight; and l.  2 * 16 * max_splits floats, which the host keeps
+  // within s_acc (tree_merge_max_splits)
+  float* s_w = s_acc;
   float* s_l = s_acc + kNodeGroup * p.max_splits;
   const int nthr = blockDim.x;
   for (int gi = 0; gi < NG; ++gi) {
@@ -1083,7 +1085,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
       const unsigned long long* ws = slot(gnode0 + n, sp);
       const unsigned long long vm = load_word(ws + D), vl = load_word(ws + D + 1);
       bool ok = true;
-      const float m = settle_word(vm, ws + D, ok), l = settle_word(vl, ws + D + 1, ok);
+      const float m = settle_word(vm, ws + D, ok, p.merge_tag), l = settle_word(vl, ws + D + 1, ok, p.merge_tag);
       s_w[n * p.max_splits + sp] = m;
       s_l[n * p.max_splits + sp] = ok ? l : __builtin_nanf("");  // a NaN weight reaches the whole row
     }
@@ -1122,7 +1124,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
           for (int c = 0; c < SB; ++c) {
             if (e < nodes_here * D && s0 + c < nsplit) {
               bool ok = true;
-              const float x = settle_word(v[i][c], slot(gnode0 + n, s0 + c) + d, ok);
+              const float x = settle_word(v[i][c], slot(gnode0 + n, s0 + c) + d, ok, p.merge_tag);
               a[i] = fmaf(ok ? x : __builtin_nanf(""), s_w[n * p.max_splits + s0 + c], a[i]);
             }
           }
@@ -1171,6 +1173,14 @@ bool tree_mfma_path(int head_dim, int page_size, int quant_block) {
 }
 
 int tree_mfma_max_waves(int head_dim) { return tree_waves_cap_dp(head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256)); }
+
+// Splits per row that the in-launch merge can hold: it keeps a node group's (m, weight) and l per
+// split, 2 * 16 * max_splits floats, in the workgroup's accumulator buffer s_acc
+// (cap * 16 * (DP + 4) floats): 272 at head_dim 64, 528 at 128, 520 at 256.
+int tree_merge_max_splits(int head_dim) {
+  const int DP = head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256);
+  return tree_waves_cap_dp(DP) * (DP + 4) / 2;
+}
 
 // Most draft nodes one wave can serve: two 16-node groups (one K/V conversion for both) on the
 // 64-dim layout and on the 128-dim one with fp16 / bf16 queries and block parameters; 16
@@ -1357,6 +1367,10 @@ static int tree_verify(const void* q, int q_dtype, const int8_t* k_values, const
   if (merged && (!mq || draft_dtype != q_dtype))
     return set_error(FS_ERR_INVALID, "tree verify with a merge area needs the multi-query kernel and drafts in q's "
                                      "dtype");
+  if (merged && p.max_splits > tree_merge_max_splits(head_dim))
+    return set_error(FS_ERR_INVALID, "tree verify: the in-launch split merge takes at most " +
+                                         std::to_string(tree_merge_max_splits(head_dim)) + " splits at head_dim " +
+                                         std::to_string(head_dim));
   p.force_partials = 1;
   // drafts in q's dtype and one split (or a merge area): the multi-query kernel finishes the rows
   // itself; otherwise split partials go to the workspace for the tail kernel

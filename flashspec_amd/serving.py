@@ -292,6 +292,9 @@ class DecodeBatch:
         # for the batch's life).  Measured on MI355X, 64 ragged requests: 600 instead of 611 us.
         order = sorted(range(len(self._requests)), key=lambda i: -self.host_lengths[i])
         self._order = torch.tensor(order, dtype=torch.int32).to(self.device)
+        # appended tokens that found no page (a -1 table entry): counted on the device by the append
+        # kernels, checked at close() (the reference allocator raises instead, paged.py:89-90, 222-224)
+        self._dropped = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._open = True
 
     # -- bookkeeping ----------------------------------------------------------------------
@@ -387,7 +390,7 @@ class DecodeBatch:
             ks.zero_point.data_ptr(), vs.values.data_ptr(), vs.scale.data_ptr(), vs.zero_point.data_ptr(),
             int(ks.values.shape[0]), self.block_table.data_ptr(), 4, int(self.block_table.shape[1]),
             len_in.data_ptr(), len_out.data_ptr(), len(self._requests), self.allocator.heads,
-            self.allocator.head_dim, self.page, _lib.stream_ptr(k_c.device)))
+            self.allocator.head_dim, self.page, self._dropped.data_ptr(), _lib.stream_ptr(k_c.device)))
 
     def _append_portable(self, k_new, v_new) -> None:
         pos = torch.tensor(self.host_lengths, dtype=torch.int64)
@@ -487,7 +490,8 @@ class DecodeBatch:
             vs.zero_point.data_ptr(), self.block_table.data_ptr(), 4, int(self.block_table.shape[1]),
             self._lengths[self._cur].data_ptr(), self._lengths[nxt].data_ptr(), out.data_ptr(), _lib.ptr(workspace),
             ws_bytes, _lib.ptr(area), area_bytes, n, a.heads, a.head_dim, int(ks.values.shape[0]), self.page,
-            max_seq_len, 1.0 / math.sqrt(a.head_dim), split_tiles, max_splits, waves, _lib.stream_ptr(self.device)))
+            max_seq_len, 1.0 / math.sqrt(a.head_dim), split_tiles, max_splits, waves, self._dropped.data_ptr(),
+            _lib.stream_ptr(self.device)))
         self._cur = nxt
         self.steps_done += 1
         for i, r in enumerate(self._requests):
@@ -495,8 +499,17 @@ class DecodeBatch:
             r.length += 1
         return out
 
+    def dropped_tokens(self) -> int:
+        """Appended tokens that found no page (block table entry -1 or past the table) and were
+        dropped by the device append, since the batch opened (reads the device counter: a sync)."""
+
+        return int(self._dropped.item())
+
     def close(self) -> None:
-        """Return reserved pages that hold no token to the front of the free list, in taken order."""
+        """Return reserved pages that hold no token to the front of the free list, in taken order.
+
+        Raises RuntimeError afterwards if any appended token was dropped for want of a page (the
+        reference allocator raises when it has no page for a token, paged.py:89-90, 222-224)."""
 
         if not self._open:
             return
@@ -508,6 +521,9 @@ class DecodeBatch:
         unused_set = set(unused)
         self.allocator._free_blocks[:0] = [p for p in self._taken if p in unused_set]
         self._open = False
+        dropped = self.dropped_tokens()
+        if dropped:
+            raise RuntimeError(f"DecodeBatch: {dropped} appended token(s) found no page and were dropped")
 
 
 def build_request_pool(lengths: Sequence[int], *, heads: int, head_dim: int, block_size: int = 16,

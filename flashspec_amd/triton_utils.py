@@ -304,6 +304,14 @@ def tree_max_waves(head_dim: int) -> int:
     return 4 if head_dim > 128 else 8
 
 
+def tree_merge_max_splits(head_dim: int) -> int:
+    """Splits per row that the multi-query tree kernel's in-launch merge holds (its LDS accumulator
+    buffer keeps two floats per node and split): 272 at head_dim 64, 528 at 128, 520 at 256."""
+
+    dp = 64 if head_dim <= 64 else (128 if head_dim <= 128 else 256)
+    return tree_max_waves(head_dim) * (dp + 4) // 2
+
+
 def plan_tree_splits(seq_len: int, units: int, head_dim: int, cu_count: int) -> tuple[int, int, int]:
     """``(split_tiles, max_splits, waves_per_block)`` of the multi-query tree kernel.
 
@@ -325,6 +333,7 @@ def plan_tree_splits(seq_len: int, units: int, head_dim: int, cu_count: int) -> 
     else:
         n = max(1, (TREE_WG_PER_CU * cu_count) // max(1, units))
         n = min(n, max(1, tiles // (2 * waves)))
+    n = min(n, tree_merge_max_splits(head_dim))
     split_tiles = math.ceil(tiles / n)
     limit = MAX_TILES_PER_WAVE * waves
     if split_tiles > limit:

@@ -446,7 +446,10 @@ int fs_update_pages_i8(const int8_t* in_values, const float* in_scale, const int
  * that page's [heads] groups are dequantized (stale rows included), the row is replaced and
  * the page is requantized in place (quant block == page_size), for K and V in one launch.
  * lengths_out[b] = pos + 1, or pos when the table entry is -1 / out of range (the token is
- * then dropped and nothing is written).  lengths_in and lengths_out must differ; the caller
+ * then dropped and nothing is written).  `dropped` (NULL, or one unsigned of device memory the
+ * caller zeroes) counts the dropped tokens, one per request, with device atomics: the reference
+ * allocator raises instead of dropping (paged.py:89-90, 222-224), so a caller that must not lose
+ * tokens checks it.  lengths_in and lengths_out must differ; the caller
  * fills the table entry of a page before the step that first writes it.
  * Replaces PagedKVAllocator.append_batch for one token per request
  * (reference src/flashspec/paged.py:108-144, with page reads at :226-245 and writes at :247-255). */
@@ -455,14 +458,16 @@ int fs_append_tokens_i8(const void* k_new, const void* v_new, int src_dtype,
                         int8_t* v_values, float* v_scale, int16_t* v_zero, int64_t num_pages,
                         const void* block_table, int table_index_bytes, int table_cols,
                         const int64_t* lengths_in, int64_t* lengths_out,
-                        int batch, int heads, int head_dim, int page_size, void* stream);
+                        int batch, int heads, int head_dim, int page_size, unsigned* dropped,
+                        void* stream);
 
 /* One serving decode step in one launch: fs_append_tokens_i8 followed by paged decode attention
  * over the advanced lengths, with the append done inside the decode kernel.  For every request b,
  * the wave whose tile holds position pos = lengths_in[b] requantizes that page (the op sequence
  * and results of fs_append_tokens_i8, bit for bit) and attends over it from registers; every row
  * covers pos + 1 tokens.  lengths_out[b] = pos + 1, or pos when the page is not backed (table
- * entry -1 or out of range) or pos >= max_seq_len -- such a token is dropped and stays masked.
+ * entry -1 or out of range) or pos >= max_seq_len -- such a token is dropped, stays masked and
+ * counts into `dropped` (NULL or a caller-zeroed device unsigned, as for fs_append_tokens_i8).
  * Needs 16-token pages holding one quant block, head_dim 64 / 128 / 256, and k_new / v_new
  * ([batch, heads, 1, head_dim]) in q's dtype; max_seq_len must exceed every lengths_in[b] for
  * the token to be kept.  Rows that split merge through `merge_area` when it is given
@@ -478,7 +483,7 @@ int fs_paged_decode_append_i8(const void* q, int q_dtype, const void* k_new, con
                               void* merge_area, int64_t merge_area_bytes,
                               int batch, int heads, int head_dim, int64_t num_pages, int page_size,
                               int max_seq_len, float sm_scale, int split_tiles, int max_splits,
-                              int waves_per_block, void* stream);
+                              int waves_per_block, unsigned* dropped, void* stream);
 
 /* Measurement helper with no counterpart in the reference: one plain streaming read of
  * `bytes` (a positive multiple of 16, `src` 16-byte aligned) by `blocks` workgroups of 256

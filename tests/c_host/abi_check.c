@@ -14,7 +14,7 @@ static void check(int ok, const char* what) {
 }
 
 int main(void) {
-  check(fs_abi_version() == 1, "fs_abi_version() == 1");
+  check(fs_abi_version() == 2, "fs_abi_version() == 2");
   check(fs_decode_workspace_bytes(256, 16, 128) == (int64_t)256 * 16 * 130 * 4, "workspace bytes");
   check(fs_decode_tiled_path(128, 16, 16) == 1 && fs_decode_tiled_path(36, 16, 16) == 0, "tiled path query");
   check(fs_tree_mfma_path(128, 16, 16) == 1 && fs_tree_mfma_path(96, 16, 16) == 0, "tree path query");

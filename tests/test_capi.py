@@ -38,7 +38,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_abi_version_and_workspace_size():
     lib = _lib.require()
-    assert lib.fs_abi_version() == 1
+    assert lib.fs_abi_version() == 2
     assert lib.fs_decode_workspace_bytes(256, 16, 128) == 256 * 16 * 130 * 4
 
 
@@ -95,15 +95,15 @@ def test_invalid_arguments_are_rejected_before_launch():
     rc = lib.fs_update_pages_i8(1, 1, 1, 4, 8, 1, 1, 1, None, None, 4, 1, 1, 0, 1, 2, 16, 64, None)
     assert rc == _lib.FS_ERR_INVALID and "in-place" in lib.fs_last_error().decode()
     # append: the two lengths buffers must differ, and the table index width is 4 or 8 bytes
-    rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 4, 7, 7, 2, 2, 64, 16, None)
+    rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 4, 7, 7, 2, 2, 64, 16, None, None)
     assert rc == _lib.FS_ERR_INVALID and "differ" in lib.fs_last_error().decode()
-    rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 2, 4, 7, 9, 2, 2, 64, 16, None)
+    rc = lib.fs_append_tokens_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 1, 2, 4, 7, 9, 2, 2, 64, 16, None, None)
     assert rc == _lib.FS_ERR_INVALID and "int32 or int64" in lib.fs_last_error().decode()
     # fused append + decode: 16-token pages, head_dim 64 / 128 / 256, two lengths buffers
 
     def fused(page, D, lens_in, lens_out):
         return lib.fs_paged_decode_append_i8(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, lens_in, lens_out, 1, None, 0,
-                                             None, 0, 2, 2, D, 8, page, 64, 0.1, 4, 1, 1, None)
+                                             None, 0, 2, 2, D, 8, page, 64, 0.1, 4, 1, 1, None, None)
 
     assert fused(32, 128, 7, 9) == _lib.FS_ERR_INVALID and "16-token pages" in lib.fs_last_error().decode()
     assert fused(16, 96, 7, 9) == _lib.FS_ERR_INVALID and "64, 128 or 256" in lib.fs_last_error().decode()
@@ -117,13 +117,21 @@ def test_invalid_arguments_are_rejected_before_launch():
     # the multi-query kernel's shapes
     tree = lib.fs_tree_verify_merged
 
-    def merged(kv_format=0, npw=0, head_dim=128):
-        return tree(1, 1, kv_format, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 1, 1, 1, None, 0, 2, 4, 2, head_dim, 8, 16, 16,
-                    64, 0.1, 4, 1, 8, npw, None)
+    def merged(kv_format=0, npw=0, head_dim=128, max_splits=1, area=None, area_bytes=0):
+        return tree(1, 1, kv_format, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 1, 1, 1, area, area_bytes, 2, 4, 2, head_dim, 8,
+                    16, 16, 64, 0.1, 4, max_splits, 8, npw, None)
 
     assert merged(kv_format=2) == _lib.FS_ERR_INVALID and "kv_format" in lib.fs_last_error().decode()
     assert merged(npw=8) == _lib.FS_ERR_INVALID and "nodes_per_workgroup" in lib.fs_last_error().decode()
     assert merged(head_dim=96) == _lib.FS_ERR_INVALID and "multi-query" in lib.fs_last_error().decode()
+    # the in-launch merge keeps 2 floats per node and split in its LDS accumulator buffer: at most
+    # 272 splits at head_dim 64 (a 256-aligned stand-in address; rejected before any HIP call)
+    assert merged(npw=16, head_dim=64, max_splits=273, area=256, area_bytes=1 << 40) == _lib.FS_ERR_INVALID
+    assert "at most 272 splits" in lib.fs_last_error().decode()
+    from flashspec_amd.triton_utils import plan_tree_splits, tree_merge_max_splits
+
+    assert [tree_merge_max_splits(d) for d in (64, 128, 256)] == [272, 528, 520]
+    assert plan_tree_splits(1 << 20, 1, 64, 1 << 12)[1] <= 272
 
 
 def test_no_alloc_entry_point_rejects_plans_beyond_its_array():

@@ -218,15 +218,16 @@ def _append_then_decode_reference(cache, kn, vn, lens_in, plan):
     ks, vs = cache.k_quant, cache.v_quant
     B, H, _, D = kn.shape
     lens_out = torch.empty_like(lens_in)
+    dropped = torch.zeros(1, dtype=torch.int32, device=DEV)
     table = cache.block_table
     _lib.check(lib.fs_append_tokens_i8(
         kn.data_ptr(), vn.data_ptr(), _lib.dtype_code(kn.dtype), ks.values.data_ptr(), ks.scale.data_ptr(),
         ks.zero_point.data_ptr(), vs.values.data_ptr(), vs.scale.data_ptr(), vs.zero_point.data_ptr(),
         int(ks.values.shape[0]), table.data_ptr(), table.element_size(), int(table.shape[1]), lens_in.data_ptr(),
-        lens_out.data_ptr(), B, H, D, cache.block_size, _lib.stream_ptr(DEV)))
+        lens_out.data_ptr(), B, H, D, cache.block_size, dropped.data_ptr(), _lib.stream_ptr(DEV)))
     after = fa.PagedKVCache(k_quant=ks, v_quant=vs, block_table=table, lengths=lens_out, block_size=cache.block_size,
                             max_seq_len=plan["max_seq_len"])
-    return lens_out, after
+    return lens_out, after, int(dropped.item())
 
 
 def _fused_append_decode(cache, q, kn, vn, lens_in, plan):
@@ -246,6 +247,7 @@ def _fused_append_decode(cache, q, kn, vn, lens_in, plan):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
     out = torch.empty_like(q)
     lens_out = torch.full_like(lens_in, -7)
+    dropped = torch.zeros(1, dtype=torch.int32, device=DEV)
     table = cache.block_table
     _lib.check(lib.fs_paged_decode_append_i8(
         q.data_ptr(), _lib.dtype_code(q.dtype), kn.data_ptr(), vn.data_ptr(), ks.values.data_ptr(),
@@ -253,8 +255,8 @@ def _fused_append_decode(cache, q, kn, vn, lens_in, plan):
         vs.zero_point.data_ptr(), table.data_ptr(), table.element_size(), int(table.shape[1]), lens_in.data_ptr(),
         lens_out.data_ptr(), out.data_ptr(), _lib.ptr(ws), ws_bytes, _lib.ptr(area), area_bytes, B, H, D,
         int(ks.values.shape[0]), cache.block_size, plan["max_seq_len"], 1.0 / float(D) ** 0.5, split_tiles,
-        max_splits, waves, _lib.stream_ptr(DEV)))
-    return out, lens_out, max_splits, waves
+        max_splits, waves, dropped.data_ptr(), _lib.stream_ptr(DEV)))
+    return out, lens_out, max_splits, waves, split_tiles, int(dropped.item())
 
 
 def _clone_cache(cache):
@@ -266,18 +268,22 @@ def _clone_cache(cache):
                            lengths=cache.lengths.clone(), block_size=cache.block_size, max_seq_len=cache.max_seq_len)
 
 
-@pytest.mark.parametrize("H,D,qdt,splits,warps", [
-    (8, 128, torch.float16, None, None),      # few rows: splits merged in-kernel
-    (8, 128, torch.float16, "3", "16"),       # 16-wave splits: workspace + merge launch
-    (32, 128, torch.float16, None, None),     # one split per row
-    (8, 64, torch.bfloat16, None, None),
-    (4, 256, torch.float32, "2", None),
+@pytest.mark.parametrize("H,D,qdt,splits,warps,drop", [
+    (8, 128, torch.float16, None, None, 250),      # few rows: splits merged in-kernel
+    (8, 128, torch.float16, "3", "16", 250),       # 16-wave splits: workspace + merge launch
+    # the dropped token's position on a split boundary (15 tiles per split): the decode counts its
+    # masked tile as a second split, and the merge launch must count it too
+    (8, 128, torch.float16, "3", "16", 240),
+    (8, 128, torch.float16, "3", None, 240),       # the same boundary, merged in-kernel
+    (32, 128, torch.float16, None, None, 250),     # one split per row
+    (8, 64, torch.bfloat16, None, None, 250),
+    (4, 256, torch.float32, "2", None, 250),
 ])
-def test_fused_append_decode_bit_identical_to_append_then_decode(monkeypatch, H, D, qdt, splits, warps):
+def test_fused_append_decode_bit_identical_to_append_then_decode(monkeypatch, H, D, qdt, splits, warps, drop):
     """fs_paged_decode_append_i8 against fs_append_tokens_i8 + paged decode on a copy of the same
     store: pages, scales, zero points, advanced lengths and outputs bit-identical.  Positions: a
     page's first row (64), its last row (399), mid-page rows (37, 1), the last, part-padded page
-    (699), a table entry of -1 at the position (250: token dropped, length kept) and a position
+    (699), a table entry of -1 at the position (`drop`: token dropped, length kept) and a position
     past the table and max_seq_len (710: likewise)."""
 
     if splits:
@@ -285,13 +291,13 @@ def test_fused_append_decode_bit_identical_to_append_then_decode(monkeypatch, H,
     if warps:
         monkeypatch.setenv("FLASHSPEC_NUM_WARPS", warps)
     B, S, bs, max_seq = 7, 700, 16, 704
-    announce(f"fused append+decode B{B} H{H} D{D} S{S} q {qdt} splits {splits} warps {warps}")
+    announce(f"fused append+decode B{B} H{H} D{D} S{S} q {qdt} splits {splits} warps {warps} drop {drop}")
     k, v = randn((B, H, S, D), 71), randn((B, H, S, D), 72)
     cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=bs, block_table_pattern="shuffled",
                                        layout_seed=3)
-    pos = [64, 399, 37, 250, 1, 699, 710]
+    pos = [64, 399, 37, drop, 1, 699, 710]
     table = cache.block_table.clone()
-    table[3, 250 // bs] = -1
+    table[3, drop // bs] = -1
     cache = fa.PagedKVCache(k_quant=cache.k_quant, v_quant=cache.v_quant, block_table=table,
                             lengths=cache.lengths, block_size=bs, max_seq_len=cache.max_seq_len)
     lens_in = torch.tensor(pos, dtype=torch.int64, device=DEV)
@@ -299,12 +305,17 @@ def test_fused_append_decode_bit_identical_to_append_then_decode(monkeypatch, H,
     q = randn((B, H, D), 73, qdt).to(DEV)
     kn, vn = randn((B, H, 1, D), 74, qdt).to(DEV), randn((B, H, 1, D), 75, qdt).to(DEV)
     ref_cache = _clone_cache(cache)
-    lens_ref, after = _append_then_decode_reference(ref_cache, kn, vn, lens_in, plan)
+    lens_ref, after, dropped_ref = _append_then_decode_reference(ref_cache, kn, vn, lens_in, plan)
     ref = fa.paged_quant_attention_triton(q, after)
-    out, lens_out, max_splits, waves = _fused_append_decode(cache, q, kn, vn, lens_in, plan)
+    out, lens_out, max_splits, waves, split_tiles, dropped = _fused_append_decode(cache, q, kn, vn, lens_in, plan)
     torch.cuda.synchronize(DEV)
-    announce(f"plan: {max_splits} splits x {waves} waves")
-    assert lens_out.tolist() == lens_ref.tolist() == [65, 400, 38, 250, 2, 700, 710]
+    announce(f"plan: {max_splits} splits x {waves} waves, {split_tiles} tiles per split")
+    if drop == 240:
+        assert drop == 16 * split_tiles and max_splits > 1
+    assert lens_out.tolist() == lens_ref.tolist() == [65, 400, 38, drop, 2, 700, 710]
+    # the two dropped tokens (the -1 entry at `drop`, and 710 past the table / max_seq_len), counted
+    # once per request by either path
+    assert dropped == dropped_ref == 2
     for ours, theirs, name in ((cache.k_quant, ref_cache.k_quant, "K"), (cache.v_quant, ref_cache.v_quant, "V")):
         assert torch.equal(ours.values, theirs.values), f"{name} values"
         assert torch.equal(ours.scale.view(torch.int32), theirs.scale.view(torch.int32)), f"{name} scales"
@@ -356,3 +367,33 @@ def test_decode_batch_dispatches_longest_first():
     q = randn((4, 4, 128), 90).to(DEV)
     assert torch.equal(batch.attend(q), fa.paged_quant_attention_triton(q, alloc.to_cache(rids)))
     batch.close()
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_decode_batch_close_raises_when_a_token_was_dropped(fused):
+    """A token whose page entry is -1 on the device is dropped by the append (one-launch step or
+    append + attend), counted on the device, and close() raises the reference allocator's
+    RuntimeError after restoring the free list (reference paged.py:89-90, 222-224)."""
+
+    announce(f"decode batch dropped-token count, fused step {fused}")
+    alloc, rids = build_request_pool([48, 70], heads=4, head_dim=128, headroom_tokens=16, seed=5, device=DEV)
+    batch = DecodeBatch(alloc, rids, max_new_tokens=3)
+    q = randn((2, 4, 128), 91).to(DEV)
+    kn, vn = randn((2, 4, 1, 128), 92).to(DEV), randn((2, 4, 1, 128), 93).to(DEV)
+    batch.step(q, kn, vn)  # every token finds its page
+    assert batch.dropped_tokens() == 0
+    pos = batch.host_lengths[0]  # 49: request 0's next token goes to page 3, row 1
+    batch.block_table[0, pos // batch.page] = -1
+    if fused:
+        batch.step(q, kn, vn)
+    else:
+        batch.append(kn, vn)
+        batch.attend(q)
+    torch.cuda.synchronize(DEV)
+    assert batch.dropped_tokens() == 1
+    assert batch.lengths.cpu().tolist() == [pos, batch.host_lengths[1]]  # request 0 kept its length
+    with pytest.raises(RuntimeError, match="dropped"):
+        batch.close()
+    assert not batch._open
+    owned = [p for r in rids for p in alloc._get_request(r).logical_blocks]
+    assert sorted(alloc._free_blocks + owned) == list(range(alloc.capacity_blocks))  # nothing lost or doubled
