@@ -280,8 +280,10 @@ SERVE_B, SERVE_LO, SERVE_HI = 64, 128, 16384
 def serving_step_bench(torch, fa, dev, steps: int, warmup: int) -> dict:
     """Serving decode step at scale: 64 requests, lengths ~ U[128, 16384] (seeded CPU draw),
     fragmented shuffled page pool, one fp16 token appended per request per step and paged
-    attention over the updated cache: ``DecodeBatch.step``, device-resident table and lengths,
-    one launch with the append inside the decode kernel."""
+    attention over the updated cache: ``DecodeBatch.step``, device-resident table and lengths.
+    At this size (2048 rows, several rounds of workgroups per CU) the step is two launches, the
+    append kernel and then the decode (requests dispatched longest first); the one-launch form,
+    with the append inside the decode kernel, serves grids of one round of workgroups."""
 
     from flashspec_amd.serving import DecodeBatch, build_request_pool
 
@@ -367,6 +369,82 @@ def quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
             "copy_ceiling": {"kernel": "stream_copy_half_kernel", "bytes": copy_bytes, "us": round(best[0] * 1e3, 2),
                              "gbps": round(copy_gbps, 1), "workgroups": best[1]},
             "frac_of_copy_ceiling": round(gbps / copy_gbps, 4)}
+
+
+def page_quantize_bench(torch, fa, dev, calls: int = 30) -> dict:
+    """``PagedKVCache.from_dense``'s page quantizer (``fs_quantize_pages_i8``, one launch per tensor)
+    on one fp16 K tensor of the metric workload ([8, 32, 4096, 128] into 2048 16-token pages), in the
+    contiguous and the shuffled page order, input resident in HBM and rotated over two tensors;
+    bytes = fp16 read + int8 write + scale/zero write.  Beside it the same 2:1 copy ceiling as the
+    blocks quantizer's (`fs_stream_copy_half` over the same tensor, best grid)."""
+
+    from flashspec_amd import _lib
+
+    lib = _lib.require()
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    xs = [torch.randn((B, H, S, D), generator=g, device=dev, dtype=torch.float16) for _ in range(2)]
+    pages = B * (S // PAGE)
+    values = torch.empty((pages, H, 1, PAGE, D), dtype=torch.int8, device=dev)
+    scale = torch.empty((pages, H, 1, 1, 1), dtype=torch.float32, device=dev)
+    zero = torch.empty((pages, H, 1, 1, 1), dtype=torch.int16, device=dev)
+    stream = _lib.stream_ptr(dev)
+    gp = torch.Generator(device=dev)
+    gp.manual_seed(0)
+    perm = torch.randperm(pages, generator=gp, device=dev)
+    nbytes = B * H * S * D * (2 + 1) + pages * H * 6
+    out = {"workload": f"fs_quantize_pages_i8 fp16 [{B}, {H}, {S}, {D}] -> {pages} pages of {PAGE} tokens",
+           "algorithmic_bytes": nbytes}
+    for name, src in (("contiguous", None), ("shuffled", perm)):
+        def call(i, src=src):
+            _lib.check(lib.fs_quantize_pages_i8(
+                xs[i % 2].data_ptr(), 1, B, H, S, D, PAGE, _lib.ptr(src), pages, values.data_ptr(),
+                scale.data_ptr(), zero.data_ptr(), stream))
+        ms = time_loop(torch, call, calls, 3)
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us_per_call": round(ms * 1e3, 2), "gbps": round(gbps, 1),
+                     "pct_of_peak": round(100 * gbps / PEAK_GBPS, 1)}
+    dst = torch.empty(B * H * S * D, dtype=torch.int8, device=dev)
+    src_bytes = xs[0].numel() * 2
+    best = None
+    for blocks in (2048, 4096, 8192):
+        cms = time_loop(torch, lambda i: _lib.check(lib.fs_stream_copy_half(
+            xs[i % 2].data_ptr(), src_bytes, dst.data_ptr(), blocks, stream)), calls, 3)
+        if best is None or cms < best[0]:
+            best = (cms, blocks)
+    copy_gbps = (src_bytes + src_bytes // 2) / (best[0] * 1e-3) / 1e9
+    out["copy_ceiling"] = {"kernel": "stream_copy_half_kernel", "us": round(best[0] * 1e3, 2),
+                           "gbps": round(copy_gbps, 1), "workgroups": best[1]}
+    for name in ("contiguous", "shuffled"):
+        out[name]["frac_of_copy_ceiling"] = round(out[name]["gbps"] / copy_gbps, 4)
+    del xs, dst, values, scale, zero
+    return out
+
+
+def c2_configured_bench(torch, fa, sets, steps: int, warmup: int, fused_ms: float, nbytes: int) -> dict:
+    """BASELINE config 2 as configured: the contiguous (fused) decode B8 H32 S4096 D128 with
+    FLASHSPEC_NUM_SPLITS=4 (the reference's own published point, triton_fused split 4), over the
+    metric's rotated input sets, beside the planner's plan on the same data (`fused_ms`)."""
+
+    old = os.environ.get("FLASHSPEC_NUM_SPLITS")
+    os.environ["FLASHSPEC_NUM_SPLITS"] = "4"
+    try:
+        def step(i):
+            q, _, kq, vq = sets[i % ROTATE]
+            return fa.fused_dequant_attention_triton(q, kq, vq)
+
+        _, st = fa.fused_dequant_attention_triton(sets[0][0], sets[0][2], sets[0][3], return_stats=True)
+        ms = time_loop(torch, step, steps, warmup)
+    finally:
+        if old is None:
+            del os.environ["FLASHSPEC_NUM_SPLITS"]
+        else:
+            os.environ["FLASHSPEC_NUM_SPLITS"] = old
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": f"fused INT8 decode B{B} H{H} S{S} D{D}, FLASHSPEC_NUM_SPLITS=4, {ROTATE} rotated sets",
+            "us_per_step": round(ms * 1e3, 2), "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 1),
+            "num_splits": st.get("num_splits"), "waves_per_workgroup": st.get("num_warps"),
+            "planner_us_per_step": round(fused_ms * 1e3, 2), "vs_planner": round(ms / fused_ms, 4)}
 
 
 # Shapes beyond the metric workload: (name, batch, heads, seq, head_dim, page, quant block, q dtype, lengths
@@ -687,6 +765,12 @@ def main() -> int:
         },
         "device": torch.cuda.get_device_name(dev),
     }
+    try:
+        # contiguous rows: no block table, no lengths (269,352,960 bytes)
+        result["c2_configured"] = c2_configured_bench(torch, fa, sets, args.steps, min(args.warmup, 300), fused_ms,
+                                                      algorithmic_bytes(lengths, H, D, PAGE, idx_bytes=0) - 8 * B)
+    except Exception as exc:  # reported, never hides the metric line
+        result["c2_configured"] = {"error": f"{type(exc).__name__}: {exc}"}
     del sets
     torch.cuda.empty_cache()
     try:
@@ -700,6 +784,11 @@ def main() -> int:
         result["quantize"] = quantize_bench(torch, fa, dev)
     except Exception as exc:  # reported, never hides the metric line
         result["quantize"] = {"error": f"{type(exc).__name__}: {exc}"}
+    torch.cuda.empty_cache()
+    try:
+        result["page_quantize"] = page_quantize_bench(torch, fa, dev)
+    except Exception as exc:  # reported, never hides the metric line
+        result["page_quantize"] = {"error": f"{type(exc).__name__}: {exc}"}
     torch.cuda.empty_cache()
     try:
         result["serving_step"] = serving_step_bench(torch, fa, dev, steps=min(args.steps, 50), warmup=5)

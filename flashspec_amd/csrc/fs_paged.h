@@ -211,6 +211,9 @@ __device__ __forceinline__ TileIndex sub_index(const DecodeParams& p, int b, int
     const int64_t ph = pg * p.heads + h;
     return {(int)(ph * (p.page_size / 8) + within / 8), (int)(ph * (p.page_size / p.quant_block) + within / p.quant_block)};
   } else {
+    // the row's store holds n_blocks * quant_block tokens: an odd number of 8-token halves leaves the
+    // last tile's second half past it (not backed; without this it would read past the store's end)
+    if (token0 >= p.n_blocks * p.quant_block) return {-1, 0};
     return {row * p.n_blocks * (p.quant_block / 8) + u, row * p.n_blocks + token0 / p.quant_block};
   }
 }

@@ -6,14 +6,17 @@ reference's own design calls for: attention goes through
 ``paged_quant_attention_triton`` (the HIP kernel on GPU, the portable path on CPU)
 instead of the portable path only (serving.py:118,139 call ``paged_quant_attention``).
 On GPU the prompt writes run as batched HIP page-update launches, and the decode loop
-keeps the block table and lengths on the device (``DecodeBatch``): one attention launch
-and one append launch per step (the reference's order: attend, then append what the
-attention produced), no per-step table rebuild on the host.
+keeps the block table and lengths on the device (``DecodeBatch``): per step one attention
+launch (``DecodeBatch.attend``) and then one append launch (``DecodeBatch.append``) -- the
+reference's order: attend, then append what the attention produced -- with no per-step
+table rebuild on the host.
 
 ``build_request_pool`` and ``DecodeBatch.step`` are the serving-at-scale pieces: a
-fragmented page pool of ragged requests, and one decode step that appends one token
-per request and then attends over the updated cache -- one launch, with the append
-inside the decode kernel.
+fragmented page pool of ragged requests, and a decode step in the other, standard order --
+append the step's token (its K/V known beforehand) for every request, then attend over the
+updated cache.  ``step`` is one launch, with the append inside the decode kernel, where the
+decode grid is one round of workgroups (e.g. 4 requests x 32 heads); larger batches (the
+64-request bench workload) take the append launch and then the decode.
 
     python -m flashspec_amd.serving --requests 8 --prompt-lens 512,2048 --decode-steps 16 --json
 """

@@ -472,8 +472,11 @@ int fs_append_tokens_i8(const void* k_new, const void* v_new, int src_dtype,
  * ([batch, heads, 1, head_dim]) in q's dtype; max_seq_len must exceed every lengths_in[b] for
  * the token to be kept.  Rows that split merge through `merge_area` when it is given
  * (fs_paged_decode_merged's contract), else through `workspace` and a merge launch made here.
- * Replaces the serving step's PagedKVAllocator.append_batch + paged attention pair
- * (reference src/flashspec/paged.py:108-144 and serving.py:126-163). */
+ * The op order is append-then-attend (standard decode: the new token's K/V are known before
+ * its attention), the order of DecodeBatch.step; the reference's serving loop attends first and
+ * appends K/V made from the attention output (serving.py:126-163), which a caller gets from the
+ * paged decode followed by fs_append_tokens_i8.  Replaces the PagedKVAllocator.append_batch +
+ * paged attention pair of a decode step (reference src/flashspec/paged.py:108-144). */
 int fs_paged_decode_append_i8(const void* q, int q_dtype, const void* k_new, const void* v_new,
                               int8_t* k_values, float* k_scale, int16_t* k_zero,
                               int8_t* v_values, float* v_scale, int16_t* v_zero,

@@ -14,7 +14,14 @@ import subprocess
 import sys
 from pathlib import Path
 
+import numpy as np
 import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import paged as op
+from oracle import quant as oq
+from tests._helpers import assert_attention_close
 
 pytestmark = pytest.mark.gpu
 
@@ -74,19 +81,39 @@ def test_microbench_triton_fused_backend_c1():
     data = _microbench("--backend", "triton_fused", "--batch", "4", "--heads", "32", "--seq-len", "2048",
                        "--head-dim", "128", "--iters", "20", "--warmup", "5", "--repeats", "5")
     _check_hip_result(data, "triton_fused", 4, 2048)
+    # the graph-captured latency (no per-call host work) beside the eager one
+    assert math.isfinite(data["graph_latency_ms"]) and 0 < data["graph_latency_ms"] < 1.0
+    print(f"C1 eager {data['latency_ms'] * 1e3:.2f} us, graph {data['graph_latency_ms'] * 1e3:.2f} us", flush=True)
 
 
-def test_microbench_paged_and_fused_agree_with_the_portable_backends():
-    """Same seeded inputs, same checksum to fp16 accuracy: the HIP backends against the reference's
-    PyTorch paths (the CLI's ``paged`` / ``fused`` backends on the same device)."""
+@pytest.mark.parametrize("backend", ["triton_paged", "triton_fused"])
+def test_microbench_hip_output_matches_the_oracle(backend, tmp_path):
+    """The CLI's HIP backends, element-wise against the CPU oracle on the same seeded inputs
+    (descending lengths, B2 H4 S300 D64): the child process saves its output (--save-output), this
+    process draws the same q, k, v from the same seeded device generator (microbench.py's draw
+    order) and runs the oracle's quantizer and attention on them."""
 
-    common = ("--batch", "2", "--heads", "4", "--seq-len", "300", "--head-dim", "64", "--iters", "1", "--warmup",
-              "0", "--repeats", "1", "--length-pattern", "descending")
-    for hip, portable in (("triton_paged", "paged"), ("triton_fused", "fused")):
-        a = _microbench("--backend", hip, *common)
-        b = _microbench("--backend", portable, *common)
-        assert a["materializes_dense_kv"] is False and b["materializes_dense_kv"] is True
-        assert abs(a["output_checksum"] - b["output_checksum"]) <= 2e-3 * 2 * 4 * 64
+    path = tmp_path / "out.npy"
+    data = _microbench("--backend", backend, "--batch", "2", "--heads", "4", "--seq-len", "300", "--head-dim", "64",
+                       "--iters", "2", "--warmup", "1", "--repeats", "2", "--length-pattern", "descending",
+                       "--save-output", str(path))
+    assert data["materializes_dense_kv"] is False
+    assert data["graph_latency_ms"] > 0
+    out = np.load(path, allow_pickle=False)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    q = torch.randn((2, 4, 64), generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn((2, 4, 300, 64), generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn((2, 4, 300, 64), generator=g, device=dev, dtype=torch.float16)
+    lengths = np.array(data["effective_lengths"], dtype=np.int64)
+    kf, vf, qf = (t.float().cpu().numpy() for t in (k, v, q))
+    if backend == "triton_paged":
+        ref = oa.paged_quant_attention(qf, op.from_dense(kf, vf, 16, lengths=lengths))
+    else:
+        ref = oa.fused_dequant_attention(qf, oq.quantize_int8_per_block(kf, 16), oq.quantize_int8_per_block(vf, 16),
+                                         lengths)
+    assert_attention_close(torch.from_numpy(out).to(torch.float16), ref, torch.float16, backend)
 
 
 @pytest.mark.timeout(600)
