@@ -807,18 +807,6 @@ struct StartWords {
 };
 constexpr int kLog2None = 31;
 
-// Rotation of a wave's tile order for a row of request b (nk tiles): the wave takes its first tile
-// (the one contiguous rows load before the row length is known), then its others from position
-// 1 + (b mod (nk - 1)) on, wrapping around.  All requests walking their tiles in step would have
-// the whole GPU read, at any moment, one page of each request; in the contiguous page layout those
-// pages sit a fixed power-of-two stride apart (one request's pages apart), and on some physical
-// placements such a set falls on few HBM channels: measured on one MI355X, 2 of 8 identical
-// metric-shape caches then read 43.4 us against 40.5-40.8 us for the others, reproducibly, while
-// shuffled pages (41.9 us) and contiguous rows (40.0-40.7 us) did not vary; with the rotation all
-// eight read 40.9-41.7 us.  The rotation depends on the request alone and applies to every layout
-// (contiguous rows included), so a row gives bit-identical results in any layout.
-__device__ __forceinline__ int tile_rotation(int b, int nk) { return nk > 2 ? b % (nk - 1) : 0; }
-
 template <int DP, typename QT, bool PAGED, int QM, int VF>
 __global__ void __launch_bounds__(kWave * max_tiled_waves(DP, QM))
 decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int32_t* w3, uint64_t w4, uint64_t w5,
@@ -1012,7 +1000,7 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   if (lane >= nk || my_tile >= tile_end) my_base = my_base1 = -1;
   // The wave takes its first tile, then the others from position 1 + rot on, wrapping around
   // (whole blocks in CHB order)
-  const int rot = CHB ? 0 : tile_rotation(b, nk);
+  const int rot = CHB ? 0 : tile_rotation(b, split, nk);
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
   if constexpr (!SPEC) load_params();
   auto convert_params = [&]() {
@@ -1088,10 +1076,7 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   const int8_t* kbase = p.kv[0];
   const int8_t* vbase = p.kv[1];
   // the wave's k-th tile in its order (k >= nk: none)
-  auto seq = [&](int k) {
-    const int kk = k + rot;
-    return k == 0 || k >= nk ? k : (kk >= nk ? kk - (nk - 1) : kk);
-  };
+  auto seq = [&](int k) { return tile_in_order(k, rot, nk); };
   auto base_of = [&](int k) { return k < nk ? readlane_i32(my_base, k) : -1; };
   auto base1_of = [&](int k) { return k < nk ? readlane_i32(my_base1, k) : -1; };
   // stored tokens from a tile's first token to the end of its contiguous run (token mode)
