@@ -515,13 +515,15 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   };
   // An unbacked tile loads tile 0 of the store (L2 hits) and is masked: a branch around the
   // loads would make the compiler keep the registers in scratch memory.
-  // Where one node group covers the tree, the wave takes its tiles in the decode kernel's rotated
-  // order (tile_rotation): the k-th is tile first + W * tile_in_order(k, rot, nk).  Measured (A/B,
-  // one box): B8 x 16 nodes 49.9 -> 49.2 us; with several node groups per (request, head) it cost
-  // 0.6 us at 64 nodes and 3.6 us with FP8 stores, so those keep the plain order.
-  const int rot = groups == 1 ? tile_rotation(b, split, nk) : 0;
+  // Where one 16-node group covers the tree, the wave takes its tiles in the decode kernel's
+  // rotated order (tile_rotation): the k-th is tile first + W * tile_in_order(k, rot, nk).
+  // Measured (A/B, one box): B8 x 16 nodes 49.9 -> 49.2 us; with several node groups per (request,
+  // head) it cost 0.6 us at 64 nodes, and in the two-group waves its registers made the FP8 layout
+  // spill, so those keep the plain order.
+  constexpr bool kRotate = NG == 1;
+  const int rot = kRotate && groups == 1 ? tile_rotation(b, split, nk) : 0;
   auto load = [&](MqTile<DP, TOK>& t, int k) {
-    k = tile_in_order(k, rot, nk);
+    if constexpr (kRotate) k = tile_in_order(k, rot, nk);
     const int64_t o = k < nk ? off_of(k) : -1;
     const size_t to = o < 0 ? 0 : (size_t)o;
     const int8_t* kp = kbase + to + (size_t)nl * D;
@@ -562,7 +564,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   // With block parameters each score is one FMA, S * (ks * qmul) + (-(1024 + zk) * ks) *
   // (sum(q) * qmul), whose addend is -inf for a masked token.
   auto scores = [&](const MqTile<DP, TOK>& t, int k, float (&sc)[NG][4], float (&vfac)[4], f16x4_t& nzv) {
-    k = tile_in_order(k, rot, nk);
+    if constexpr (kRotate) k = tile_in_order(k, rot, nk);
     const bool backed = k < nk && off_of(k) >= 0;
     const int token0 = (first + W * k) * kTile + 4 * g;
     float ksc[4], kzo[4];
