@@ -201,3 +201,36 @@ def test_graph_replay_with_split_merge(monkeypatch):
         torch.cuda.synchronize(DEV)
         assert torch.equal(out, eager), f"replay {i}"
         assert torch.equal(again, eager), f"eager after replay {i}"
+
+
+def test_stale_merge_words_from_earlier_launches_are_not_taken(monkeypatch):
+    """Every word of the merge area planted with a stale tag and a value far off the result: the
+    next split decode reads past them (each launch tags its words with a fresh value; a plain
+    tag of 1 is what every word carried before per-launch tags), overwrites and clears them, and
+    gives the same bits as before the planting."""
+
+    import struct
+
+    monkeypatch.setenv("FLASHSPEC_NUM_SPLITS", "4")
+    B, H, D = 2, 8, 128
+    q, cache = _paged(B, H, 1000, D, 24, [1000, 777])
+    qd = q.to(DEV)
+    first, st = fa.paged_quant_attention_triton(qd, cache, return_stats=True)
+    assert st["num_splits"] == 4.0 and st["num_warps"] <= triton_utils.MERGE_MAX_WAVES  # in-launch merge
+    assert _area_is_zero()
+    area = triton_utils._MERGE_AREAS[(DEV.index, _lib.stream_ptr(DEV))]
+    rows, splits = B * H, int(st["num_splits"])
+    counts = (rows * 4 + 255) // 256 * 256
+    slots = area[counts:counts + rows * splits * (D + 2) * 8].view(torch.int64)
+    stale = (1 << 32) | struct.unpack("<I", struct.pack("<f", 1e30))[0]
+    try:
+        announce("stale tagged words in the merge area")
+        slots.fill_(stale)
+        torch.cuda.synchronize(DEV)
+        again = fa.paged_quant_attention_triton(qd, cache)
+        assert _area_is_zero(), "the launch left planted words behind"
+        assert torch.equal(again, first)
+        assert_attention_close(again, oracle_paged_attention(q, cache), torch.float16, "after stale words")
+    finally:
+        area.zero_()
+        torch.cuda.synchronize(DEV)
