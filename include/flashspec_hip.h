@@ -259,9 +259,11 @@ int fs_tree_verify_i8_channel(const void* q, int q_dtype,
  * area per stream), and the last split of each (request, head, node group) merges them and
  * finishes the rows (path tokens, output) -- no workspace and no tail launch.  kv_format 0 =
  * affine INT8 per block or token, 1 = FP8 E4M3 (zero arrays unused); drafts in q's dtype;
- * nodes_per_workgroup 0 (the library's choice), 16 or 32.  Other arguments as for
- * fs_tree_verify_i8.  No counterpart in the reference (its Kernel 3 is planned only,
- * doc/TODO.MD:186-237).
+ * nodes_per_workgroup 0 (the library's choice), 16 or 32.  The in-launch merge holds at most
+ * 272 splits per row at head_dim 64, 528 at 128 and 520 at 256 (two floats per node and split
+ * in the workgroup's LDS accumulator); larger max_splits with max_splits > 1 are rejected
+ * (FS_ERR_INVALID).  Other arguments as for fs_tree_verify_i8.  No counterpart in the reference
+ * (its Kernel 3 is planned only, doc/TODO.MD:186-237).
  */
 int fs_tree_verify_merged(const void* q, int q_dtype, int kv_format,
                           const void* k_values, const float* k_scale, const int16_t* k_zero,
