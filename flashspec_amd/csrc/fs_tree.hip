@@ -842,10 +842,11 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   // Waves w and w ^ 4 of an 8-wave workgroup share a SIMD, where the older one wins every tie
   // for issue: measured, waves 0-3 finished their tiles 25-40% before waves 4-7, which then ran
   // alone.  With p.pace_waves (grids of more workgroups than CUs, where a CU takes its next
-  // workgroup only once the slowest wave is done) each wave posts its progress in LDS and lowers
-  // its priority while it is ahead of its partner: a scheduling hint only, the work and its order
-  // stay fixed.  Measured at B8 x 64 nodes (two workgroups per CU in turn) 137 -> 133.6 us; with
-  // one workgroup per CU it cost 0.6-0.8 us.
+  // workgroup only once the slowest wave is done, and two-group waves) each wave posts its progress
+  // in LDS and lowers its priority while it is ahead of its partner: a scheduling hint only, the
+  // work and its order stay fixed.  Measured at B8 x 64 nodes (two workgroups per CU in turn)
+  // 137 -> 133.6 us; with one workgroup per CU it cost one-group waves 0.3-0.6 us and saved
+  // two-group ones ~1 us (B4 x 64 nodes 50.7 -> 49.5 us, FP8 51.5 -> 50.3).
   __shared__ int s_prog[8];
   const bool balance = W == 8 && p.pace_waves;
   auto pace = [&](int k) {
@@ -1296,7 +1297,7 @@ int launch_tree_prefix_mfma(const DecodeParams& p, int q_dtype, int waves, int p
   const int64_t units = (int64_t)batch * p.heads * groups * p.max_splits;
   if (units > 0x7fffffffLL) return set_error(FS_ERR_INVALID, "tree verify grid too large");
   DecodeParams pp = p;
-  pp.pace_waves = units > device_cu_count();
+  pp.pace_waves = units > device_cu_count() || per_wave == 2 * kNodeGroup;
   const dim3 grid((unsigned)units), block(kWave * waves);
   switch (q_dtype) {
     case FS_F32: launch_mq_q<float>(pp, tok, per_wave, grid, block, st); break;
