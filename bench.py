@@ -473,7 +473,9 @@ SHAPES = [
     ("page_16_quant_8", 8, 32, 4096, 128, 16, 8, "float16", None),
     ("head_dim_40", 8, 32, 4096, 40, 16, 16, "float16", None),
     ("head_dim_120", 8, 32, 4096, 120, 16, 16, "float16", None),
-    ("head_dim_36_generic", 8, 32, 4096, 36, 16, 16, "float16", None),
+    ("head_dim_36", 8, 32, 4096, 36, 16, 16, "float16", None),
+    ("head_dim_100", 8, 32, 4096, 100, 16, 16, "float16", None),
+    ("head_dim_34_generic", 8, 32, 4096, 34, 16, 16, "float16", None),
     ("batch_1_splitk", 1, 32, 16384, 128, 16, 16, "float16", None),
     ("c1_symmetric_per_token", 4, 32, 2048, 128, 16, 1, "float16", None),
     ("c2_symmetric_per_token", 8, 32, 4096, 128, 16, 1, "float16", None),

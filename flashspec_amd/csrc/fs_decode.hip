@@ -113,10 +113,11 @@ struct QSliceF {
 #pragma unroll
     for (int e = 0; e < 16; ++e) q[e] = to_f32(qp[e]);
   }
-  // the first 8 dims only (the lane holding a head_dim's last 8 dims); the rest zero
-  __device__ __forceinline__ void load8(const QT* qp) {
+  // the lane holding a head_dim's last 16 - s0 dims (s0 = 4, 8 or 12): qp points at the row's
+  // last 16 values, of which it keeps [s0, 16) in place and clears the rest
+  __device__ __forceinline__ void load_tail(const QT* qp, int s0) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) q[e] = e < 8 ? to_f32(qp[e]) : 0.f;
+    for (int e = 0; e < 16; ++e) q[e] = e >= s0 ? to_f32(qp[e]) : 0.f;
   }
   __device__ __forceinline__ void clear() {
 #pragma unroll
@@ -142,13 +143,13 @@ struct QSlice<__half> {
   static constexpr float kOffset = 1024.f;  // dot16 returns sum q*(1024+u)
   uint32_t qp[8];  // (q0,q2),(q1,q3),(q4,q6),(q5,q7),...
   float qsum_part;
-  template <int N = 16>
-  __device__ __forceinline__ void load(const __half* q) {
+  // dims [s0, 16) of q (s0 a multiple of 4); the others zero
+  __device__ __forceinline__ void load_from(const __half* q, int s0) {
     const uint16_t* h = (const uint16_t*)q;
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      if (4 * k < N) {
+      if (4 * k >= s0) {
         qp[2 * k] = (uint32_t)h[4 * k] | ((uint32_t)h[4 * k + 2] << 16);
         qp[2 * k + 1] = (uint32_t)h[4 * k + 1] | ((uint32_t)h[4 * k + 3] << 16);
 #pragma unroll
@@ -159,8 +160,10 @@ struct QSlice<__half> {
     }
     qsum_part = s;
   }
-  // the first 8 dims only (the lane holding a head_dim's last 8 dims); the rest zero
-  __device__ __forceinline__ void load8(const __half* q) { load<8>(q); }
+  __device__ __forceinline__ void load(const __half* q) { load_from(q, 0); }
+  // the lane holding a head_dim's last 16 - s0 dims (s0 = 4, 8 or 12): q points at the row's
+  // last 16 values, of which it keeps [s0, 16) in place and clears the rest
+  __device__ __forceinline__ void load_tail(const __half* q, int s0) { load_from(q, s0); }
   __device__ __forceinline__ void clear() {
 #pragma unroll
     for (int k = 0; k < 8; ++k) qp[k] = 0u;
@@ -812,8 +815,8 @@ __global__ void __launch_bounds__(kWave * max_tiled_waves(DP, QM))
 decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int32_t* w3, uint64_t w4, uint64_t w5,
                    uint64_t w6, const DecodeParams p) {
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
-  constexpr bool T8 = QM == kQmBlockTail8 || QM == kQmTokenTail8;  // head_dim an odd multiple of 8
-  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken || QM == kQmTokenTail8, CHB = QM == kQmChannelBlocks;
+  constexpr bool TAIL = QM == kQmBlockTail || QM == kQmTokenTail;  // head_dim not a multiple of 16
+  constexpr bool SUB = QM == kQmSub, TOK = QM == kQmToken || QM == kQmTokenTail, CHB = QM == kQmChannelBlocks;
   constexpr bool CH = QM == kQmChannel || CHB;
   constexpr bool APP = QM == kQmBlockAppend;  // one token appended to every request first
   static_assert(!APP || (PAGED && VF == kVfInt8), "the fused append serves paged INT8 stores");
@@ -854,10 +857,10 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   const int row = (b * nq + n) * heads + h;
   // The lane's 16 query values (dims [16j, 16j + 16), j = lane % LPT), fetched as 16-byte loads
   // now, so that their round trip overlaps the row length's and the block table's; converted
-  // once the first tile is on its way.  Head dims that are odd multiples of 8, and queries not
+  // once the first tile is on its way.  Head dims that are not multiples of 16, and queries not
   // 16-byte aligned, load them there instead.
   uint4 qraw[sizeof(QT)];
-  const bool qvec = !T8 && ((uintptr_t)qp & 15) == 0 && 16 * (lane % LPT) < D;
+  const bool qvec = !TAIL && ((uintptr_t)qp & 15) == 0 && 16 * (lane % LPT) < D;
   if (qvec) {
     const uint4* src = reinterpret_cast<const uint4*>(qp + (size_t)row * D + 16 * (lane % LPT));
 #pragma unroll
@@ -940,9 +943,11 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   const int j = lane % LPT;  // dim slice [16j, 16j+16)
   const int g = lane / LPT;  // token row within a load
   const bool active = 16 * j < D;  // lanes past head_dim (D < DP) hold zeros
-  // T8: the lane whose dims [16j, 16j + 16) pass the row end (D = 16j + 8) loads the row's last
-  // 16 bytes, [D - 16, D), and keeps their upper half as its dims 16j .. 16j + 7
-  const bool straddle = T8 && active && 16 * j + 16 > D;
+  // TAIL: the lane whose dims [16j, 16j + 16) pass the row end (D = 16j + 4, 8 or 12) loads the
+  // row's last 16 bytes, [D - 16, D), like its query values: its dims 16j .. D - 1 sit at
+  // positions s0 = 16j + 16 - D .. 15 of its registers, positions below s0 meet a zero query, and
+  // its accumulator is moved down by s0 once after the loop
+  const bool straddle = TAIL && active && 16 * j + 16 > D;
   const int col = active ? (straddle ? D - 16 : 16 * j) : 0;
   const int lane_off = g * D + col;
   const int rstride = RPL * D;
@@ -1053,7 +1058,7 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   float qsum = 0.f;
   auto prepare_q = [&]() {
     if (straddle) {
-      q.load8(qp + (size_t)row * D + 16 * j);
+      q.load_tail(qp + (size_t)row * D + D - 16, 16 * j + 16 - D);
     } else if (qvec) {
       QT qv[16];
       __builtin_memcpy(qv, qraw, sizeof(qv));
@@ -1106,15 +1111,6 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
       load_tile_tok<DP, VF == kVfInt8>(t, p, kbase, vbase, base_of(k), avail_of(k), D, g, col);
     else
       load_tile<DP>(t, kbase, vbase, base_of(k), D, lane_off, rstride);
-    if constexpr (T8) {
-      if (straddle) {
-#pragma unroll
-        for (int r = 0; r < LPTILE; ++r) {
-          t.k[r] = make_uint4(t.k[r].z, t.k[r].w, 0u, 0u);
-          t.v[r] = make_uint4(t.v[r].z, t.v[r].w, 0u, 0u);
-        }
-      }
-    }
   };
   auto consume = [&](const TileRegs<DP>& t, int k) {
     k = seq(k);
@@ -1207,6 +1203,18 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   }
 #pragma unroll
   for (int e = 0; e < 16; ++e) st.acc[e] -= st.zacc;
+  if constexpr (TAIL) {
+    if (straddle) {  // dims 16j .. D - 1 from positions s0 .. 15 to 0 .. 15 - s0
+      const int s0 = 16 * j + 16 - D;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float a4 = e + 4 < 16 ? st.acc[e + 4] : 0.f;
+        const float a8 = e + 8 < 16 ? st.acc[e + 8] : 0.f;
+        const float a12 = e + 12 < 16 ? st.acc[e + 12] : 0.f;
+        st.acc[e] = s0 == 4 ? a4 : (s0 == 8 ? a8 : a12);
+      }
+    }
+  }
   // One running maximum per wave (lanes of a token-row group already share theirs), then the
   // groups' sums, scattered so that each lane holds NV = LPT / 4 dims of the wave's result.
   constexpr int NV = LPT / 4;
@@ -1402,11 +1410,13 @@ combine_splits_kernel(const float* part_ml, const float* part_acc, const int64_t
 // Tiled path: head_dim a multiple of 16 up to 256 (served by the 64-, 128- or 256-dim
 // register layout), quant blocks a multiple of 8 tokens with whole quant blocks per page, or
 // one parameter set per token (quant block 1) on contiguous rows or pages of 16k tokens.
-// Per-channel stores take the tiled path with quant blocks of a multiple of 16 tokens.
+// Per-channel stores take the tiled path with quant blocks of a multiple of 16 tokens.  A
+// head_dim that is a multiple of 4 but not of 16 (20 .. 252) takes it with quant blocks of a
+// multiple of 16 tokens or per-token parameters.
 static bool tiled_path(int head_dim, int page_size, int quant_block, bool per_channel = false) {
-  if (head_dim < 16 || head_dim > 256 || head_dim % 8 != 0 || page_size <= 0) return false;
-  if (head_dim % 16 != 0) {  // an odd multiple of 8: block and per-token parameters only
-    if (head_dim < 24 || per_channel) return false;
+  if (head_dim < 16 || head_dim > 256 || head_dim % 4 != 0 || page_size <= 0) return false;
+  if (head_dim % 16 != 0) {  // a straddling lane (from 20 dims on): block and per-token parameters only
+    if (head_dim < 20 || per_channel) return false;
     if (quant_block == 1) return page_size == 1 || page_size % kTile == 0;
     return quant_block % kTile == 0 && page_size % quant_block == 0;
   }
@@ -1508,13 +1518,13 @@ static int launch_typed(const DecodeParams& p, bool tiled, int waves_per_block, 
     else if (p.per_channel)
       launch_tiled<QT, PAGED, kQmChannel>(p, sw, grid, block, st);
     else if (p.quant_block == 1 && p.head_dim % 16 != 0)
-      launch_tiled<QT, PAGED, kQmTokenTail8>(p, sw, grid, block, st);
+      launch_tiled<QT, PAGED, kQmTokenTail>(p, sw, grid, block, st);
     else if (p.quant_block == 1)
       launch_tiled<QT, PAGED, kQmToken>(p, sw, grid, block, st);
     else if (p.quant_block % kTile != 0)
       launch_tiled<QT, PAGED, kQmSub>(p, sw, grid, block, st);
     else if (p.head_dim % 16 != 0)
-      launch_tiled<QT, PAGED, kQmBlockTail8>(p, sw, grid, block, st);
+      launch_tiled<QT, PAGED, kQmBlockTail>(p, sw, grid, block, st);
     else
       launch_tiled<QT, PAGED, kQmBlock>(p, sw, grid, block, st);
   } else {

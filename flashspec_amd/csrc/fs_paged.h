@@ -18,10 +18,10 @@ enum QuantMode : int {
   kQmToken = 2,  // one entry per token (quant block 1, e.g. symmetric per-token INT8)
   kQmChannel = 3,  // per quant block (a multiple of 16 tokens) one entry per channel
   kQmChannelBlocks = 4,  // kQmChannel with quant blocks of >= 2 tiles: waves take whole blocks
-  // kQmBlock / kQmToken for a head_dim that is an odd multiple of 8 (>= 24): the lane whose 16
-  // dims straddle the row end loads the row's last 16 bytes and keeps their upper half
-  kQmBlockTail8 = 5,
-  kQmTokenTail8 = 6,
+  // kQmBlock / kQmToken for a head_dim that is a multiple of 4 but not of 16 (>= 20): the lane
+  // whose 16 dims straddle the row end loads the row's last 16 bytes and uses their upper part
+  kQmBlockTail = 5,
+  kQmTokenTail = 6,
   // kQmBlock (paged, 16-token pages holding one quant block, head_dim 64 / 128 / 256) with one
   // decode token appended to every request inside the launch (fs_paged_decode_append_i8)
   kQmBlockAppend = 7,

@@ -45,9 +45,12 @@ int fs_abi_version(void);
 int64_t fs_decode_workspace_bytes(int64_t rows, int64_t max_splits, int64_t head_dim);
 
 /*
- * Which decode kernel serves a shape: 1 = tiled path (head_dim a multiple of 16 up
- * to 256, quant block a multiple of 16, page a multiple of the quant block), 0 =
- * generic path.  The split plan differs:
+ * Which decode kernel serves a shape: 1 = tiled path, 0 = generic path.  The tiled
+ * path takes head_dim a multiple of 16 up to 256 with quant blocks of a multiple of
+ * 8 tokens (pages a multiple of the quant block), or one scale per token (quant
+ * block 1) on contiguous rows or pages of a multiple of 16 tokens; and head_dim a
+ * multiple of 4 from 20 to 252 with quant blocks of a multiple of 16 tokens or one
+ * scale per token.  The split plan differs:
  * on the tiled path one split is one workgroup of `waves_per_block` cooperating
  * waves (split_tiles <= 64 * waves_per_block); on the generic path one split is
  * one wave and `waves_per_block` only groups independent waves.

@@ -16,7 +16,7 @@ static void check(int ok, const char* what) {
 int main(void) {
   check(fs_abi_version() == 2, "fs_abi_version() == 2");
   check(fs_decode_workspace_bytes(256, 16, 128) == (int64_t)256 * 16 * 130 * 4, "workspace bytes");
-  check(fs_decode_tiled_path(128, 16, 16) == 1 && fs_decode_tiled_path(36, 16, 16) == 0, "tiled path query");
+  check(fs_decode_tiled_path(128, 16, 16) == 1 && fs_decode_tiled_path(34, 16, 16) == 0, "tiled path query");
   check(fs_tree_mfma_path(128, 16, 16) == 1 && fs_tree_mfma_path(96, 16, 16) == 0, "tree path query");
   /* head_dim 0: rejected before launch, with a message */
   int rc = fs_paged_decode_i8((const void*)1, FS_F16, (const int8_t*)1, (const float*)1, (const int16_t*)1,

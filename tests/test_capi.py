@@ -62,11 +62,15 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.fs_decode_tiled_path(128, 16, 16) == 1 and lib.fs_decode_tiled_path(128, 32, 16) == 1
     assert lib.fs_decode_tiled_path(48, 16, 16) == 1 and lib.fs_decode_tiled_path(96, 32, 32) == 1
     assert lib.fs_decode_tiled_path(128, 16, 8) == 1 and lib.fs_decode_tiled_path(128, 24, 24) == 1
-    assert lib.fs_decode_tiled_path(128, 4, 4) == 0 and lib.fs_decode_tiled_path(68, 16, 16) == 0
-    # head_dim an odd multiple of 8 (>= 24): block and per-token parameters on the tiled path
+    assert lib.fs_decode_tiled_path(128, 4, 4) == 0 and lib.fs_decode_tiled_path(66, 16, 16) == 0
+    # head_dim a multiple of 4 but not of 16 (>= 20): block and per-token parameters on the tiled path
     assert lib.fs_decode_tiled_path(72, 16, 16) == 1 and lib.fs_decode_tiled_path(24, 16, 1) == 1
-    assert lib.fs_decode_tiled_path(8, 16, 16) == 0 and lib.fs_decode_tiled_path(72, 8, 8) == 0
-    assert lib.fs_decode_tiled_path_channel(72, 16, 16) == 0
+    assert lib.fs_decode_tiled_path(68, 16, 16) == 1 and lib.fs_decode_tiled_path(36, 32, 1) == 1
+    assert lib.fs_decode_tiled_path(20, 16, 16) == 1 and lib.fs_decode_tiled_path(252, 16, 16) == 1
+    assert lib.fs_decode_tiled_path(8, 16, 16) == 0 and lib.fs_decode_tiled_path(12, 16, 16) == 0
+    assert lib.fs_decode_tiled_path(72, 8, 8) == 0 and lib.fs_decode_tiled_path(36, 8, 8) == 0
+    assert lib.fs_decode_tiled_path(34, 16, 16) == 0 and lib.fs_decode_tiled_path(260, 16, 16) == 0
+    assert lib.fs_decode_tiled_path_channel(72, 16, 16) == 0 and lib.fs_decode_tiled_path_channel(36, 16, 16) == 0
     assert lib.fs_decode_tiled_path(128, 48, 32) == 0 and lib.fs_decode_tiled_path(512, 16, 16) == 0
     # per-channel stores with 64-token blocks: waves take whole blocks, so a split holds whole
     # blocks of 4 tiles and a wave at most 64 tiles
@@ -109,8 +113,8 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert fused(16, 96, 7, 9) == _lib.FS_ERR_INVALID and "64, 128 or 256" in lib.fs_last_error().decode()
     assert fused(16, 128, 7, 7) == _lib.FS_ERR_INVALID and "lengths_out" in lib.fs_last_error().decode()
     assert fused(16, 128, 7, None) == _lib.FS_ERR_INVALID
-    # a request order needs the tiled path (head_dim 36 takes the generic kernel)
-    rc = lib.fs_paged_decode_ordered(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 1, None, 0, None, 0, 2, 2, 36, 8, 16, 16,
+    # a request order needs the tiled path (head_dim 34 takes the generic kernel)
+    rc = lib.fs_paged_decode_ordered(1, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 1, 1, 1, None, 0, None, 0, 2, 2, 34, 8, 16, 16,
                                      64, 0.1, 4, 1, 1, None)
     assert rc == _lib.FS_ERR_INVALID and "tiled" in lib.fs_last_error().decode()
     # tree verification with the in-launch merge: INT8 or FP8 only, 16 / 32 / library-chosen node groups,

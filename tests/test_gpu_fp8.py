@@ -96,7 +96,9 @@ def _fused_fp8(B, H, S, D, bs, seed, q_dtype):
     (2, 2, 77, 40, 16, torch.float16, [77, 5]),      # head_dim 40: an odd multiple of 8
     (2, 4, 160, 128, 1, torch.float16, [160, 33]),   # one scale per token
     (2, 2, 90, 56, 1, torch.bfloat16, [90, 41]),     # head_dim 56, one scale per token
-    (2, 2, 70, 44, 16, torch.float16, [70, 9]),      # generic kernel: head_dim 44
+    (2, 2, 70, 44, 16, torch.float16, [70, 9]),      # head_dim 44: 12 straddling dims
+    (2, 2, 80, 148, 1, torch.bfloat16, [80, 21]),    # head_dim 148: 4 straddling dims, one scale per token
+    (2, 2, 70, 42, 16, torch.float16, [70, 9]),      # generic kernel: head_dim 42
 ])
 def test_fused_fp8_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     from tests._helpers import to_qt
@@ -107,8 +109,8 @@ def test_fused_fp8_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     got, stats = fa.fused_dequant_attention_triton(q.to(DEV), to_qt(kq, DEV), to_qt(vq, DEV),
                                                    lengths=None if lens is None else lens.to(DEV), return_stats=True)
     sync()
-    # tiled: head_dim a multiple of 16, or an odd multiple of 8 with block / per-token scales
-    assert stats["tiled_path"] == float(D % 16 == 0 or (D % 8 == 0 and D >= 24 and (bs == 1 or bs % 16 == 0)))
+    # tiled: head_dim a multiple of 16, or one of 4 from 20 on with block / per-token scales
+    assert stats["tiled_path"] == float(D % 16 == 0 or (D % 4 == 0 and D >= 20 and (bs == 1 or bs % 16 == 0)))
     ref = oa.fused_dequant_attention(np_of(q.float()), kq, vq, None if lens is None else lens.numpy())
     if lengths is not None and 0 in lengths:
         keep = [i for i, L in enumerate(lengths) if L != 0]

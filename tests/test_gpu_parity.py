@@ -152,6 +152,8 @@ def _sym_fused_case(B, H, S, D, seed, q_dtype):
     (1, 2, 300, 256, torch.float16, None),
     (2, 3, 50, 96, torch.float32, [50, 17]),
     (2, 3, 120, 104, torch.float16, [120, 64]),     # head_dim 104: the straddling lane in token mode
+    (2, 2, 90, 52, torch.bfloat16, [90, 33]),       # head_dim 52: 4 straddling dims in token mode
+    (1, 3, 140, 124, torch.float32, None),          # head_dim 124: 12 straddling dims in token mode
 ])
 def test_fused_symmetric_per_token_matches_oracle(B, H, S, D, q_dtype, lengths):
     announce(f"fused symmetric per-token B{B} H{H} S{S} D{D} {q_dtype} lengths={lengths}")
@@ -386,7 +388,10 @@ def _fused_case(B, H, S, D, bs, seed, q_dtype=torch.float16, lengths=None):
     (2, 3, 333, 120, 16, torch.bfloat16, [333, 200]),     # head_dim 120 on the 128-dim layout
     (1, 2, 260, 248, 32, torch.float32, None),            # head_dim 248 on the 256-dim layout
     (2, 2, 1500, 88, 16, torch.float16, [1500, 700]),     # head_dim 88, split-K
-    (2, 2, 90, 36, 16, torch.float16, [90, 31]),          # generic path: head_dim 36
+    (2, 2, 90, 36, 16, torch.float16, [90, 31]),          # head_dim 36: the straddling lane keeps 4 dims
+    (1, 2, 150, 100, 16, torch.bfloat16, [150]),          # head_dim 100: 4 dims past 96 on the 128-dim layout
+    (2, 2, 130, 220, 32, torch.float32, [130, 47]),       # head_dim 220: 12 dims past 208 on the 256-dim layout
+    (2, 2, 90, 34, 16, torch.float16, [90, 31]),          # generic path: head_dim 34
 ])
 def test_fused_attention_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     announce(f"fused B{B} H{H} S{S} D{D} bs{bs} {q_dtype} lengths={lengths}")
@@ -442,7 +447,10 @@ def _paged_case(B, H, S, D, page, seed, layout="contiguous", lengths=None, q_dty
     (2, 2, 200, 112, 64, "interleaved", [200, 64]),       # head_dim 112, page 64
     (2, 2, 50, 24, 16, "contiguous", [50, 9]),            # head_dim 24: the straddling lane loads bytes 8..23
     (2, 3, 300, 72, 32, "shuffled", [300, 45]),           # head_dim 72, two tiles per page
-    (2, 2, 60, 20, 16, "interleaved", [60, 13]),          # generic path: head_dim 20
+    (2, 2, 60, 20, 16, "interleaved", [60, 13]),          # head_dim 20: the straddling lane loads bytes 4..19
+    (2, 3, 300, 44, 32, "shuffled", [300, 45]),           # head_dim 44: 12 dims past 32, two tiles per page
+    (2, 2, 200, 196, 16, "contiguous", [200, 77]),        # head_dim 196: 4 dims past 192 on the 256-dim layout
+    (2, 2, 60, 18, 16, "interleaved", [60, 13]),          # generic path: head_dim 18
     (3, 4, 200, 128, 8, "shuffled", [200, 17, 9]),        # 8-token pages: two pages per tile
     (2, 2, 100, 64, 8, "interleaved", [100, 8]),          # 8-token pages, 64-dim layout
     (2, 3, 150, 96, 24, "shuffled", [150, 50]),           # 24-token pages

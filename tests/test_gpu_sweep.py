@@ -3,8 +3,8 @@
 Each case draws batch, heads, head_dim, page size, KV format, query dtype, page layout and
 ragged lengths (empty and one-token rows included) from its own seed, so the hand-picked
 parity cases' kernel paths also meet in combinations nobody listed: the 64/128/256-dim
-layouts, head_dims that are odd multiples of 8 (the straddling lane) or not multiples of 8
-(generic kernel), sub-tile pages, per-token / FP8 / per-channel parameters (single-tile and
+layouts, head_dims that are multiples of 4 but not of 16 (the straddling lane) or not
+multiples of 4 (generic kernel), sub-tile pages, per-token / FP8 / per-channel parameters (single-tile and
 whole-block waves), forced split counts.  Attention within max-abs 2e-3 / max-rel 1e-2 of
 the oracle, zero rows for empty requests.
 """
@@ -25,7 +25,7 @@ from tests._helpers import assert_attention_close, from_cache, np_of, randn
 pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda", 0)
-HEAD_DIMS = (16, 24, 32, 36, 40, 48, 64, 72, 96, 104, 120, 128, 136, 160, 200, 248, 256)
+HEAD_DIMS = (16, 20, 24, 32, 34, 36, 40, 44, 48, 64, 72, 96, 100, 104, 120, 128, 136, 160, 200, 212, 248, 256)
 PAGES = (8, 16, 32, 48, 64)
 FORMATS = ("affine_block", "symmetric_token", "fp8_block", "affine_channel")
 QDTYPES = (torch.float16, torch.bfloat16, torch.float32)
