@@ -607,12 +607,13 @@ __device__ __forceinline__ float allreduce_groups(float x) {
 // is all zero again when the kernel ends.  Nobody waits for
 // a workgroup that has not yet arrived; the waits end within the latency of stores already issued
 // (bounded by kMergeSpins regardless, after which the row is written as NaN).
-// Thread tid holds dims tid + k * blockDim.x (k < DPT) of its split's un-normalized state a[k], with
-// the split's max M (log2 units) and denominator L.
-template <int DPT, typename QT>
+// Thread tid holds dims tid + k * NTHR (k < DPT; NTHR = the workgroup's threads) of its split's
+// un-normalized state a[k], with the split's max M (log2 units) and denominator L.
+template <int DPT, int NTHR, typename QT>
 __device__ __forceinline__ void merge_splits_here(const DecodeParams& p, int* s_last, int row, int split, int nsplit,
                                                   int D, float M, float L, const float (&a)[DPT]) {
-  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int tid = threadIdx.x;
+  constexpr int nthr = NTHR;
   const size_t rs = (size_t)D + 2;
   unsigned long long* slots = p.merge_slots + (size_t)row * p.max_splits * rs;
   unsigned long long* own = slots + (size_t)split * rs;
@@ -716,9 +717,13 @@ __device__ __forceinline__ void merge_splits_here(const DecodeParams& p, int* s_
   if (tid == 0) __hip_atomic_store(p.merge_count + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The workgroup's NW waves' states in LDS -> the row's output (one split) or the split's state.
+// NW is the workgroup's wave count, so the thread count is a constant here (blockDim.x is read from
+// the implicit kernel arguments: a scalar load after the loop, on a line nothing else reads).
 template <int NW, int DP, typename QT>
 __device__ __forceinline__ void merge_waves(const DecodeParams& p, const float* s_acc, const float* s_ml, int* s_last,
                                             int row, int split, int nsplit, int D) {
+  constexpr int kThreads = NW * kWave;
   float mv[NW], lv[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
@@ -741,17 +746,17 @@ __device__ __forceinline__ void merge_waves(const DecodeParams& p, const float* 
     float a[DPT];
 #pragma unroll
     for (int k = 0; k < DPT; ++k) {
-      const int d = threadIdx.x + k * blockDim.x;
+      const int d = threadIdx.x + k * kThreads;
       a[k] = 0.f;
       if (d < D) {
 #pragma unroll
         for (int w = 0; w < NW; ++w) a[k] = fmaf(s_acc[w * DP + d], ew[w], a[k]);
       }
     }
-    merge_splits_here<DPT, QT>(p, s_last, row, split, nsplit, D, M, L, a);
+    merge_splits_here<DPT, kThreads, QT>(p, s_last, row, split, nsplit, D, M, L, a);
     return;
   }
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+  for (int d = threadIdx.x; d < D; d += kThreads) {
     float x[NW];
 #pragma unroll
     for (int w = 0; w < NW; ++w) x[w] = s_acc[w * DP + d];
