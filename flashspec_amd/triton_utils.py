@@ -190,6 +190,19 @@ LIGHT_MIN_SPLIT_TILES = 64
 # B4 S4096 (256 tiles) keeps its split: 2 x 4 waves 29.1 / 27.9 against unsplit x 8 29.9 / 29.3.
 HALVE_MIN_SPLIT_TILES = 128
 HALF_EMPTY_WAVES = 8
+# A forced split count (FLASHSPEC_NUM_SPLITS) of two or more can put several workgroups on each CU:
+# the plan then halves its waves while a workgroup holds more than 8 (what the in-kernel merge
+# serves) or, with more workgroups than CUs, the grid more than FORCED_WAVES_PER_CU waves per CU, as
+# long as a split's tiles still fit its waves.
+# Measured on MI355X (one box, fused / paged us, 3+ rotated input sets), with the waves the plan
+# took before: B8 H32 S4096 D128 4 splits (the reference's C2 setting) 2 waves 46.1 / 47.9 against
+# 16 waves 53.5 / 57.3, 2 splits 4 waves 44.0 / 46.0 against 16 waves 49.4 / 53.0, 8 splits 1 wave
+# 52.5 / 51.1 against 8 waves 57.7 / 58.3; B8 S2048 4 splits 2 waves 27.1 / 26.8 against 8 waves
+# 31.4 / 31.7; B4 S2048 4 splits 4 waves 16.2 / 16.0 against 8 waves 17.0 / 16.9; B1 S16384
+# 4 splits 8 waves 29.4 / 30.4 against 16 waves 31.6 / 33.1, 16 splits 4 waves 29.5 / 31.4
+# against 16 waves 32.8 / 36.4.
+FORCED_WAVES_PER_CU = 8
+FORCED_MAX_WAVES = 8
 GENERIC_WAVES_PER_CU = 16
 GENERIC_MIN_SPLIT_TILES = 8
 GENERIC_MAX_SPLIT_TILES = 64
@@ -276,6 +289,12 @@ def plan_splits(seq_len: int, rows: int, block_n: int, cu_count: int, *, tiled: 
             if light and grp == 1 and cu_count * 3 // 4 <= rows * n <= cu_count and \
                     LIGHT_MIN_SPLIT_TILES <= split_groups <= LIGHT_WAVES * MAX_TILES_PER_WAVE:
                 waves = LIGHT_WAVES
+            if forced is not None and n > 1:
+                need = math.ceil(split_groups / (MAX_TILES_PER_WAVE // grp))  # waves a split's tiles need
+                several = rows * n > cu_count  # more than one workgroup per CU
+                while waves // 2 >= need and (waves > FORCED_MAX_WAVES or
+                                              several and rows * n * waves > cu_count * FORCED_WAVES_PER_CU):
+                    waves //= 2
         cap = MAX_TILES_PER_WAVE // grp * waves
         if split_groups > cap:
             split_groups = math.ceil(groups / math.ceil(groups / cap))

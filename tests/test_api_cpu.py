@@ -153,6 +153,18 @@ def test_split_plan_covers_every_tile(clean_env):
     assert plan(4096, 160, 128, 256, light=True) == (128, 2, 16)   # 320 workgroups: more than one per CU
     clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1")  # 128 of 256 CUs busy: not full enough for 4 waves
     assert plan(2048, 128, 128, 256, light=True) == (128, 1, 16)
+    # forced split counts of 2+: at most 8 waves per workgroup (in-kernel merge) and, with more
+    # workgroups than CUs, about 8 resident waves per CU; enough for a split's tiles
+    clean_env.setenv("FLASHSPEC_NUM_SPLITS", "4")
+    assert plan(4096, 256, 128, 256, light=True) == (64, 4, 2)     # the reference's C2 setting
+    assert plan(4096, 256, 128, 256) == (64, 4, 2)
+    assert plan(2048, 128, 128, 256, light=True) == (32, 4, 4)
+    assert plan(16384, 32, 128, 256, light=True) == (256, 4, 8)
+    clean_env.setenv("FLASHSPEC_NUM_SPLITS", "2")
+    assert plan(4096, 256, 128, 256, light=True) == (128, 2, 4)
+    assert plan(65536, 256, 128, 256, light=True) == (1024, 4, 16)  # 2048-tile splits need 32 waves
+    clean_env.setenv("FLASHSPEC_NUM_SPLITS", "8")
+    assert plan(4096, 256, 128, 256, light=True) == (32, 8, 1)
     clean_env.delenv("FLASHSPEC_NUM_SPLITS")
     clean_env.setenv("FLASHSPEC_NUM_WARPS", "16")
     assert plan(4096, 256, 128, 256, waves=triton_utils.forced_tiled_waves(), light=True) == (256, 1, 16)
@@ -169,8 +181,8 @@ def test_split_plan_covers_every_tile(clean_env):
     assert plan(4096, 8, 128, 256) == (8, 32, 2)
     clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1")
     assert plan(4096, 256, 128, 256) == (256, 1, 16)
-    clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1000")  # clamped to ceil(S/block_n)
-    assert plan(4096, 256, 128, 256) == (8, 32, 2)
+    clean_env.setenv("FLASHSPEC_NUM_SPLITS", "1000")  # clamped to ceil(S/block_n); 8192 workgroups of 1 wave
+    assert plan(4096, 256, 128, 256) == (8, 32, 1)
     clean_env.setenv("FLASHSPEC_NUM_WARPS", "8")
     assert triton_utils.forced_tiled_waves() == 8
     clean_env.setenv("FLASHSPEC_NUM_WARPS", "16")
