@@ -1013,17 +1013,70 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   const int rot = CHB ? 0 : tile_rotation(b, split, nk);
   float my_ks = 0.f, my_kz = 0.f, my_vs = 0.f, my_vz = 0.f;
   if constexpr (!SPEC) load_params();
+  float qk_eff = p.qk_scale;  // the key scales' factor (bf16 queries: divided by their scale)
+  // bf16 queries over INT8 blocks take the fp16 score path (QB16): the wave's query row is scaled by
+  // the power of two that puts its largest |q| into [2^13, 2^14), which bf16's 8 significant bits
+  // survive exactly in fp16, and the key scales take the inverse power (qk_eff).
+  constexpr bool QB16 = std::is_same<QT, __hip_bfloat16>::value && VF == kVfInt8 &&
+                        (QM == kQmBlock || QM == kQmBlockTail || QM == kQmBlockAppend);
+  using QS = typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>,
+                                       typename std::conditional<QB16, QSlice<__half>, QSlice<QT>>::type>::type;
+  QS q;
+  float qsum = 0.f;
+  auto prepare_q = [&]() {
+    if constexpr (QB16) {
+      float x[16];
+      const QT* src = straddle ? qp + (size_t)row * D + D - 16 : qp + (size_t)row * D + 16 * j;
+      const int s0 = straddle ? 16 * j + 16 - D : 0;
+      if (qvec) {
+        QT qv[16];
+        __builtin_memcpy(qv, qraw, sizeof(qv));
+#pragma unroll
+        for (int e = 0; e < 16; ++e) x[e] = to_f32(qv[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) x[e] = active && e >= s0 ? to_f32(src[e]) : 0.f;
+      }
+      float mx = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, fabsf(x[e]));
+      mx = wave_max_valu(mx);
+      // floor(log2(mx)) from the exponent field (a zero or subnormal mx gives the largest shift)
+      int sh = 13 - ((int)((__float_as_uint(mx) >> 23) & 0xffu) - 127);
+      sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
+      const float up = __uint_as_float((uint32_t)(127 + sh) << 23);
+      qk_eff = p.qk_scale * __uint_as_float((uint32_t)(127 - sh) << 23);
+      __half h[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) h[e] = __float2half_rn(x[e] * up);
+      q.load(h);
+    } else if (straddle) {
+      q.load_tail(qp + (size_t)row * D + D - 16, 16 * j + 16 - D);
+    } else if (qvec) {
+      QT qv[16];
+      __builtin_memcpy(qv, qraw, sizeof(qv));
+      q.load(qv);
+    } else if (active) {
+      q.load(qp + (size_t)row * D + 16 * j);
+    } else {
+      q.clear();
+    }
+    qsum = group_sum<LPT>(q.sum());
+  };
   auto convert_params = [&]() {
     // the empty asm keeps the conversions here, and the tile loads ahead of them: folded into the
     // loads' branch, or with the tile loads moved below them, they would wait before those go out
     asm volatile("" : "+v"(ks_raw), "+v"(vs_raw), "+v"(kz_raw), "+v"(vz_raw)::"memory");
     const bool backed = my_base >= 0;  // SPEC loaded lanes now masked: their parameters stay 0
-    my_ks = backed ? ks_raw * p.qk_scale : 0.f;
+    my_ks = backed ? ks_raw * qk_eff : 0.f;
     my_kz = backed ? (float)kz_raw : 0.f;
     my_vs = backed ? vs_raw : 0.f;
     my_vz = backed ? (float)vz_raw : 0.f;
   };
-  if constexpr (APP) convert_params();  // the append below updates the parameters of its tile
+  if constexpr (APP) {  // the append below updates the parameters of its tile
+    if constexpr (QB16) prepare_q();  // qk_eff first
+    convert_params();
+  }
   float my_ks1 = 0.f, my_kz1 = 0.f, my_vs1 = 0.f, my_vz1 = 0.f;
   if constexpr (SUB) {
     if (my_base1 >= 0) {
@@ -1058,23 +1111,6 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
     }
   }
 
-  using QS = typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>, QSlice<QT>>::type;
-  QS q;
-  float qsum = 0.f;
-  auto prepare_q = [&]() {
-    if (straddle) {
-      q.load_tail(qp + (size_t)row * D + D - 16, 16 * j + 16 - D);
-    } else if (qvec) {
-      QT qv[16];
-      __builtin_memcpy(qv, qraw, sizeof(qv));
-      q.load(qv);
-    } else if (active) {
-      q.load(qp + (size_t)row * D + 16 * j);
-    } else {
-      q.clear();
-    }
-    qsum = group_sum<LPT>(q.sum());
-  };
 
   LaneState st;
   st.m = kNegBig;
@@ -1187,7 +1223,7 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
     requant_appended_page<DP, QT>(prm, a, p, readlane_i32(my_base, k_app), readlane_i32(my_meta, k_app), app_off,
                                   lane_off, rstride, g);
     if (lane == k_app) {
-      my_ks = prm[0] * p.qk_scale;  // as the lane-held parameters are formed from the store
+      my_ks = prm[0] * qk_eff;  // as the lane-held parameters are formed from the store
       my_kz = prm[1];
       my_vs = prm[2];
       my_vz = prm[3];
@@ -1197,8 +1233,9 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
     if (k_app >= 0) finish_append(append());
   }
   if constexpr (!SPEC) load(ta, 0);
+  if constexpr (QB16 && !APP) prepare_q();  // qk_eff first
   if constexpr (!APP) convert_params();
-  prepare_q();
+  if constexpr (!QB16) prepare_q();
   for (int k = 0; k < nk; k += 2) {
     load(tb2, k + 1);
     consume(ta, k);

@@ -457,7 +457,7 @@ class DecodeBatch:
         max_seq_len = -(-(max(self.host_lengths) + 1) // self.page) * self.page
         rows = len(self._requests) * a.heads
         plan = launch_plan(max_seq_len, rows, a.head_dim, self.page, self.page, self.device,
-                           light=q.dtype == torch.float16)
+                           light=q.dtype in (torch.float16, torch.bfloat16))
         if rows * plan[3] > device_cu_count(self.device):
             return None
         return max_seq_len, plan
