@@ -379,9 +379,14 @@ struct LaneState {
   float acc[16];
 };
 
+// Contraction stays off here: a score s enters both the running max and exp2(s - m), and fused into
+// the subtraction (fma(x, ks, -m)) its product would carry its rounding error into the exponent --
+// half an ulp of s, which at extreme logits (|s| ~ 1e10 in log2 units) turns a weight of 1 into 0 or
+// inf.  The same holds in every loop below that rescales by a running max.
 template <int DP, int VF, typename QS>
 __device__ __forceinline__ void consume_tile(LaneState& st, const TileRegs<DP>& t, const QS& q, float qsum,
                                              const RowMeta<TileRegs<DP>::LPTILE>& rm, int token0, int len, int g) {
+#pragma clang fp contract(off)
   constexpr int LPT = TileRegs<DP>::LPT, RPL = TileRegs<DP>::RPL, LPTILE = TileRegs<DP>::LPTILE;
   float s[LPTILE];
   bool ok[LPTILE];
@@ -1299,6 +1304,7 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
 template <typename QT, bool PAGED, int VF, bool CH = false>
 __global__ void __launch_bounds__(1024)
 decode_generic_kernel(const DecodeParams p) {
+#pragma clang fp contract(off)  // the scores feed both the running max and exp2 (see consume_tile)
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
   if (wave >= p.rows * p.max_splits) return;

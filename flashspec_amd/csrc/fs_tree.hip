@@ -267,6 +267,7 @@ __device__ __forceinline__ void tree_path_accumulate(float& M, float& L, float (
                                                      const DT* dk, const DT* dv, size_t stride,
                                                      const int64_t* parents, int b, int n, int nq, int D,
                                                      float qk_scale, int lane) {
+#pragma clang fp contract(off)  // each score feeds both the running max and exp2(score - max)
   float qv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < CMAX; ++c) {
@@ -564,6 +565,8 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   // With block parameters each score is one FMA, S * (ks * qmul) + (-(1024 + zk) * ks) *
   // (sum(q) * qmul), whose addend is -inf for a masked token.
   auto scores = [&](const MqTile<DP, TOK>& t, int k, float (&sc)[NG][4], float (&vfac)[4], f16x4_t& nzv) {
+    // no contraction of the scores' last products into the softmax's exp2(score - max)
+#pragma clang fp contract(off)
     if constexpr (kRotate) k = tile_in_order(k, rot, nk);
     const bool backed = k < nk && off_of(k) >= 0;
     const int token0 = (first + W * k) * kTile + 4 * g;
@@ -740,6 +743,7 @@ tree_prefix_mfma_kernel(const DecodeParams p) {
   // the fp16 V rows as the A operand into a zeroed accumulator that joins acc in its value units
   // (1 / vref).  The path walks do the same sum one token at a time.
   auto draft_pair = [&](int j) {
+#pragma clang fp contract(off)  // the scores feed both the running max and exp2 (see scores)
     const unsigned char* kst = s_stage;
     const unsigned char* vst = s_stage + (size_t)nq * D * sizeof(QT);
     uint64_t anc[NG];

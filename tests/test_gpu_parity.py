@@ -509,6 +509,35 @@ def test_paged_attention_other_query_dtypes(q_dtype):
     assert_attention_close(got, oracle_paged_attention(q, cache), q_dtype, str(q_dtype))
 
 
+@pytest.mark.parametrize("D,qb,q_dtype", [(128, 16, torch.bfloat16), (120, 16, torch.bfloat16),
+                                          (64, 32, torch.bfloat16), (64, 16, torch.float32),
+                                          (128, 16, torch.float32), (34, 16, torch.float32)])
+def test_query_rows_at_extreme_magnitudes(D, qb, q_dtype):
+    """Rows of zeros, of tiny and of huge values, and a row whose one large element sits beside tiny
+    ones.  bf16 queries over INT8 blocks enter the fp16 score path scaled by a power of two per row
+    (the tiny elements fall to fp16 subnormals or zero); huge rows make the softmax one-hot, which
+    holds only if exp2(score - max) sees the same rounded score as the running max (64-dim layout,
+    generic kernel at head_dim 34)."""
+
+    announce(f"query magnitudes D{D} qb{qb} {q_dtype}")
+    B, H, S = 2, 4, 300
+    base = randn((B, H, D), 91, torch.float32)
+    rows = [torch.zeros(D), base[0, 1] * 1e-20, base[0, 2] * 1e20, base[0, 3]]
+    big = torch.full((D,), 1e-6)
+    big[D // 3] = 1e4
+    rows += [big, base[1, 1] * 3e-3, base[1, 2] * 40.0, -base[1, 3]]
+    q = torch.stack(rows).reshape(B, H, D).to(q_dtype)
+    k = randn((B, H, S, D), 92)
+    v = randn((B, H, S, D), 93)
+    lens = torch.tensor([S, 137], dtype=torch.int64)
+    cache = fa.PagedKVCache.from_dense(k.to(DEV), v.to(DEV), block_size=qb, lengths=lens.to(DEV),
+                                       block_table_pattern="shuffled", layout_seed=4)
+    got = fa.paged_quant_attention_triton(q.to(DEV), cache)
+    sync()
+    assert lib_tiled(D, qb, qb) == (D % 4 == 0)
+    assert_attention_close(got, oracle_paged_attention(q, cache), q_dtype, f"magnitudes D{D} {q_dtype}")
+
+
 def test_metric_shape_paged_b8_h32_s4096_d128_matches_oracle():
     announce("metric paged B8 H32 S4096 D128")
     q, cache = _paged_case(8, 32, 4096, 128, 16, seed=0)
