@@ -218,6 +218,21 @@ def test_tree_mfma_prefix_matches_oracle(B, H, S, D, N, page, fmt, q_dtype, leng
     assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), q_dtype, f"mfma {fmt}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("kernel", ["mfma", "rows"])
+def test_tree_one_hot_rows_at_extreme_logits(D, kernel):
+    """fp32 queries scaled by 1e20: every row's softmax is one-hot over its prefix and path tokens,
+    which holds only where exp2(score - max) sees the same rounded score as the running max (the
+    MFMA prefix kernel, the path walks, and the decode rows of kernel="rows")."""
+
+    announce(f"tree one-hot rows D{D} kernel={kernel}")
+    B, H, S, N = 2, 4, 300, 6
+    parents = _random_parents(B, N, 9)
+    got, ref, _ = _run(B, H, S, D, N, parents, [300, 150], q_dtype=torch.float32, seed=43, kernel=kernel,
+                       q_scale=1e20)
+    assert_attention_close(got.reshape(B * N, H, D), ref.reshape(B * N, H, D), torch.float32, "one-hot rows")
+
+
 @pytest.mark.parametrize("q_dtype,q_scale", [(torch.bfloat16, 3000.0), (torch.bfloat16, 1e-3), (torch.float32, 40.0),
                                              (torch.float32, 1e-4), (torch.float16, 20.0)])
 def test_tree_mfma_query_magnitudes(q_dtype, q_scale):
