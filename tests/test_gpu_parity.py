@@ -538,6 +538,31 @@ def test_query_rows_at_extreme_magnitudes(D, qb, q_dtype):
     assert_attention_close(got, oracle_paged_attention(q, cache), q_dtype, f"magnitudes D{D} {q_dtype}")
 
 
+@pytest.mark.parametrize("q_dtype", [torch.float16, torch.bfloat16])
+def test_long_rows_split_many_ways(q_dtype):
+    """Two heads over ~100k-token rows (6250 tiles): the planner splits each row dozens of ways and
+    the splits merge inside the launch; paged (shuffled pages, ragged) and contiguous."""
+
+    announce(f"long rows {q_dtype}")
+    B, H, S, D = 1, 2, 100_000, 128
+    lens = [99_993]
+    q, cache = _paged_case(B, H, S, D, 16, seed=77, layout="shuffled", lengths=lens, q_dtype=q_dtype)
+    got, stats = fa.paged_quant_attention_triton(q.to(DEV), cache, return_stats=True)
+    sync()
+    assert stats["num_splits"] >= 16
+    assert_attention_close(got, oracle_paged_attention(q, cache), q_dtype, "long paged")
+    k = randn((B, H, S, D), 78)
+    v = randn((B, H, S, D), 79)
+    kq = oq.quantize_int8_per_block(np_of(k.float()), 16)
+    vq = oq.quantize_int8_per_block(np_of(v.float()), 16)
+    lt = torch.tensor(lens, dtype=torch.int64)
+    got, stats = fa.fused_dequant_attention_triton(q.to(DEV), to_qt(kq, DEV), to_qt(vq, DEV), lengths=lt.to(DEV),
+                                                   return_stats=True)
+    sync()
+    assert stats["num_splits"] >= 16
+    assert_attention_close(got, oa.fused_dequant_attention(np_of(q.float()), kq, vq, lt.numpy()), q_dtype, "long fused")
+
+
 def test_metric_shape_paged_b8_h32_s4096_d128_matches_oracle():
     announce("metric paged B8 H32 S4096 D128")
     q, cache = _paged_case(8, 32, 4096, 128, 16, seed=0)
