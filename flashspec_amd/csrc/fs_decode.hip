@@ -173,6 +173,41 @@ struct QSlice<__half> {
   __device__ __forceinline__ float dot(uint4 raw) const { return dot16_u8_f16(qp, raw); }
 };
 
+// Query slice for FP8 E4M3 keys with fp16 queries (bf16 ones scaled into fp16 by a power of two):
+// fp16 pairs in dim order (q0,q1),(q2,q3),..., the order in which v_cvt_scalef32_pk_f16_fp8 turns a
+// key dword's codes into two fp16 pairs.  E4M3 codes convert to fp16 exactly (3 mantissa bits,
+// exponents 2^-9 .. 2^8), and the fp16 products are exact in fdot2's fp32 sums, as the fp32 path's
+// are; there is no zero point, so no sum of the query.
+struct QSliceH8 {
+  static constexpr float kOffset = 0.f;
+  uint32_t qp[8];
+  // dims [s0, 16) of q (s0 a multiple of 4); the others zero
+  __device__ __forceinline__ void load_from(const __half* q, int s0) {
+    const uint16_t* h = (const uint16_t*)q;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qp[k] = 2 * k >= s0 ? (uint32_t)h[2 * k] | ((uint32_t)h[2 * k + 1] << 16) : 0u;
+  }
+  __device__ __forceinline__ void load(const __half* q) { load_from(q, 0); }
+  __device__ __forceinline__ void load_tail(const __half* q, int s0) { load_from(q, s0); }
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qp[k] = 0u;
+  }
+  __device__ __forceinline__ float sum() const { return 0.f; }
+  __device__ __forceinline__ float dot_fp8(uint4 raw) const {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const half2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[k], 1.0f, false);
+      const half2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[k], 1.0f, true);
+      a0 = __builtin_amdgcn_fdot2(lo, __builtin_bit_cast(half2_t, qp[2 * k]), a0, false);
+      a1 = __builtin_amdgcn_fdot2(hi, __builtin_bit_cast(half2_t, qp[2 * k + 1]), a1, false);
+    }
+    return a0 + a1;
+  }
+};
+
 __device__ __forceinline__ void axpy16_u8(float* acc, float wgt, uint4 raw) {
   const uint32_t w[4] = {raw.x ^ 0x80808080u, raw.y ^ 0x80808080u, raw.z ^ 0x80808080u,
                          raw.w ^ 0x80808080u};
@@ -1022,10 +1057,15 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
   // bf16 queries over INT8 blocks take the fp16 score path (QB16): the wave's query row is scaled by
   // the power of two that puts its largest |q| into [2^13, 2^14), which bf16's 8 significant bits
   // survive exactly in fp16, and the key scales take the inverse power (qk_eff).
-  constexpr bool QB16 = std::is_same<QT, __hip_bfloat16>::value && VF == kVfInt8 &&
-                        (QM == kQmBlock || QM == kQmBlockTail || QM == kQmBlockAppend);
-  using QS = typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>,
-                                       typename std::conditional<QB16, QSlice<__half>, QSlice<QT>>::type>::type;
+  constexpr bool QB16 = std::is_same<QT, __hip_bfloat16>::value &&
+                        (QM == kQmBlock || QM == kQmBlockTail || (QM == kQmBlockAppend && VF == kVfInt8));
+  // FP8 keys with fp16 queries (any parameter mode but per channel) or bf16 ones (QB16) take
+  // fp16 dot products too (QSliceH8)
+  constexpr bool H8 = VF == kVfFp8 && !CH && (std::is_same<QT, __half>::value || QB16);
+  using QS = typename std::conditional<
+      H8, QSliceH8,
+      typename std::conditional<VF == kVfFp8 || CH, QSliceF<QT>,
+                                typename std::conditional<QB16, QSlice<__half>, QSlice<QT>>::type>::type>::type;
   QS q;
   float qsum = 0.f;
   auto prepare_q = [&]() {

@@ -130,7 +130,7 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     sm_scale = 1.0 / math.sqrt(float(head_dim))
     rows = batch * heads
     per_channel = is_per_channel(k_quant)
-    light = q_c.dtype in (torch.float16, torch.bfloat16) and k_quant.values.dtype == torch.int8
+    light = q_c.dtype in (torch.float16, torch.bfloat16) and k_quant.values.dtype in (torch.int8, FP8_DTYPE)
     tiled, waves, split_tiles, max_splits, block_n = launch_plan(seq_len, rows, head_dim, block_size, block_size,
                                                                  dev, per_channel=per_channel, light=light)
     stream = _lib.stream_ptr(dev)

@@ -114,7 +114,7 @@ def _run_paged_quant_attention_triton(q: torch.Tensor, cache: PagedKVCache, retu
     sm_scale = 1.0 / math.sqrt(float(head_dim))
     rows = batch * heads
     per_channel = is_per_channel(kq)
-    light = q_c.dtype in (torch.float16, torch.bfloat16) and kq.values.dtype == torch.int8
+    light = q_c.dtype in (torch.float16, torch.bfloat16) and kq.values.dtype in (torch.int8, FP8_DTYPE)
     tiled, waves, split_tiles, max_splits, block_n = launch_plan(
         max_seq_len, rows, head_dim, int(cache.block_size), int(kq.block_size), dev, per_channel=per_channel,
         light=light)

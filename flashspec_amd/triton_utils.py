@@ -166,14 +166,15 @@ MAX_TILED_WAVES = 16
 MIN_SPLIT_TILES = 8
 MIN_TILES_PER_WAVE = 4
 MAX_TILES_PER_WAVE = 64
-# Light tiles (fp16 or bf16 query, INT8 values with one scale / zero point per 16-token page,
-# head_dim 128: the fp16 dot2 score path with every lane busy; bf16 rows enter it scaled by a power
-# of two) run 4-wave workgroups when the grid puts one workgroup on 3/4 to all of the CUs and a
-# split holds 128..256 tiles (32..64 per wave, so no extra split).  Measured on MI355X (one box each,
-# settled clocks, 3 rotated input sets), paged / fused us with 4 against 16 waves: B8 H32 S4096 D128
-# 43.4 / 42.1 vs 45.5 / 43.1 (bf16 query: 41.6-41.7 / 41.0-41.1 vs 44.2 / 42.9-43.8), S2048
-# 25.1 / 24.3 vs 26.4 / 24.8, B4 S8192 46.4 / 45.0 vs 49.0 / 46.3, B2 S8192 29.3 / 27.3 vs
-# 30.1 / 27.8, B1 S16384 29.7 / 29.2 vs 30.4 / 29.3.  Heavier tiles (fp32 query, FP8,
+# Light tiles (fp16 or bf16 query, INT8 or FP8 E4M3 values with one scale (and zero point) per
+# 16-token page, head_dim 128: the fp16 dot2 score path with every lane busy; bf16 rows enter it
+# scaled by a power of two) run 4-wave workgroups when the grid puts one workgroup on 3/4 to all of
+# the CUs and a split holds 128..256 tiles (32..64 per wave, so no extra split).  Measured on MI355X
+# (one box each, settled clocks, 3 rotated input sets), paged / fused us with 4 against 16 waves:
+# B8 H32 S4096 D128 43.4 / 42.1 vs 45.5 / 43.1 (bf16 query: 41.6-41.7 / 41.0-41.1 vs 44.2 /
+# 42.9-43.8; FP8 values: 43.5-44.2 / 40.9-41.1 vs 44.1-44.3 / 44.2-44.4), S2048 25.1 / 24.3 vs
+# 26.4 / 24.8, B4 S8192 46.4 / 45.0 vs 49.0 / 46.3, B2 S8192 29.3 / 27.3 vs 30.1 / 27.8, B1 S16384
+# 29.7 / 29.2 vs 30.4 / 29.3.  Heavier tiles (fp32 query,
 # per-token or per-channel parameters, 64- or 256-dim layouts, head_dim 96 in the 128-dim layout:
 # 41.0 vs 37.5 us, pages of two quant blocks: 45.2 vs 44.5 us) and grids of more than one
 # workgroup per CU (ragged B16: 56.5 vs 49.7 us) keep more waves, and so do half-empty grids
@@ -368,7 +369,7 @@ def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_bl
                 per_channel: bool = False, light: bool = False):
     """(tiled, waves_per_block, split_tiles, max_splits, block_n) for one decode launch.
 
-    ``light``: fp16 or bf16 query over INT8 values (the caller's part of the LIGHT_WAVES condition;
+    ``light``: fp16 or bf16 query over INT8 or FP8 values (the caller's part of the LIGHT_WAVES condition;
     the store layout part is checked here).
 
     The plan is a pure function of the shape, the device and the three env knobs, which are
