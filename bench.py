@@ -475,6 +475,7 @@ SHAPES = [
     ("head_dim_120", 8, 32, 4096, 120, 16, 16, "float16", None),
     ("head_dim_36", 8, 32, 4096, 36, 16, 16, "float16", None),
     ("head_dim_100", 8, 32, 4096, 100, 16, 16, "float16", None),
+    ("q_bfloat16_head_dim_100", 8, 32, 4096, 100, 16, 16, "bfloat16", None),
     ("head_dim_34_generic", 8, 32, 4096, 34, 16, 16, "float16", None),
     ("batch_1_splitk", 1, 32, 16384, 128, 16, 16, "float16", None),
     ("c1_symmetric_per_token", 4, 32, 2048, 128, 16, 1, "float16", None),

@@ -1078,6 +1078,16 @@ decode_rows_kernel(const void* w0, const int64_t* w1, const void* w2, const int3
         __builtin_memcpy(qv, qraw, sizeof(qv));
 #pragma unroll
         for (int e = 0; e < 16; ++e) x[e] = to_f32(qv[e]);
+      } else if constexpr (TAIL) {
+        // the lane's 16 values lie inside the row: one batch of loads, then the dims below s0
+        // cleared (loads under a per-value condition went out one round trip at a time)
+        QT v[16];
+        if (active) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) v[e] = src[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) x[e] = active && e >= s0 ? to_f32(v[e]) : 0.f;
       } else {
 #pragma unroll
         for (int e = 0; e < 16; ++e) x[e] = active && e >= s0 ? to_f32(src[e]) : 0.f;
