@@ -98,6 +98,7 @@ def _fused_fp8(B, H, S, D, bs, seed, q_dtype):
     (2, 2, 90, 56, 1, torch.bfloat16, [90, 41]),     # head_dim 56, one scale per token
     (2, 2, 70, 44, 16, torch.float16, [70, 9]),      # head_dim 44: 12 straddling dims
     (2, 2, 80, 148, 1, torch.bfloat16, [80, 21]),    # head_dim 148: 4 straddling dims, one scale per token
+    (2, 2, 75, 100, 16, torch.bfloat16, [75, 18]),   # head_dim 100, bf16 q on the fp16 score path, block scales
     (2, 2, 70, 42, 16, torch.float16, [70, 9]),      # generic kernel: head_dim 42
 ])
 def test_fused_fp8_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
@@ -119,11 +120,15 @@ def test_fused_fp8_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     assert_attention_close(got, ref, q_dtype, "fused fp8")
 
 
-@pytest.mark.parametrize("layout,page,q_dtype", [("contiguous", 16, torch.float16), ("shuffled", 16, torch.bfloat16),
-                                                 ("interleaved", 32, torch.float32), ("shuffled", 64, torch.float16)])
-def test_paged_fp8_matches_oracle(layout, page, q_dtype):
-    announce(f"paged fp8 {layout} page{page} {q_dtype}")
-    B, H, S, D = 3, 4, 300, 128
+@pytest.mark.parametrize("layout,page,q_dtype,D", [("contiguous", 16, torch.float16, 128),
+                                                   ("shuffled", 16, torch.bfloat16, 128),
+                                                   ("interleaved", 32, torch.float32, 128),
+                                                   ("shuffled", 64, torch.float16, 128),
+                                                   ("shuffled", 16, torch.bfloat16, 100),  # straddling lane
+                                                   ("contiguous", 32, torch.float16, 36)])
+def test_paged_fp8_matches_oracle(layout, page, q_dtype, D):
+    announce(f"paged fp8 {layout} page{page} {q_dtype} D{D}")
+    B, H, S = 3, 4, 300
     q = randn((B, H, D), 21 + page, q_dtype)
     k, v = randn((B, H, S, D), 22 + page), randn((B, H, S, D), 23 + page)
     lens = torch.tensor([300, 31, 16], dtype=torch.int64)
