@@ -132,7 +132,8 @@ def _run_fused_dequant_attention_triton(q: torch.Tensor, k_quant: QuantizedTenso
     per_channel = is_per_channel(k_quant)
     light = q_c.dtype in (torch.float16, torch.bfloat16) and k_quant.values.dtype in (torch.int8, FP8_DTYPE)
     tiled, waves, split_tiles, max_splits, block_n = launch_plan(seq_len, rows, head_dim, block_size, block_size,
-                                                                 dev, per_channel=per_channel, light=light)
+                                                                 dev, per_channel=per_channel, light=light,
+                                                                 contiguous=True)
     stream = _lib.stream_ptr(dev)
     if tiled and max_splits > 1 and waves <= MERGE_MAX_WAVES:
         # split rows merge inside the decode launch (no workspace, no merge launch)

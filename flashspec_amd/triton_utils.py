@@ -205,6 +205,15 @@ HALF_EMPTY_WAVES = 8
 # against 16 waves 32.8 / 36.4.
 FORCED_WAVES_PER_CU = 8
 FORCED_MAX_WAVES = 8
+
+# Contiguous (fused) rows at head_dim 64 take at most 8 waves per workgroup in the default plan
+# (the 64-dim register layout; paged rows and the head_dims below 64 that share the layout keep
+# up to 16).  Measured on MI355X (H32, one box, fused us, default 16 waves -> 8): B8 S4096 INT8
+# 25.02 -> 23.12, bf16 / fp32 queries 24.5 / 24.35 -> 23.2 / 22.95, FP8 24.14 -> 22.81, 32-token
+# blocks 24.5 -> 23.0, per-token scales 26.5 -> 24.96, B2 S8192 (4 splits) 18.2 -> 15.58, B1 S16384
+# (8 splits) 18.2 -> 17.15, B16 S4096 43.2 -> 43.2; paged B8 S4096 26.0 -> 26.4; fused head_dim 48
+# 19.3 -> 20.7 and 40 19.03 -> 20.76.
+CONTIGUOUS_D64_WAVES = 8
 GENERIC_WAVES_PER_CU = 16
 GENERIC_MIN_SPLIT_TILES = 8
 GENERIC_MAX_SPLIT_TILES = 64
@@ -366,11 +375,12 @@ _PLAN_KNOBS = ("FLASHSPEC_NUM_WARPS", "FLASHSPEC_BLOCK_N", "FLASHSPEC_NUM_SPLITS
 
 
 def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, device,
-                per_channel: bool = False, light: bool = False):
+                per_channel: bool = False, light: bool = False, contiguous: bool = False):
     """(tiled, waves_per_block, split_tiles, max_splits, block_n) for one decode launch.
 
     ``light``: fp16 or bf16 query over INT8 or FP8 values (the caller's part of the LIGHT_WAVES condition;
-    the store layout part is checked here).
+    the store layout part is checked here).  ``contiguous``: rows of a contiguous store (the fused
+    kernel), whose default plan at head_dim 64 takes at most CONTIGUOUS_D64_WAVES waves.
 
     The plan is a pure function of the shape, the device and the three env knobs, which are
     read on every call; it is computed once per distinct combination (a few microseconds of
@@ -380,7 +390,7 @@ def launch_plan(seq_len: int, rows: int, head_dim: int, page_size: int, quant_bl
     env = os.environ
     knobs = tuple(env.get(k) for k in _PLAN_KNOBS)
     return _launch_plan_cached(int(seq_len), int(rows), int(head_dim), int(page_size), int(quant_block),
-                               dev.type, dev.index, bool(per_channel), bool(light), knobs)
+                               dev.type, dev.index, bool(per_channel), bool(light), bool(contiguous), knobs)
 
 
 def torch_device(device):
@@ -391,7 +401,7 @@ def torch_device(device):
 
 @functools.lru_cache(maxsize=512)
 def _launch_plan_cached(seq_len: int, rows: int, head_dim: int, page_size: int, quant_block: int, dev_type: str,
-                        dev_index, per_channel: bool, light: bool, knobs: tuple):
+                        dev_index, per_channel: bool, light: bool, contiguous: bool, knobs: tuple):
     """`knobs` only keys the cache: the helpers below read the same values from the environment."""
 
     import torch
@@ -413,6 +423,9 @@ def _launch_plan_cached(seq_len: int, rows: int, head_dim: int, page_size: int, 
     group = quant_block // TILE_TOKENS if tiled and per_channel else 1
     light = light and tiled and not per_channel and quant_block == TILE_TOKENS and page_size == TILE_TOKENS and \
         head_dim == 128
+    # the default plan's ceiling (a forced wave count keeps only the register limit above)
+    if contiguous and tiled and not per_channel and head_dim == 64:
+        max_waves = min(max_waves, CONTIGUOUS_D64_WAVES)
     split_tiles, max_splits, waves = plan_splits(seq_len, rows, block_n, device_cu_count(device), tiled=tiled,
                                                  waves=waves, max_waves=max_waves, tile_group=group, light=light)
     return tiled, waves, split_tiles, max_splits, block_n

@@ -108,6 +108,28 @@ def test_default_knobs_match_reference(clean_env):
     assert triton_fused._resolve_block_n() == 128 and triton_fused._resolve_num_warps() == 4
 
 
+def test_contiguous_rows_at_head_dim_64_plan_eight_waves(clean_env):
+    """The default plan for contiguous rows at head_dim 64 takes 8-wave workgroups; paged rows, the
+    tail head_dims that share the 64-dim layout and a forced wave count keep their own."""
+
+    from flashspec_amd import _lib
+
+    _lib.require()  # the tiled-path rule is a host function of the library
+    clean_env.setitem(triton_utils._CU_CACHE, 0, 256)
+    triton_utils._launch_plan_cached.cache_clear()
+    plan = triton_utils.launch_plan
+    dev = torch.device("cuda", 0)
+    assert plan(4096, 256, 64, 16, 16, dev, contiguous=True) == (True, 8, 256, 1, 128)
+    assert plan(4096, 256, 64, 16, 16, dev) == (True, 16, 256, 1, 128)
+    assert plan(4096, 256, 48, 16, 16, dev, contiguous=True)[1] == 16
+    assert plan(4096, 256, 128, 16, 16, dev, contiguous=True)[1] == 16
+    tiled, waves, split_tiles, max_splits, _ = plan(8192, 64, 64, 16, 16, dev, contiguous=True)
+    assert (waves, max_splits) == (8, 4) and split_tiles * max_splits >= 512
+    clean_env.setenv("FLASHSPEC_NUM_WARPS", "16")
+    assert plan(4096, 256, 64, 16, 16, dev, contiguous=True)[1] == 16
+    triton_utils._launch_plan_cached.cache_clear()
+
+
 def test_split_plan_covers_every_tile(clean_env):
     for tiled in (True, False):
         for seq_len in (1, 15, 16, 17, 129, 1500, 2048, 4096, 16384, 65536):
