@@ -410,6 +410,26 @@ def test_fused_attention_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     assert_attention_close(got, ref, q_dtype, "fused")
 
 
+def test_fused_head_dim_64_default_plan_takes_eight_waves(monkeypatch):
+    """Contiguous rows at head_dim 64 (B8 H32 S2048, one split) plan 8-wave workgroups; the result
+    matches the oracle and a forced 16-wave plan."""
+
+    announce("fused head_dim 64, default 8-wave plan")
+    for key in ("FLASHSPEC_NUM_WARPS", "FLASHSPEC_NUM_SPLITS", "FLASHSPEC_BLOCK_N"):
+        monkeypatch.delenv(key, raising=False)
+    q, kq, vq, _ = _fused_case(8, 32, 2048, 64, 16, seed=64)
+    args = (q.to(DEV), to_qt(kq, DEV), to_qt(vq, DEV))
+    got, stats = fa.fused_dequant_attention_triton(*args, return_stats=True)
+    sync()
+    assert stats["num_warps"] == 8.0 and stats["num_splits"] == 1.0
+    assert_attention_close(got, oa.fused_dequant_attention(np_of(q), kq, vq, None), torch.float16, "fused d64")
+    monkeypatch.setenv("FLASHSPEC_NUM_WARPS", "16")
+    other, stats16 = fa.fused_dequant_attention_triton(*args, return_stats=True)
+    sync()
+    assert stats16["num_warps"] == 16.0
+    assert (got.float() - other.float()).abs().max().item() <= 2e-3
+
+
 def test_fused_split_k_is_used_and_matches_single_split(monkeypatch):
     announce("fused split vs single split")
     q, kq, vq, _ = _fused_case(2, 4, 1500, 128, 16, seed=5)
