@@ -410,6 +410,37 @@ def test_fused_attention_matches_oracle(B, H, S, D, bs, q_dtype, lengths):
     assert_attention_close(got, ref, q_dtype, "fused")
 
 
+@pytest.mark.parametrize("D,q_dtype,fmt", [(128, torch.float16, "int8"), (128, torch.bfloat16, "int8"),
+                                           (128, torch.float32, "int8"), (128, torch.bfloat16, "fp8"),
+                                           (128, torch.float16, "fp8"), (64, torch.float16, "int8"),
+                                           (100, torch.bfloat16, "int8")])
+def test_queries_not_16_byte_aligned(D, q_dtype, fmt):
+    """Queries that start one element past a 16-byte boundary load value by value instead of as
+    16-byte words; paged and fused outputs equal the aligned queries' bit for bit and match the
+    oracle."""
+
+    announce(f"unaligned queries D{D} {q_dtype} {fmt}")
+    B, H, S = 2, 4, 300
+    q = randn((B, H, D), 71 + D, q_dtype).to(DEV)
+    base = torch.zeros(B * H * D + 1, dtype=q_dtype, device=DEV)
+    qu = base[1:].view(B, H, D)
+    qu.copy_(q)
+    assert qu.is_contiguous() and qu.data_ptr() % 16 != 0
+    k, v = randn((B, H, S, D), 72).to(DEV), randn((B, H, S, D), 73).to(DEV)
+    kv_format = "fp8_block" if fmt == "fp8" else "affine_block"
+    cache = fa.PagedKVCache.from_dense(k, v, block_size=16, kv_format=kv_format)
+    quantize = fa.quantize_fp8_per_block if fmt == "fp8" else fa.quantize_int8_per_block
+    kq, vq = quantize(k, 16), quantize(v, 16)
+    paged_a = fa.paged_quant_attention_triton(q, cache)
+    paged_u = fa.paged_quant_attention_triton(qu, cache)
+    fused_a = fa.fused_dequant_attention_triton(q, kq, vq)
+    fused_u = fa.fused_dequant_attention_triton(qu, kq, vq)
+    sync()
+    assert torch.equal(paged_a, paged_u) and torch.equal(fused_a, fused_u)
+    assert_attention_close(paged_u, oracle_paged_attention(q.cpu(), cache), q_dtype, "unaligned q, paged")
+    assert_attention_close(fused_u, oracle_fused_attention(q.cpu(), kq, vq), q_dtype, "unaligned q, fused")
+
+
 def test_fused_head_dim_64_default_plan_takes_eight_waves(monkeypatch):
     """Contiguous rows at head_dim 64 (B8 H32 S2048, one split) plan 8-wave workgroups; the result
     matches the oracle and a forced 16-wave plan."""
