@@ -368,6 +368,34 @@ def test_tree_parents_cache_reuse_and_change():
         fa.tree_verify_attention(q, cache, dk, dv, bad)
 
 
+@pytest.mark.parametrize("q_dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_tree_mfma_unaligned_queries(q_dtype):
+    """Query rows that start one element past a 16-byte boundary are fetched value by value (and
+    the drafts then walk global memory); both match the oracle, and each other to fp32 rounding."""
+
+    announce(f"tree mfma unaligned queries {q_dtype}")
+    B, H, S, D, N = 2, 8, 500, 128, 12
+    parents = torch.tensor(_random_parents(B, N, 78)).to(DEV)
+    q = randn((B, N, H, D), 96, torch.float32).to(q_dtype).to(DEV)
+    k, v = randn((B, H, S, D), 97).to(DEV), randn((B, H, S, D), 98).to(DEV)
+    dk = randn((B, N, H, D), 99, torch.float32).to(q_dtype).to(DEV)
+    dv = randn((B, N, H, D), 100, torch.float32).to(q_dtype).to(DEV)
+    cache = fa.PagedKVCache.from_dense(k, v, 16, lengths=torch.tensor([500, 233]).to(DEV))
+    raw = torch.zeros(q.numel() + 1, dtype=q_dtype, device=DEV)
+    q_off = raw[1:].view(B, N, H, D)
+    q_off.copy_(q)
+    assert q_off.data_ptr() % 16 != 0 and q_off.is_contiguous()
+    a, st = fa.tree_verify_attention(q, cache, dk, dv, parents, return_stats=True, kernel="mfma")
+    b = fa.tree_verify_attention(q_off, cache, dk, dv, parents, kernel="mfma")
+    torch.cuda.synchronize(DEV)
+    assert st["mfma_prefix"] == 1.0
+    ref = ot.tree_verify_attention(np_of(q.float()), from_cache(cache), np_of(dk.float()), np_of(dv.float()),
+                                   np_of(parents))
+    assert_attention_close(a, ref, q_dtype, "aligned queries")
+    assert_attention_close(b, ref, q_dtype, "unaligned queries")
+    assert (a.float() - b.float()).abs().max().item() <= 2e-3
+
+
 def test_tree_mfma_unaligned_drafts_walk_global_memory():
     """Draft tensors whose data does not start on a 16-byte boundary are not copied to LDS: each
     node's path is then walked in global memory, token by token, where aligned fp16 drafts enter
